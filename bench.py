@@ -1,0 +1,213 @@
+"""Benchmark: GPT-2-small-shape bf16 prefill forward on one MI355X.
+
+One step = one `Network.predict` of the notebook GPT composition (embedding, 12 decoder
+blocks, final LayerNorm, tied LM head, SoftMax) over B=8 x T=1024 token ids that are already
+resident in HBM. Prints one JSON line (see the fields below) with:
+  value       tokens/s of the whole forward (8192 tokens / step time)
+  roofline    the dense bf16 MFMA GEMMs (QKV, out-proj, FFN1, FFN2, LM head): algorithmic
+              FLOPs / summed kernel time from HIP events around each launch, vs 2.5 PFLOP/s
+  row_kernels standalone LayerNorm / RMSNorm / causal softmax / RoPE
+              in GB/s of algorithmic bytes vs 8 TB/s
+  cpu_baseline the NumPy restatement (oracle/) on a bounded sample of the same workload
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "torchless-nn_amd")
+sys.path[:0] = [ROOT, PKG]
+os.environ.setdefault("XP_RUNTIME", "MI355X")
+
+import numpy as np  # noqa: E402
+
+METRIC = "GPT fwd tokens/sec @1 GPU; norm/softmax/RoPE HBM GB/s; GEMM MFMA % of peak"
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+CFG = dict(vocab=50257, ctx=1024, layers=12, d=768, heads=12, act="gelu")
+BATCH, SEQ = 8, 1024
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gpt_forward_flops(B, T, cfg):
+    C, V, L = cfg["d"], cfg["vocab"], cfg["layers"]
+    M = B * T
+    dense = L * 2 * M * C * (3 * C + C + 4 * C + 4 * C)
+    head = 2 * M * C * V
+    attn = L * B * cfg["heads"] * 2 * (2 * T * T * (C // cfg["heads"]))
+    return dense, head, attn
+
+
+def row_kernel_bench(xp, reps=20):
+    """BASELINE config 2 standalone row kernels; GB/s of algorithmic bytes per call. Each
+    rep uses its own buffers (rotated among >256 MB) so the 256 MB MALL cannot serve them."""
+    out = {}
+    rng = np.random.default_rng(0)
+
+    def timed(name, fn, nbytes, nbuf):
+        for i in range(2):
+            fn(i % nbuf)
+        xp.synchronize()
+        e0, e1 = xp.Event(), xp.Event()
+        e0.record()
+        for i in range(reps):
+            fn(i % nbuf)
+        e1.record()
+        ms = e0.elapsed_ms(e1) / reps
+        out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 2),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "bytes": int(nbytes)}
+        log(f"{name}: {out[name]}")
+
+    for dt, es in (("fp32", 4), ("bf16", 2)):
+        R, Cn = 16384, 4096
+        host = rng.standard_normal((R, Cn)).astype(np.float32)
+        xs = [xp.array(host, dtype=dt) for _ in range(2)]
+        ys = [xp.empty((R, Cn), dt) for _ in range(2)]
+        g = xp.array(rng.standard_normal(Cn).astype(np.float32), dtype=dt)
+        b = xp.array(rng.standard_normal(Cn).astype(np.float32), dtype=dt)
+        nb = es * (2.0 * R * Cn + 2 * Cn)
+        timed(f"layernorm_{dt}_16384x4096", lambda i: xp.layernorm(xs[i], g, b, np.float32(1e-5), out=ys[i]), nb, 2)
+        timed(f"rmsnorm_{dt}_16384x4096", lambda i: xp.rmsnorm(xs[i], g, np.float32(1e-6), out=ys[i]),
+              es * (2.0 * R * Cn + Cn), 2)
+        del xs, ys
+        B, H, T = 8, 12, 1024
+        s_host = rng.standard_normal((B, H, T, T)).astype(np.float32)
+        ss = [xp.array(s_host, dtype=dt) for _ in range(2)]
+        ps = [xp.empty((B, H, T, T), dt) for _ in range(2)]
+        del s_host
+        kept = B * H * T * (T + 1) / 2
+        timed(f"softmax_causal_{dt}_8x12x1024x1024",
+              lambda i: xp.softmax(ss[i], causal=True, period=T, out=ps[i]), es * (kept + B * H * T * T), 2)
+        del ss, ps
+        D = 64
+        nrot = 12  # 12 x (25..50 MB in + out) rotated > 256 MB
+        r_host = rng.standard_normal((B, H, T, D)).astype(np.float32)
+        rx = [xp.array(r_host, dtype=dt) for _ in range(nrot)]
+        ry = [xp.empty((B, H, T, D), dt) for _ in range(nrot)]
+        tab = xp.rope_table(T, D, 10000.0)
+        timed(f"rope_{dt}_8x12x1024x64", lambda i: xp.rope(rx[i], tab, out=ry[i]), es * 2.0 * B * H * T * D, nrot)
+        del rx, ry
+    return out
+
+
+def cpu_baseline(sample_seqs=1, sample_T=SEQ):
+    """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
+    of the workload: `sample_seqs` sequences of T tokens of the same model."""
+    from oracle import numpy_ref as ref
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max(int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas")
+    except Exception:
+        pass
+    params = ref.gpt_params(CFG, 0)
+    ids = np.random.default_rng(1).integers(0, CFG["vocab"], (sample_seqs, sample_T))
+    t0 = time.perf_counter()
+    ref.gpt_forward(ids, params, CFG)
+    dt = time.perf_counter() - t0
+    return {"value": round(sample_seqs * sample_T / dt, 1), "unit": "tokens/s",
+            "cores": threads or 1, "kind": "port",
+            "sample": (f"{sample_seqs} x {sample_T} tokens of the same GPT-2-small-shape forward, "
+                       f"fp32 NumPy (oracle/numpy_ref.py), one run of {dt:.1f} s; sgemm on "
+                       f"{threads} BLAS threads, ufuncs single-threaded; "
+                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-row-kernels", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import tl_hip as xp
+    import gpt
+    xp.ctx()
+    log("building GPT-2-small-shape model (bf16) and seeding weights")
+    net, _ = gpt.build_gpt(CFG, dtype="bf16")
+    gpt.seed_parameters(net, 0)
+    ids = xp.array(np.random.default_rng(1).integers(0, CFG["vocab"], (BATCH, SEQ)).astype(np.int32))
+    xp.synchronize()
+
+    for i in range(args.warmup):
+        net.predict(ids)
+    xp.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+
+    e0, e1 = xp.Event(), xp.Event()
+    xp.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        out = net.predict(ids)
+    e1.record()
+    xp.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / args.steps
+    tokens_s = BATCH * SEQ / (ms * 1e-3)
+    log(f"timed {args.steps} steps: {ms:.3f} ms/step (event), wall {wall / args.steps * 1e3:.3f} ms/step")
+    del out
+
+    # per-launch kernel profile: the same K steps again with HIP events around every launch
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    for _ in range(args.steps):
+        net.predict(ids)
+    xp.synchronize()
+    fam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
+    breakdown = {}
+    for f, r in fam.items():
+        if r["launches"]:
+            breakdown[f] = {"ms_per_step": round(r["ms"] / args.steps, 4),
+                            "launches_per_step": r["launches"] // args.steps,
+                            "tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1) if r["flops"] else None,
+                            "gbs": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)}
+    log(f"breakdown: {json.dumps(breakdown)}")
+    g = fam["gemm_mfma"]
+    achieved = g["flops"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
+    roofline = {"bound": "mfma", "kernel": "gemm_mfma_kernel (QKV, out-proj, FFN1, FFN2, LM head)",
+                "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 2),
+                "flops_per_launch": round(g["flops"] / max(1, g["launches"])),
+                "traffic": None}
+
+    rows = {} if args.no_row_kernels else row_kernel_bench(xp)
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
+    if cpu:
+        log(f"cpu baseline: {cpu}")
+
+    dense, head, attn = gpt_forward_flops(BATCH, SEQ, CFG)
+    line = {
+        "metric": METRIC, "value": round(tokens_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: weights N(0,0.02) seeded, token ids uniform in [0,50257) seeded",
+        "config": {"workload": "GPT-2-small-shape decoder prefill (BASELINE config 3)",
+                   "global_batch": BATCH, "seq_len": SEQ, "vocab": CFG["vocab"],
+                   "layers": CFG["layers"], "d_model": CFG["d"], "heads": CFG["heads"],
+                   "ffn": 4 * CFG["d"], "parallelism": "none (1 GPU)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "gemm_flops_per_step": {"dense": dense, "lm_head": head, "attention_full": attn},
+        "kernel_breakdown": breakdown,
+        "row_kernels": rows,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,204 @@
+/*
+ * libtl — C ABI of the MI355X (gfx950) runtime behind torchless-nn's Layer interface.
+ *
+ * The reference library has no native boundary: every `xp.*` expression in a Layer's
+ * forward is a CuPy (CUDA) or NumPy (CPU) call, chosen at import by XP_RUNTIME
+ * (reference backend.py:3-22). This library is what the new XP_RUNTIME=MI355X value binds
+ * through ctypes. Each entry point below names the reference expression(s) it replaces.
+ *
+ * Conventions
+ *  - Every function returns an int status (TL_OK == 0) and never throws. On failure the
+ *    message is available from tl_last_error() on the calling thread.
+ *  - Device buffers are plain pointers obtained from tl_malloc. The caller owns them; the
+ *    library keeps no pointer after a call returns.
+ *  - All compute calls are asynchronous enqueues on the context's single in-order HIP
+ *    stream. tl_memcpy_d2h, tl_memcpy2d_d2h and tl_sync block. Data errors detected
+ *    inside kernels (e.g. an out-of-range token id) are latched in a device status word
+ *    and reported, as TL_ERR_BAD_INPUT, by the next blocking call.
+ *  - Sizes, leading dimensions and strides are int64 and counted in elements.
+ *  - A context must not be used by two host threads at once.
+ */
+#ifndef LIBTL_H
+#define LIBTL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct tl_ctx tl_ctx;
+
+/* Element types. Floating-point data is fp32 or bf16 (bf16 stored as raw uint16). */
+enum tl_dtype { TL_F32 = 0, TL_BF16 = 1, TL_I32 = 2, TL_I64 = 3, TL_U8 = 4 };
+
+enum tl_status {
+  TL_OK = 0,
+  TL_ERR_INVALID = 1,     /* bad argument: null pointer, bad shape, bad enum */
+  TL_ERR_HIP = 2,         /* a HIP runtime call failed */
+  TL_ERR_OOM = 3,         /* device allocation failed after emptying the cache */
+  TL_ERR_NO_DEVICE = 4,   /* no HIP device, or the index is out of range */
+  TL_ERR_BAD_INPUT = 5,   /* a kernel saw invalid data (latched, reported at sync) */
+  TL_ERR_UNSUPPORTED = 6  /* valid request this build does not implement */
+};
+
+/* Activations (reference activations.py). */
+enum tl_act { TL_ACT_NONE = 0, TL_ACT_GELU = 1, TL_ACT_SILU = 2 };
+
+/* Layout of the GEMM B operand. */
+enum tl_b_layout {
+  TL_B_NK = 0, /* B given as Bt[n*ldb + k]  (C = A * Bt^T; weights pre-packed, tied head) */
+  TL_B_KN = 1  /* B given as B[k*ldb + n]   (C = A * B, the reference's `x @ W`) */
+};
+
+/* Epilogue variants of tl_gemm. */
+enum tl_epilogue {
+  TL_EPI_STORE = 0,     /* C[m,n] = f(acc) */
+  TL_EPI_QKV_SPLIT = 1  /* scatter [M, (Hq+2*Hkv)*Dh] into q [B,Hq,T,Dh], k [B,Hkv,T,Dh], vt [B,Hkv,Dh,T] */
+};
+
+/* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */
+enum tl_kfamily {
+  TL_KF_GEMM_MFMA = 0,  /* bf16 MFMA GEMM, dense projections and LM head */
+  TL_KF_GEMM_BATCHED = 1, /* bf16 MFMA GEMM, batched attention products (QK^T, PV) */
+  TL_KF_GEMM_SIMT = 2,  /* generic VALU GEMM (fp32 and unaligned shapes) */
+  TL_KF_LAYERNORM = 3,
+  TL_KF_RMSNORM = 4,
+  TL_KF_SOFTMAX = 5,
+  TL_KF_ROPE = 6,
+  TL_KF_ACT = 7,
+  TL_KF_EMBED = 8,
+  TL_KF_ARGMAX = 9,
+  TL_KF_ATTENTION = 10, /* fused causal attention */
+  TL_KF_MISC = 11,      /* fill, cast, transpose, add */
+  TL_KF_COUNT = 12
+};
+
+/* Argument block of tl_gemm: C = epilogue(A * op(B)), batched over z in [0, batch).
+ * z splits as zo = z / batch_inner, zi = z % batch_inner and every operand pointer
+ * advances by zo*s?_o + zi*s?_i elements. Epilogue order, per element:
+ *   v = acc; if (divisor != 1) v = v / divisor; if (bias) v += bias[n];
+ *   v = act(v); if (residual) v += residual[m*ldr + n]; store v in dtype_out. */
+typedef struct tl_gemm_desc {
+  int64_t M, N, K;
+  const void* A; int64_t lda;
+  const void* B; int64_t ldb; int32_t b_layout;
+  void* C; int64_t ldc;
+  int32_t dtype_in, dtype_out;
+  int64_t batch, batch_inner;
+  int64_t sa_o, sa_i, sb_o, sb_i, sc_o, sc_i;
+  const void* bias;                     /* [N], dtype_in, or NULL */
+  const void* residual; int64_t ldr;    /* dtype_out, or NULL */
+  int64_t sr_o, sr_i;
+  int32_t act;                          /* enum tl_act */
+  float divisor;
+  int32_t epilogue;                     /* enum tl_epilogue */
+  void* q; void* k; void* vt;           /* TL_EPI_QKV_SPLIT outputs */
+  int64_t seq_len, n_heads_q, n_heads_kv, head_dim;
+  int32_t family;                       /* enum tl_kfamily used by the profiler */
+} tl_gemm_desc;
+
+/* ---- runtime ------------------------------------------------------------------------ */
+int tl_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* tl_last_error(void);
+int tl_device_count(int* count);
+/* Replaces the CUDA runtime selection at reference backend.py:7-18. */
+int tl_init(int device, tl_ctx** out);
+int tl_destroy(tl_ctx* ctx);
+/* Caching allocator (stream-ordered reuse on the context stream). Replaces CuPy's pool
+ * behind every fresh `xp` array a forward allocates (e.g. reference layers.py:208). */
+int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr);
+int tl_free(tl_ctx* ctx, void* ptr);
+int tl_empty_cache(tl_ctx* ctx);
+int tl_mem_stats(tl_ctx* ctx, size_t* bytes_in_use, size_t* bytes_cached);
+/* Host<->device copies. Replace `xp.array(host)` (reference network.py:297, 332) and
+ * `.get()` (reference demo.ipynb:1535). h2d returns once the host buffer may be reused. */
+int tl_memcpy_h2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
+int tl_memcpy_d2h(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
+int tl_memcpy_d2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
+int tl_memcpy2d_h2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size_t spitch,
+                    size_t width_bytes, size_t rows);
+int tl_memcpy2d_d2h(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size_t spitch,
+                    size_t width_bytes, size_t rows);
+/* Waits for the stream, then reports any latched kernel data error. */
+int tl_sync(tl_ctx* ctx);
+/* Events on the context stream, for timing. */
+int tl_event_create(tl_ctx* ctx, void** ev);
+int tl_event_record(tl_ctx* ctx, void* ev);
+int tl_event_elapsed_ms(void* start, void* stop, float* ms);
+int tl_event_destroy(void* ev);
+/* Per-launch event profiler: while enabled for a family mask, every launch of a kernel of
+ * those families is bracketed by events; tl_kprof_query sums them after a sync. */
+int tl_kprof_enable(tl_ctx* ctx, uint32_t family_mask);
+int tl_kprof_reset(tl_ctx* ctx);
+int tl_kprof_query(tl_ctx* ctx, int family, int64_t* launches, double* total_ms,
+                   double* flops, double* bytes);
+
+/* ---- elementwise helpers -------------------------------------------------------------- */
+/* y[i] = value (a kernel, not hipMemset, so it is safe under graph capture).
+ * Replaces init_zeros_tensor (reference backend.py:33-34). */
+int tl_fill(tl_ctx* ctx, void* y, int64_t n, int32_t dtype, double value);
+int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dtype_x, int32_t dtype_y);
+/* y[c*ldy + r] = x[r*ldx + c]: weight pre-packing into the K-contiguous GEMM layout. */
+int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t ldy, int32_t dtype);
+/* y = a + b (elementwise, same shape). Replaces the residual adds at reference
+ * layers.py:465-466 when they are not fused into a GEMM epilogue. */
+int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype);
+
+/* ---- the hot path --------------------------------------------------------------------- */
+/* out[i, :] = table[ids[i], :] + pos[pos0 + i % seq_len, :]  (pos may be NULL).
+ * Replaces GPTEmbedFront.forward (reference transformer_adapters.py:148-153). Ids outside
+ * [0, vocab) zero the row and latch TL_ERR_BAD_INPUT. */
+int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* table,
+                 const void* pos, void* out, int64_t n_tokens, int64_t seq_len, int64_t pos0,
+                 int64_t vocab, int64_t dim, int64_t ld_out, int32_t dtype);
+/* y = (x - mean) / sqrt(var + eps) * gamma + beta per row (population variance).
+ * Replaces LayerNorm.forward (reference layers.py:415-428). */
+int tl_layernorm_fwd(tl_ctx* ctx, const void* x, const void* gamma, const void* beta, void* y,
+                     int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float eps,
+                     int32_t dtype);
+/* y = x / sqrt(mean(x^2) + eps) * (gamma_offset + gamma) per row. No reference counterpart
+ * (the reference has only a TODO for it, layers.py:394). */
+int tl_rmsnorm_fwd(tl_ctx* ctx, const void* x, const void* gamma, void* y, int64_t rows,
+                   int64_t cols, int64_t ldx, int64_t ldy, float eps, float gamma_offset,
+                   int32_t dtype);
+/* y = exp((x - max)/temperature) / sum(...) per row. With causal != 0, row r only attends
+ * to columns j <= (r % period) + offset; the others get exactly 0. Replaces the attention
+ * softmax with its -1e9 additive mask (reference layers.py:295-300) and SoftMax.forward
+ * (reference activations.py:57-64). */
+int tl_softmax_fwd(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t ldy, float temperature, int32_t causal, int64_t period,
+                   int64_t offset, int32_t dtype);
+/* table (fp32, [2][T][D/2]: cos block then sin block) of angles (pos0 + t) * base^(-2i/D),
+ * evaluated in fp64. No reference counterpart (positions are absolute there). */
+int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
+                  int64_t pos0);
+/* Rotate-half RoPE over x [n_seq, T, D] (row pitch D): for i < D/2,
+ * y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i+D/2] cos + x[i] sin. */
+int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
+                int64_t seq_len, int64_t head_dim, int32_t dtype);
+/* Replaces GeLU.forward / SiLU.forward (reference activations.py:24-28, 41-45). */
+int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype);
+/* out[r] = first index of the maximum of row r (NaN counts as the maximum), int64.
+ * Replaces xp.argmax(y_hat, axis=-1) (reference network.py:315, 338). */
+int tl_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+              int32_t dtype, void* out_ids);
+/* Every matmul of the forward: reference layers.py:208, 286, 293, 303, 306, 372, 373,
+ * transformer_adapters.py:49, 93, 176. */
+int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* desc);
+/* Fused causal attention for q [BH, T, D], k [BH/g, Tk, D], vt [BH/g, D, Tk] (g query heads
+ * share one kv head): out[b, t, h*D + d] with row pitch ld_out, scores divided by
+ * `divisor`; query t sits at key position t + offset. Replaces reference
+ * layers.py:293-304 (scores, mask, softmax, P.V, head merge) in one kernel. */
+int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, void* out,
+                     int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
+                     int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
+                     float divisor, int32_t causal, int32_t dtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LIBTL_H */

@@ -1,0 +1,260 @@
+"""CPU oracle: a NumPy restatement of torchless-nn's transformer forward.
+
+TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg may import this module, and only as the checker (or, for the baseline, as the timed
+CPU path). The product path (torchless-nn_amd/) never imports it.
+
+Each function follows the reference op for op (file:line under luke-skynet/torchless-nn),
+in float32 as the reference's CPU runtime does (backend.py:24). Functions with no reference
+counterpart (RMSNorm, RoPE, GeGLU) restate the published definitions named in their
+docstrings.
+
+Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/):
+  gelu, silu       closed forms in float64 (silu against x*sigmoid(x), an independent
+                   formula), odd-part identity f(x) - f(-x) = x, f(0) = 0
+  softmax          float64 closed form, rows sum to 1, shift invariance, masked entries
+                   exactly 0, single-column rows equal 1
+  layernorm        brute-force float64 loops; per-row mean -> beta and std -> gamma
+  rmsnorm          brute-force float64 loops; invariance to positive row scaling
+  rope             complex-multiplication form, identity at position 0, pair norms
+                   preserved, <R_m q, R_n k> depends only on m - n
+  mha              brute-force per-head loops in float64 (golden fixture); permutation
+                   weights pin the head split/merge order
+  embed_front      brute-force gather + add
+  argmax           NumPy semantics (first maximum, first NaN) on hand-made ties
+  gpt_forward      brute-force float64 composition of the above at a tiny shape (golden
+                   fixture)
+  bf16 rounding    hand-computed bit patterns (ties to even, NaN, inf)
+The reference itself was not imported or run: its files are pure Python over CuPy/NumPy
+with no golden vectors, and every function above is pinned by the checks listed.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+# ---- bf16 (round to nearest even) -----------------------------------------------------
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even, NaN kept quiet."""
+    u = np.ascontiguousarray(x, dtype=F32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + (0x7FFF + ((u >> 16) & 1))) >> 16).astype(np.uint16)
+    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+    return r
+
+
+def from_bf16_bits(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(F32)
+
+
+def round_bf16(x) -> np.ndarray:
+    """Value of float32 `x` after a round trip through bf16."""
+    x = np.asarray(x, dtype=F32)
+    return from_bf16_bits(bf16_bits(x)).reshape(x.shape)
+
+
+def max_rel(got, ref) -> float:
+    """Parity metric: max |got - ref| / max |ref| over the whole tensor."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    denom = np.max(np.abs(ref)) if ref.size else 0.0
+    if denom == 0:
+        return float(np.max(np.abs(got - ref))) if ref.size else 0.0
+    return float(np.max(np.abs(got - ref)) / denom)
+
+
+# ---- activations (reference activations.py) -------------------------------------------
+def gelu(x):
+    """activations.py:24-28: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x**3)))."""
+    x = np.asarray(x, dtype=F32)
+    t = np.tanh((2 / np.pi) ** 0.5 * (x + 0.044715 * x ** 3))
+    return 0.5 * x * (1 + t)
+
+
+def silu(x):
+    """activations.py:41-45: x * (1 + tanh(x/2)) / 2."""
+    x = np.asarray(x, dtype=F32)
+    return x * ((1 + np.tanh(x / 2)) / 2)
+
+
+def softmax(x, temperature=F32(1.0)):
+    """activations.py:57-64: exp((x - max)/T) / sum over the last axis."""
+    x = np.asarray(x, dtype=F32)
+    normalization = np.max(x, axis=-1, keepdims=True)
+    exponent = np.exp((x - normalization) / temperature)
+    return exponent / np.sum(exponent, axis=-1, keepdims=True)
+
+
+def act(x, name):
+    return {"gelu": gelu, "silu": silu}[name](x)
+
+
+# ---- normalisation ---------------------------------------------------------------------
+def layernorm(x, gamma, beta, eps=F32(1e-5)):
+    """layers.py:415-428: population mean/var, std = (var + eps)**0.5, gamma*norm + beta."""
+    x = np.asarray(x, dtype=F32)
+    mean = np.mean(x, axis=-1, keepdims=True)
+    var = np.var(x, axis=-1, keepdims=True)
+    centered = x - mean
+    std = (var + eps) ** F32(0.5)
+    normed = centered / std
+    return gamma * normed + beta
+
+
+def rmsnorm(x, gamma, eps=F32(1e-6), gamma_offset=0.0):
+    """RMSNorm (Zhang & Sennrich 2019): x / sqrt(mean(x^2) + eps) * (offset + gamma).
+    No reference counterpart (layers.py:394 is a TODO); offset 1 is Gemma's convention."""
+    x = np.asarray(x, dtype=F32)
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return (x / np.sqrt(ms + F32(eps))) * (F32(gamma_offset) + gamma)
+
+
+# ---- RoPE (Su et al. 2021, rotate-half pairing as in GPT-NeoX/Gemma) -------------------
+def rope_table(seq_len, head_dim, base=10000.0, pos0=0):
+    """cos/sin of (pos0 + t) * base^(-2i/D), evaluated in float64, stored as float32."""
+    half = head_dim // 2
+    i = np.arange(half, dtype=np.float64)
+    inv_freq = base ** (-(2 * i) / head_dim)
+    ang = (pos0 + np.arange(seq_len, dtype=np.float64))[:, None] * inv_freq[None, :]
+    return np.cos(ang).astype(F32), np.sin(ang).astype(F32)
+
+
+def rope(x, cos, sin):
+    """x [..., T, D]: y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin, halves of the last axis."""
+    x = np.asarray(x, dtype=F32)
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * cos - x2 * sin, x2 * cos + x1 * sin], axis=-1)
+
+
+# ---- layers (reference layers.py) -------------------------------------------------------
+def dense(x, w, b):
+    """layers.py:206-209: x @ W + b."""
+    return np.asarray(x, dtype=F32) @ w + b
+
+
+def causal_mask(context_length):
+    """layers.py:254-256: tril -> 0 on/below the diagonal, -1e9 above (float32)."""
+    mask = np.tril(np.ones((context_length, context_length)))
+    return np.where(mask == 0, -1e9, 0.0).astype(F32, copy=False)
+
+
+def mha(x, wqkv, bqkv, wo, bo, num_heads, decoder=False, context_length=None, rnd=None):
+    """layers.py:281-307 (dropout is the identity at inference, layers.py:231-232).
+    `rnd` (optional) rounds the tensors the device materialises (bf16 pipeline)."""
+    r = rnd or (lambda a: a)
+    x = np.asarray(x, dtype=F32)
+    B, T, C = x.shape
+    D = C // num_heads
+    qkv = r(x @ wqkv + bqkv)
+    query, key_t, value = np.split(qkv, 3, axis=2)
+    query = query.reshape((B, T, num_heads, D)).transpose(0, 2, 1, 3)
+    key_t = key_t.reshape((B, T, num_heads, D)).transpose(0, 2, 3, 1)
+    value = value.reshape((B, T, num_heads, D)).transpose(0, 2, 1, 3)
+    attends = r((query @ key_t) / F32(D ** 0.5))
+    if decoder:
+        attends = attends + causal_mask(context_length or T)[:T, :T]
+    normalization = np.max(attends, axis=-1, keepdims=True)
+    exponent = np.exp(attends - normalization)
+    probs = r(exponent / np.sum(exponent, axis=-1, keepdims=True))
+    heads = r(probs @ value)
+    heads = heads.transpose(0, 2, 1, 3).reshape(B, T, C)
+    return heads @ wo + bo
+
+
+def ffn(x, w1, b1, w2, b2, activation="gelu", rnd=None):
+    """layers.py:369-375: act(x W1 + b1) W2 + b2."""
+    r = rnd or (lambda a: a)
+    h = r(act(np.asarray(x, dtype=F32) @ w1 + b1, activation))
+    return h @ w2 + b2
+
+
+def block(x, p, num_heads, activation="gelu", decoder=True, context_length=None, rnd=None):
+    """layers.py:463-467: y = x + MHA(LN1 x); z = y + FFN(LN2 y).
+    p = [g1, b1, Wqkv, bqkv, Wo, bo, g2, b2, W1, bb1, W2, bb2] (layers.py:458 order)."""
+    r = rnd or (lambda a: a)
+    g1, be1, wqkv, bqkv, wo, bo, g2, be2, w1, bb1, w2, bb2 = p
+    y = r(x + mha(r(layernorm(x, g1, be1)), wqkv, bqkv, wo, bo, num_heads, decoder,
+                  context_length, rnd))
+    z = r(y + ffn(r(layernorm(y, g2, be2)), w1, bb1, w2, bb2, activation, rnd))
+    return z
+
+
+# ---- GPT adapters (reference transformer_adapters.py) ---------------------------------
+def embed_front(ids, table, pos):
+    """transformer_adapters.py:148-153: table[ids] + pos[:T]."""
+    ids = np.asarray(ids)
+    return table[ids] + pos[: ids.shape[1], :]
+
+
+def sinusoidal_positions(context_length, embed_size):
+    """transformer_adapters.py:128-135."""
+    pos = np.arange(context_length)[:, None]
+    i = np.arange(embed_size)[None, :]
+    tab = pos / 10000 ** (2 * (i // 2) / embed_size)
+    tab[:, 0::2] = np.sin(tab[:, 0::2])
+    tab[:, 1::2] = np.cos(tab[:, 1::2])
+    return tab.astype(F32, copy=False)
+
+
+def embed_back(x, table):
+    """transformer_adapters.py:174-177: logits = x @ table^T."""
+    return np.asarray(x, dtype=F32) @ table.transpose()
+
+
+def argmax(x):
+    """network.py:315, 338: xp.argmax(y_hat, axis=-1) (NumPy: first max, first NaN)."""
+    return np.argmax(x, axis=-1)
+
+
+def vit_head(x, w, b):
+    """transformer_adapters.py:89-95: x[:, 0, :] @ W + b."""
+    return np.asarray(x, dtype=F32)[:, 0, :] @ w + b
+
+
+# ---- GPT composition (reference demo.ipynb:1473-1501) ---------------------------------
+def gpt_param_shapes(cfg):
+    """Parameter shapes in `layer.parameters` order for the notebook GPT composition:
+    GPTEmbedFront [pos, table] (transformer_adapters.py:138, 143), each TransformerBlock
+    (layers.py:458 with 275-279, 362-366), the final LayerNorm [gamma, beta]."""
+    V, T, C, L = cfg["vocab"], cfg["ctx"], cfg["d"], cfg["layers"]
+    shapes = [("pos", (T, C)), ("table", (V, C))]
+    for l in range(L):
+        shapes += [(f"b{l}.g1", (C,)), (f"b{l}.be1", (C,)), (f"b{l}.wqkv", (C, 3 * C)),
+                   (f"b{l}.bqkv", (3 * C,)), (f"b{l}.wo", (C, C)), (f"b{l}.bo", (C,)),
+                   (f"b{l}.g2", (C,)), (f"b{l}.be2", (C,)), (f"b{l}.w1", (C, 4 * C)),
+                   (f"b{l}.bb1", (4 * C,)), (f"b{l}.w2", (4 * C, C)), (f"b{l}.bb2", (C,))]
+    shapes += [("lnf.g", (C,)), ("lnf.be", (C,))]
+    return shapes
+
+
+def gpt_params(cfg, seed, scale=0.02, bf16=False):
+    """Seeded fill: N(0,1)*scale in parameter order from default_rng(seed); LayerNorm
+    gammas get +1 so the affine part is exercised around the identity."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in gpt_param_shapes(cfg):
+        a = rng.standard_normal(shape, dtype=F32) * F32(scale)
+        if name.endswith(".g1") or name.endswith(".g2") or name == "lnf.g":
+            a = a + F32(1.0)
+        out[name] = round_bf16(a) if bf16 else a
+    return out
+
+
+def gpt_forward(ids, params, cfg, bf16=False, return_logits=False):
+    """demo.ipynb:1473-1501: embed -> dropout(identity) -> L blocks -> LN -> tied head ->
+    SoftMax. With bf16=True every tensor the device materialises is rounded to bf16."""
+    rnd = round_bf16 if bf16 else None
+    r = rnd or (lambda a: a)
+    H, L = cfg["heads"], cfg["layers"]
+    x = r(embed_front(ids, params["table"], params["pos"]))
+    for l in range(L):
+        p = [params[f"b{l}.{k}"] for k in ("g1", "be1", "wqkv", "bqkv", "wo", "bo", "g2", "be2",
+                                          "w1", "bb1", "w2", "bb2")]
+        x = block(x, p, H, cfg.get("act", "gelu"), True, cfg["ctx"], rnd)
+    x = r(layernorm(x, params["lnf.g"], params["lnf.be"]))
+    logits = r(embed_back(x, params["table"]))
+    probs = r(softmax(logits))
+    return (probs, logits) if return_logits else probs

@@ -1,0 +1,128 @@
+"""CPU checks of the C-ABI boundary and the host logic (no kernel is launched here)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "libtl.h")
+PKG = os.path.join(ROOT, "torchless-nn_amd")
+LIB = os.path.join(PKG, "libtl.so")
+
+needs_lib = pytest.mark.skipif(not os.path.exists(LIB), reason="libtl.so not built")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    import tl_hip
+    assert header_functions() == sorted(tl_hip.SIGNATURES)
+
+
+@needs_lib
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    missing = [f for f in header_functions() if not hasattr(lib, f)]
+    assert not missing, missing
+
+
+@needs_lib
+def test_exported_symbols_are_exactly_the_header():
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True).stdout
+    exported = sorted(set(re.findall(r" T (tl_[a-z0-9_]+)$", out, flags=re.M)))
+    assert exported == header_functions()
+
+
+def test_gemm_desc_layout_matches_header():
+    """The ctypes struct must mirror tl_gemm_desc field for field."""
+    import tl_hip
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct tl_gemm_desc \{(.*?)\} tl_gemm_desc;", text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        decl = re.sub(r"^(const\s+)?(void\s*\*|int64_t|int32_t|float)\s*", "", decl)
+        names += [re.sub(r"[\s*]", "", n) for n in decl.split(",")]
+    assert names == [f[0] for f in tl_hip._GemmDesc._fields_]
+
+
+@needs_lib
+def test_no_device_is_a_clean_error():
+    """This container has no GPU: tl_init must fail with TL_ERR_NO_DEVICE and a message,
+    and the Python runtime must raise rather than fall back to the CPU."""
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import tl_hip\n"
+        "try:\n"
+        "    tl_hip.ctx()\n"
+        "except tl_hip.NoDeviceError as e:\n"
+        "    print('NODEV', e)\n"
+        "else:\n"
+        "    print('HAVE_DEVICE')\n" % PKG)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    if "HAVE_DEVICE" in r.stdout:
+        pytest.skip("a GPU is present")
+    assert "NODEV" in r.stdout, r.stdout + r.stderr
+    assert "device" in r.stdout.lower()
+
+
+@needs_lib
+def test_null_arguments_are_rejected_without_a_context():
+    lib = ctypes.CDLL(LIB)
+    lib.tl_init.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    lib.tl_last_error.restype = ctypes.c_char_p
+    assert lib.tl_init(0, None) == 1  # TL_ERR_INVALID
+    assert b"null" in lib.tl_last_error()
+    lib.tl_sync.argtypes = [ctypes.c_void_p]
+    assert lib.tl_sync(None) == 1
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = (
+        "import os, sys; os.environ['TL_LIBRARY'] = %r; sys.path.insert(0, %r)\n"
+        "import tl_hip\n"
+        "try:\n"
+        "    tl_hip.load_library()\n"
+        "except ImportError as e:\n"
+        "    print('IMPORTERROR', e)\n" % (str(tmp_path / "nope.so"), PKG))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert "IMPORTERROR" in r.stdout, r.stdout + r.stderr
+
+
+def test_other_runtimes_are_refused():
+    for value in ("CUDA", "CPU"):
+        code = "import os, sys; os.environ['XP_RUNTIME'] = %r; sys.path.insert(0, %r)\nimport backend\n" % (value, PKG)
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+        assert r.returncode != 0 and "MI355X" in r.stderr
+
+
+def test_host_bf16_conversion_matches_oracle():
+    import tl_hip
+    from oracle import numpy_ref as ref
+    x = np.random.default_rng(0).standard_normal(10000).astype(np.float32) * 100
+    x[:4] = [np.inf, -np.inf, 0.0, -0.0]
+    assert np.array_equal(tl_hip.f32_to_bf16_bits(x), ref.bf16_bits(x))
+    bits = tl_hip.f32_to_bf16_bits(x)
+    assert np.array_equal(tl_hip.bf16_bits_to_f32(bits), ref.from_bf16_bits(bits))
+
+
+def test_dtype_mapping():
+    import tl_hip
+    assert tl_hip.as_dtype(np.float64) is tl_hip.float32
+    assert tl_hip.as_dtype(np.uint8) is tl_hip.uint8
+    assert tl_hip.as_dtype(np.int64) is tl_hip.int64
+    assert tl_hip.as_dtype(np.int16) is tl_hip.int32
+    assert tl_hip.as_dtype("bf16") is tl_hip.bfloat16
+    with pytest.raises(TypeError):
+        tl_hip.as_dtype(np.complex64)

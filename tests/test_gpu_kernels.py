@@ -1,0 +1,317 @@
+"""Kernel parity on the MI355X: every libtl kernel against the NumPy oracle on the same
+seeded inputs. Bars: fp32 max_rel <= 1e-5, bf16 max_rel <= 2e-2 (max |diff| / max |ref|),
+integer outputs bit-exact."""
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+F32 = np.float32
+TOL = {"fp32": 1e-5, "bf16": 2e-2}
+
+
+@pytest.fixture(scope="module")
+def xp():
+    import tl_hip
+    tl_hip.ctx()
+    return tl_hip
+
+
+def rnd(dt, a):
+    return ref.round_bf16(a) if dt == "bf16" else np.asarray(a, F32)
+
+
+def up(xp, a, dt):
+    return xp.array(np.asarray(a, F32), dtype=dt)
+
+
+# ---- helpers ---------------------------------------------------------------------------
+def test_fill_cast_add_transpose(xp):
+    t = xp.empty((3, 5), "fp32").fill(2.5)
+    assert np.all(t.get() == 2.5)
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((37, 53)).astype(F32)
+    d = up(xp, a, "fp32")
+    assert np.array_equal(d.astype("bf16").get(), ref.round_bf16(a))
+    assert np.array_equal((d + d).get(), a + a)
+    assert np.array_equal(xp.transpose2d(d).get(), a.T)
+    b = up(xp, a, "bf16")
+    assert np.array_equal(xp.transpose2d(b).get(), ref.round_bf16(a).T)
+    for dt in ("int32", "int64", "uint8"):
+        z = xp.zeros((7,), dt)
+        assert z.get().tolist() == [0] * 7
+
+
+# ---- LayerNorm / RMSNorm ------------------------------------------------------------------
+NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (33, 4096), (2, 5000), (4, 8192), (3, 12000)]
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("shape", NORM_SHAPES)
+def test_layernorm(xp, dt, shape):
+    rng = np.random.default_rng(hash(shape) % 1000)
+    x = rnd(dt, rng.standard_normal(shape).astype(F32) * 2 + 0.5)
+    g = rnd(dt, rng.standard_normal(shape[1]).astype(F32))
+    b = rnd(dt, rng.standard_normal(shape[1]).astype(F32))
+    y = xp.layernorm(up(xp, x, dt), up(xp, g, dt), up(xp, b, dt), F32(1e-5)).get()
+    want = ref.layernorm(x, g, b)
+    assert ref.max_rel(y, rnd(dt, want)) <= TOL[dt], (dt, shape)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("shape", NORM_SHAPES)
+def test_rmsnorm(xp, dt, shape):
+    rng = np.random.default_rng(hash(shape) % 1000 + 1)
+    x = rnd(dt, rng.standard_normal(shape).astype(F32))
+    g = rnd(dt, rng.standard_normal(shape[1]).astype(F32) * 0.1)
+    for off in (0.0, 1.0):
+        y = xp.rmsnorm(up(xp, x, dt), up(xp, g, dt), F32(1e-6), off).get()
+        assert ref.max_rel(y, ref.rmsnorm(x, g, F32(1e-6), off)) <= TOL[dt], (dt, shape, off)
+
+
+def test_layernorm_golden(xp):
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "layernorm_small.npz"))
+    y = xp.layernorm(up(xp, z["x"], "fp32"), up(xp, z["gamma"], "fp32"), up(xp, z["beta"], "fp32"), F32(1e-5)).get()
+    assert ref.max_rel(y, z["y"]) <= 1e-5
+
+
+# ---- softmax ------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("cols", [1, 5, 64, 200, 1024, 2100, 4096, 8200, 50257, 140000])
+def test_softmax_rows(xp, dt, cols):
+    rng = np.random.default_rng(cols)
+    rows = 3 if cols > 10000 else 9
+    x = rnd(dt, rng.standard_normal((rows, cols)).astype(F32) * 3)
+    pitch = (cols + 7) // 8 * 8
+    d = xp.empty((rows, cols), dt, pitch=pitch)
+    d.set(x)
+    for temp in (1.0, 0.7):
+        y = xp.softmax(d, temperature=temp).get()
+        want = ref.softmax(x, F32(temp))
+        assert ref.max_rel(y, want) <= TOL[dt], (dt, cols, temp)
+        np.testing.assert_allclose(y.sum(-1), 1.0, rtol=3e-2 if dt == "bf16" else 1e-5)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("T", [1, 7, 64, 129, 1024, 2048])
+def test_softmax_causal(xp, dt, T):
+    rng = np.random.default_rng(T)
+    B = 2 if T <= 1024 else 1
+    s = rnd(dt, rng.standard_normal((B, 3, T, T)).astype(F32) * 2)
+    pitch = (T + 7) // 8 * 8
+    d = xp.empty(s.shape, dt, pitch=pitch)
+    d.set(s)
+    y = xp.softmax(d, causal=True, period=T, offset=0).get()
+    want = ref.softmax(s + ref.causal_mask(T))
+    assert ref.max_rel(y, want) <= TOL[dt], (dt, T)
+    iu = np.triu_indices(T, 1)
+    assert np.all(y[..., iu[0], iu[1]] == 0)  # masked probabilities are exact zeros
+
+
+def test_softmax_causal_offset(xp):
+    """Decode-style rows: query t sees keys <= t + offset."""
+    rng = np.random.default_rng(11)
+    Tq, Tk, off = 4, 19, 15
+    s = rng.standard_normal((2, Tq, Tk)).astype(F32)
+    d = xp.empty(s.shape, "fp32", pitch=24)
+    d.set(s)
+    y = xp.softmax(d, causal=True, period=Tq, offset=off).get()
+    mask = np.where(np.arange(Tk)[None, :] <= np.arange(Tq)[:, None] + off, 0, -1e9).astype(F32)
+    assert ref.max_rel(y, ref.softmax(s + mask)) <= 1e-5
+
+
+def test_softmax_causal_golden(xp):
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "softmax_causal_small.npz"))
+    s = z["scores"]
+    d = xp.empty(s.shape, "fp32", pitch=8)
+    d.set(s)
+    y = xp.softmax(d, causal=True, period=s.shape[-1]).get()
+    assert ref.max_rel(y, z["probs"]) <= 1e-5
+
+
+# ---- RoPE ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 3, 16, 64), (1, 2, 5, 6), (8, 12, 1024, 64), (1, 2, 33, 256)])
+def test_rope(xp, dt, shape):
+    rng = np.random.default_rng(sum(shape))
+    x = rnd(dt, rng.standard_normal(shape).astype(F32))
+    T, D = shape[-2], shape[-1]
+    for pos0 in (0, 37):
+        tab = xp.rope_table(T, D, 10000.0, pos0)
+        cos, sin = ref.rope_table(T, D, 10000.0, pos0)
+        got_tab = tab.get()
+        assert ref.max_rel(got_tab[0], cos) <= 1e-6 and ref.max_rel(got_tab[1], sin) <= 1e-6
+        y = xp.rope(up(xp, x, dt), tab).get()
+        assert ref.max_rel(y, ref.rope(x, cos, sin)) <= TOL[dt], (dt, shape, pos0)
+
+
+# ---- activations --------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("n", [1, 13, 4096, 1000003])
+def test_activations(xp, dt, n):
+    rng = np.random.default_rng(n)
+    x = rnd(dt, rng.standard_normal(n).astype(F32) * 4)
+    d = up(xp, x, dt)
+    for name, code in (("gelu", xp.TL_ACT_GELU), ("silu", xp.TL_ACT_SILU)):
+        y = xp.activation(d, code).get()
+        assert ref.max_rel(y, ref.act(x, name)) <= TOL[dt], (dt, n, name)
+
+
+# ---- embedding gather ---------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("ids_dtype", [np.uint8, np.int32, np.int64])
+@pytest.mark.parametrize("C", [7, 128, 768])
+def test_embed(xp, dt, ids_dtype, C):
+    rng = np.random.default_rng(C)
+    V, B, T, ctx = 65, 3, 17, 20
+    table = rnd(dt, rng.standard_normal((V, C)).astype(F32))
+    pos = rnd(dt, rng.standard_normal((ctx, C)).astype(F32))
+    ids = rng.integers(0, V, (B, T)).astype(ids_dtype)
+    y = xp.embed(xp.array(ids), up(xp, table, dt), up(xp, pos, dt), T, out_shape=(B, T, C)).get()
+    want = rnd(dt, ref.embed_front(ids, table, pos))
+    assert np.array_equal(y, want)  # one add per element, rounded once: bit-exact
+
+
+def test_embed_out_of_range_is_an_error(xp):
+    table = up(xp, np.ones((5, 8), F32), "fp32")
+    ids = xp.array(np.array([[1, 5]], np.int32))
+    y = xp.embed(ids, table, None, 2, out_shape=(1, 2, 8))
+    with pytest.raises(xp.BadInputError):
+        y.get()
+    xp.synchronize()  # the latched error was consumed
+    ids = xp.array(np.array([[1, -1]], np.int64))
+    xp.embed(ids, table, None, 2, out_shape=(1, 2, 8))
+    with pytest.raises(IndexError):
+        xp.synchronize()
+
+
+# ---- argmax --------------------------------------------------------------------------------
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("cols", [1, 3, 65, 1000, 50257])
+def test_argmax(xp, dt, cols):
+    rng = np.random.default_rng(cols)
+    x = rnd(dt, rng.standard_normal((37, cols)).astype(F32))
+    if cols >= 3:
+        x[0, :] = 1.0                  # all ties -> index 0
+        x[1, cols // 2:] = 99.0         # tie run -> first index of the run
+        x[2, 1] = np.nan                # NaN wins
+        x[2, cols - 1] = np.nan
+    pitch = (cols + 7) // 8 * 8
+    d = xp.empty(x.shape, dt, pitch=pitch)
+    d.set(x)
+    got = xp.argmax(d).get()
+    assert got.dtype == np.int64
+    assert np.array_equal(got, np.argmax(x, axis=-1)), (dt, cols)
+
+
+# ---- GEMM ----------------------------------------------------------------------------------
+GEMM_CASES = [  # M, N, K
+    (1, 1, 8), (5, 7, 8), (64, 64, 64), (130, 70, 72), (128, 128, 768), (257, 300, 136),
+    (512, 2304, 768), (1000, 65, 128), (8, 50257, 64),
+]
+
+
+def gemm_ref(a, w, bias=None, act=None, res=None, divisor=1.0):
+    y = a.astype(np.float64) @ w.astype(np.float64)
+    if divisor != 1.0:
+        y = y / divisor
+    if bias is not None:
+        y = y + bias
+    if act is not None:
+        y = ref.act(y.astype(F32), act).astype(np.float64)
+    if res is not None:
+        y = y + res
+    return y
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("mnk", GEMM_CASES)
+def test_gemm_layouts_and_epilogues(xp, dt, mnk):
+    M, N, K = mnk
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a = rnd(dt, rng.standard_normal((M, K)).astype(F32))
+    w = rnd(dt, rng.standard_normal((K, N)).astype(F32) / np.sqrt(K))
+    bias = rnd(dt, rng.standard_normal(N).astype(F32))
+    res = rnd(dt, rng.standard_normal((M, N)).astype(F32))
+    da, dbias, dres = up(xp, a, dt), up(xp, bias, dt), up(xp, res, dt)
+    wt = up(xp, np.ascontiguousarray(w.T), dt)   # [N, K]
+    wkn = up(xp, w, dt)                            # [K, N]
+    ldc = (N + 7) // 8 * 8
+    cases = [
+        dict(),
+        dict(bias=True),
+        dict(bias=True, act="gelu"),
+        dict(bias=True, act="silu", res=True),
+        dict(divisor=8.0),
+    ]
+    for layout in ("nk", "kn"):
+        for c in cases:
+            out = xp.empty((M, N), dt, pitch=ldc)
+            act = {None: xp.TL_ACT_NONE, "gelu": xp.TL_ACT_GELU, "silu": xp.TL_ACT_SILU}[c.get("act")]
+            B, ldb, bl = (wt, K, xp.TL_B_NK) if layout == "nk" else (wkn, N, xp.TL_B_KN)
+            xp.gemm(da, B, M=M, N=N, K=K, lda=K, ldb=ldb, b_layout=bl, C=out, ldc=ldc,
+                    bias=dbias if c.get("bias") else None, act=act,
+                    residual=dres if c.get("res") else None, ldr=N,
+                    divisor=c.get("divisor", 1.0))
+            want = gemm_ref(a, w, bias if c.get("bias") else None, c.get("act"),
+                            res if c.get("res") else None, c.get("divisor", 1.0))
+            err = ref.max_rel(out.get(), rnd(dt, want))
+            assert err <= TOL[dt], (dt, mnk, layout, c, err)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_gemm_fp32_output_from_bf16(xp, dt):
+    M, N, K = 200, 96, 256
+    rng = np.random.default_rng(3)
+    a = rnd("bf16", rng.standard_normal((M, K)).astype(F32))
+    w = rnd("bf16", rng.standard_normal((N, K)).astype(F32))
+    out = xp.empty((M, N), "fp32")
+    xp.gemm(up(xp, a, "bf16"), up(xp, w, "bf16"), M=M, N=N, K=K, lda=K, ldb=K,
+            b_layout=xp.TL_B_NK, C=out, ldc=N, out_dtype="fp32")
+    assert ref.max_rel(out.get(), a.astype(np.float64) @ w.T.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_gemm_batched_two_level(xp, dt):
+    """P.V-style product: batch z = (b, h); output written into merged heads [B, T, H*D]."""
+    B, H, T, D = 2, 3, 40, 16
+    rng = np.random.default_rng(5)
+    p = rnd(dt, rng.random((B, H, T, T)).astype(F32))
+    vt = rnd(dt, rng.standard_normal((B, H, D, T)).astype(F32))
+    ldp = 40
+    dp = up(xp, p, dt)
+    out = xp.empty((B, T, H * D), dt)
+    xp.gemm(dp, up(xp, vt, dt), M=T, N=D, K=T, lda=ldp, ldb=T, b_layout=xp.TL_B_NK, C=out,
+            ldc=H * D, batch=B * H, batch_inner=H, sa=(H * T * ldp, T * ldp),
+            sb=(H * D * T, D * T), sc=(T * H * D, D), family="gemm_batched")
+    want = np.einsum("bhts,bhds->bthd", p.astype(np.float64), vt.astype(np.float64)).reshape(B, T, H * D)
+    assert ref.max_rel(out.get(), rnd(dt, want)) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("heads", [(4, 4), (8, 1), (4, 2)])
+def test_gemm_qkv_split(xp, dt, heads):
+    Hq, Hkv = heads
+    B, T, C, D = 2, 24, 64, 16
+    N = (Hq + 2 * Hkv) * D
+    rng = np.random.default_rng(Hq * 10 + Hkv)
+    x = rnd(dt, rng.standard_normal((B * T, C)).astype(F32))
+    w = rnd(dt, rng.standard_normal((C, N)).astype(F32) / 8)
+    bias = rnd(dt, rng.standard_normal(N).astype(F32))
+    q = xp.empty((B, Hq, T, D), dt)
+    k = xp.empty((B, Hkv, T, D), dt)
+    vt = xp.empty((B, Hkv, D, T), dt)
+    wt = up(xp, np.ascontiguousarray(w.T), dt)
+    xp.gemm(up(xp, x, dt), wt, M=B * T, N=N, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+            bias=up(xp, bias, dt), qkv=(q, k, vt, T, Hq, Hkv, D))
+    y = rnd(dt, gemm_ref(x, w, bias)).reshape(B, T, N)
+    qw, kw = Hq * D, Hkv * D
+    want_q = y[..., :qw].reshape(B, T, Hq, D).transpose(0, 2, 1, 3)
+    want_k = y[..., qw:qw + kw].reshape(B, T, Hkv, D).transpose(0, 2, 1, 3)
+    want_vt = y[..., qw + kw:].reshape(B, T, Hkv, D).transpose(0, 2, 3, 1)
+    for got, want in ((q, want_q), (k, want_k), (vt, want_vt)):
+        assert ref.max_rel(got.get(), want) <= TOL[dt]

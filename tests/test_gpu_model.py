@@ -1,0 +1,159 @@
+"""Model-level parity on the MI355X: the Layer interface (layers.py, transformer_adapters.py,
+network.py) on XP_RUNTIME=MI355X against the NumPy oracle on identical seeded weights and
+token ids. fp32: max_rel <= 1e-5; bf16: max_rel <= 2e-2 on logits; argmax ids bit-exact
+against np.argmax of the downloaded logits."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def tl():
+    import tl_hip
+    tl_hip.ctx()
+    import backend
+    import gpt
+    import layers
+    import transformer_adapters
+    return dict(xp=tl_hip, backend=backend, gpt=gpt, layers=layers, ta=transformer_adapters)
+
+
+def run_gpt(tl, cfg, ids, dt, seed, scale=0.02):
+    net, _ = tl["gpt"].build_gpt(cfg, dtype=dt)
+    tl["gpt"].seed_parameters(net, seed, scale)
+    probs = net.predict(ids)
+    logits = net.layers[-2].output
+    return net, probs, logits
+
+
+def test_char_gpt_fp32_end_to_end(tl):
+    """vocab 65, ctx 128, 4 layers, d 128, 4 heads, GeLU, batch 4."""
+    cfg = dict(vocab=65, ctx=128, layers=4, d=128, heads=4, act="gelu")
+    ids = np.random.default_rng(1).integers(0, 65, (4, 128))
+    net, probs, logits = run_gpt(tl, cfg, ids, "fp32", seed=0)
+    want_p, want_l = ref.gpt_forward(ids, ref.gpt_params(cfg, 0), cfg, return_logits=True)
+    got_l = logits.get()
+    assert ref.max_rel(got_l, want_l) <= 1e-5
+    assert ref.max_rel(probs.get(), want_p) <= 1e-5
+    ids_dev = tl["xp"].argmax(logits).get()
+    assert np.array_equal(ids_dev, np.argmax(got_l, -1))
+    assert np.array_equal(tl["xp"].argmax(probs).get(), np.argmax(probs.get(), -1))
+
+
+def test_char_gpt_uint8_ids_like_the_notebook(tl):
+    cfg = dict(vocab=65, ctx=128, layers=1, d=128, heads=4, act="silu")
+    ids = np.random.default_rng(2).integers(0, 65, (2, 50)).astype(np.uint8)
+    net, probs, logits = run_gpt(tl, cfg, ids, "fp32", seed=3)
+    want = ref.gpt_forward(ids, ref.gpt_params(cfg, 3), cfg)
+    assert ref.max_rel(probs.get(), want) <= 1e-5
+
+
+def test_tiny_gpt_golden(tl):
+    z = np.load(os.path.join(GOLDEN, "gpt_tiny.npz"))
+    cfg = {k[4:]: (z[k].item() if z[k].ndim == 0 else z[k]) for k in z.files if k.startswith("cfg_")}
+    cfg["act"] = str(cfg["act"])
+    net, probs, logits = run_gpt(tl, cfg, z["ids"], "fp32", seed=7, scale=0.5)
+    assert ref.max_rel(logits.get(), z["logits"]) <= 1e-5
+    assert ref.max_rel(probs.get(), z["probs"]) <= 1e-5
+    assert np.array_equal(tl["xp"].argmax(logits).get(), np.argmax(z["logits"], -1))
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("decoder", [True, False])
+@pytest.mark.parametrize("shape", [(2, 16, 64, 4), (1, 100, 96, 3), (2, 256, 768, 12)])
+def test_multihead_attention_layer(tl, dt, decoder, shape):
+    B, T, C, H = shape
+    tl["backend"].set_float_type(dt)
+    mha = tl["layers"].MultiHeadAttention(C, T + 4, H, decoder=decoder)
+    rng = np.random.default_rng(B * T + C)
+    P = [rng.standard_normal(p.shape).astype(F32) * F32(0.3 / np.sqrt(C) * 4) for p in mha.parameters]
+    P = [ref.round_bf16(p) if dt == "bf16" else p for p in P]
+    for p, a in zip(mha.parameters, P):
+        p.set(a)
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    if dt == "bf16":
+        x = ref.round_bf16(x)
+    y = mha.forward(tl["xp"].array(x, dtype=dt)).get()
+    want = ref.mha(x, *P, H, decoder, T + 4, rnd=ref.round_bf16 if dt == "bf16" else None)
+    tol = 1e-5 if dt == "fp32" else 2e-2
+    assert ref.max_rel(y, want) <= tol, (dt, decoder, shape)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_dense_and_vit_head(tl, dt):
+    tl["backend"].set_float_type(dt)
+    rng = np.random.default_rng(9)
+    d = tl["layers"].Dense(48, 10)
+    head = tl["ta"].VitMLPHead(384, 10)
+    for layer in (d, head):
+        for p in layer.parameters:
+            p.set(rng.standard_normal(p.shape).astype(F32) * F32(0.1))
+    rnd = ref.round_bf16 if dt == "bf16" else (lambda a: a)
+    x = rnd(rng.standard_normal((5, 7, 48)).astype(F32))
+    y = d.forward(tl["xp"].array(x, dtype=dt)).get()
+    w, b = [rnd(p.get()) for p in d.parameters]
+    tol = 1e-5 if dt == "fp32" else 2e-2
+    assert ref.max_rel(y, ref.dense(x, w, b)) <= tol
+    xv = rnd(rng.standard_normal((6, 65, 384)).astype(F32))
+    yv = head.forward(tl["xp"].array(xv, dtype=dt)).get()
+    w, b = [p.get() for p in head.parameters]
+    assert ref.max_rel(yv, ref.vit_head(xv, w, b)) <= tol
+
+
+def test_gpt2_small_shape_bf16_short(tl):
+    """BASELINE config 3 model (vocab 50257, 12 layers, d 768, 12 heads) at B=2, T=128."""
+    cfg = dict(vocab=50257, ctx=1024, layers=12, d=768, heads=12, act="gelu")
+    ids = np.random.default_rng(5).integers(0, 50257, (2, 128))
+    net, probs, logits = run_gpt(tl, cfg, ids, "bf16", seed=0)
+    want_p, want_l = ref.gpt_forward(ids, ref.gpt_params(cfg, 0, bf16=True), cfg, bf16=True,
+                                     return_logits=True)
+    got_l = logits.get()
+    assert ref.max_rel(got_l, want_l) <= 2e-2
+    assert ref.max_rel(probs.get(), want_p) <= 2e-2
+    assert np.array_equal(tl["xp"].argmax(logits).get(), np.argmax(got_l, -1))
+
+
+def test_gpt2_small_full_shape_bf16(tl):
+    """BASELINE config 3 at its full size, B=8, T=1024: size-independent properties over the
+    whole batch, oracle parity on sequence 0 (causal rows of one sequence depend only on
+    that sequence), and batch independence of sequence 0."""
+    cfg = dict(vocab=50257, ctx=1024, layers=12, d=768, heads=12, act="gelu")
+    ids = np.random.default_rng(6).integers(0, 50257, (8, 1024))
+    net, probs, logits = run_gpt(tl, cfg, ids, "bf16", seed=1)
+    xp = tl["xp"]
+    ids_logits = xp.argmax(logits).get()
+    ids_probs = xp.argmax(probs).get()
+    p_last = probs.get()[:, -1, :]
+    np.testing.assert_allclose(p_last.astype(np.float64).sum(-1), 1.0, rtol=2e-2)
+    # softmax is monotone: the most likely token is the largest logit (up to bf16 ties)
+    agree = np.mean(ids_logits == ids_probs)
+    assert agree > 0.99, agree
+    l0 = logits.get()[0]
+    want_p, want_l = ref.gpt_forward(ids[:1], ref.gpt_params(cfg, 1, bf16=True), cfg, bf16=True,
+                                     return_logits=True)
+    assert ref.max_rel(l0, want_l[0]) <= 2e-2
+    probs1 = net.predict(ids[:1])
+    l1 = net.layers[-2].output.get()[0]
+    assert ref.max_rel(l1, l0) <= 1e-6
+
+
+def test_sequence_longer_than_context_is_rejected(tl):
+    cfg = dict(vocab=11, ctx=8, layers=1, d=16, heads=2, act="gelu")
+    net, _ = tl["gpt"].build_gpt(cfg, dtype="fp32")
+    with pytest.raises(ValueError):
+        net.predict(np.zeros((1, 9), np.int64))
+
+
+def test_out_of_range_token_raises_index_error(tl):
+    cfg = dict(vocab=11, ctx=8, layers=1, d=16, heads=2, act="gelu")
+    net, _ = tl["gpt"].build_gpt(cfg, dtype="fp32")
+    with pytest.raises(IndexError):
+        net.predict(np.array([[1, 11]])).get()
+    tl["xp"].synchronize()

@@ -1,0 +1,227 @@
+"""Pins the NumPy oracle (oracle/numpy_ref.py) against closed forms, brute force and
+invariants, so that a dropped term, wrong sign, transposed operand or wrong index in the
+oracle fails here before it can vouch for a kernel."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+F32 = np.float32
+
+
+# ---- bf16 rounding ------------------------------------------------------------------------
+def test_bf16_rounding_bit_patterns():
+    vals = np.array([1.0, -2.0, 0.0, np.inf, -np.inf], dtype=F32)
+    assert ref.bf16_bits(vals).tolist() == [0x3F80, 0xC000, 0x0000, 0x7F80, 0xFF80]
+    # ties to even: 0x3F808000 is halfway between 0x3F80 and 0x3F81 -> even 0x3F80
+    u = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x3F807FFF], dtype=np.uint32)
+    assert ref.bf16_bits(u.view(F32)).tolist() == [0x3F80, 0x3F82, 0x3F81, 0x3F80]
+    nan = ref.bf16_bits(np.array([np.nan], dtype=F32))
+    assert (int(nan[0]) & 0x7F80) == 0x7F80 and (int(nan[0]) & 0x7F) != 0
+    assert np.array_equal(ref.round_bf16(np.array([3.0], F32)), np.array([3.0], F32))
+
+
+def test_max_rel_metric():
+    assert ref.max_rel([1.0, 2.0], [1.0, 2.0]) == 0.0
+    assert math.isclose(ref.max_rel([1.0, 2.5], [1.0, 2.0]), 0.25)
+
+
+# ---- activations ----------------------------------------------------------------------
+def test_gelu_closed_form_and_identities():
+    x = np.linspace(-8, 8, 2001, dtype=F32)
+    x64 = x.astype(np.float64)
+    exact = 0.5 * x64 * (1 + np.tanh(math.sqrt(2 / math.pi) * (x64 + 0.044715 * x64 ** 3)))
+    assert np.max(np.abs(ref.gelu(x) - exact)) < 1e-5
+    assert ref.gelu(np.zeros(3, F32)).tolist() == [0, 0, 0]
+    # odd-part identity: gelu(x) - gelu(-x) = x (because tanh is odd)
+    np.testing.assert_allclose(ref.gelu(x) - ref.gelu(-x), x, atol=1e-5)
+    assert abs(float(ref.gelu(np.array([1.0], F32))[0]) - 0.8411920) < 1e-6
+
+
+def test_silu_matches_sigmoid_form():
+    x = np.linspace(-20, 20, 4001, dtype=F32)
+    sig = 1 / (1 + np.exp(-x.astype(np.float64)))  # independent formula
+    np.testing.assert_allclose(ref.silu(x), x * sig, atol=2e-6, rtol=1e-5)
+    np.testing.assert_allclose(ref.silu(x) - ref.silu(-x), x, atol=1e-5)
+
+
+def test_softmax_properties():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((7, 33)).astype(F32) * 4
+    p = ref.softmax(x)
+    e = np.exp(x.astype(np.float64) - x.max(-1, keepdims=True))
+    np.testing.assert_allclose(p, e / e.sum(-1, keepdims=True), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(p.sum(-1), 1.0, rtol=1e-5)
+    np.testing.assert_allclose(ref.softmax(x + F32(3.0)), p, rtol=1e-5, atol=1e-7)
+    assert ref.softmax(np.array([[5.0]], F32)).tolist() == [[1.0]]
+    # temperature divides the shifted logits
+    e2 = np.exp((x.astype(np.float64) - x.max(-1, keepdims=True)) / 2.0)
+    np.testing.assert_allclose(ref.softmax(x, F32(2.0)), e2 / e2.sum(-1, keepdims=True), rtol=1e-5)
+
+
+# ---- normalisation ----------------------------------------------------------------------
+def _ln_brute(x, g, b, eps):
+    out = np.zeros_like(x, dtype=np.float64)
+    for r in range(x.shape[0]):
+        row = [float(v) for v in x[r]]
+        n = len(row)
+        mu = sum(row) / n
+        var = sum((v - mu) ** 2 for v in row) / n
+        for c in range(n):
+            out[r, c] = (row[c] - mu) / math.sqrt(var + eps) * float(g[c]) + float(b[c])
+    return out
+
+
+def test_layernorm_brute_force_and_invariants():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((5, 37)).astype(F32) * 3 + 1
+    g = rng.standard_normal(37).astype(F32)
+    b = rng.standard_normal(37).astype(F32)
+    np.testing.assert_allclose(ref.layernorm(x, g, b), _ln_brute(x, g, b, 1e-5), rtol=1e-5, atol=1e-5)
+    y = ref.layernorm(x, np.ones(37, F32), np.zeros(37, F32))
+    np.testing.assert_allclose(y.mean(-1), 0, atol=1e-6)
+    np.testing.assert_allclose(y.std(-1), np.sqrt(x.var(-1) / (x.var(-1) + 1e-5)), rtol=1e-5)
+
+
+def test_rmsnorm_brute_force_and_scale_invariance():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4, 19)).astype(F32)
+    g = rng.standard_normal(19).astype(F32)
+    brute = np.zeros((4, 19))
+    for r in range(4):
+        ms = sum(float(v) ** 2 for v in x[r]) / 19
+        for c in range(19):
+            brute[r, c] = float(x[r, c]) / math.sqrt(ms + 1e-6) * (1.0 + float(g[c]))
+    np.testing.assert_allclose(ref.rmsnorm(x, g, 1e-6, 1.0), brute, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(ref.rmsnorm(x * F32(7.0), g, 0.0), ref.rmsnorm(x, g, 0.0), rtol=1e-5, atol=1e-6)
+
+
+# ---- RoPE ---------------------------------------------------------------------------------
+def test_rope_against_complex_form_and_invariants():
+    rng = np.random.default_rng(3)
+    T, D = 9, 8
+    x = rng.standard_normal((2, T, D)).astype(F32)
+    cos, sin = ref.rope_table(T, D, 10000.0)
+    y = ref.rope(x, cos, sin)
+    half = D // 2
+    z = x[..., :half].astype(np.float64) + 1j * x[..., half:]
+    theta = 10000.0 ** (-np.arange(half) * 2.0 / D)
+    rot = z * np.exp(1j * np.arange(T)[:, None] * theta[None, :])
+    np.testing.assert_allclose(y[..., :half], rot.real, atol=1e-5)
+    np.testing.assert_allclose(y[..., half:], rot.imag, atol=1e-5)
+    np.testing.assert_allclose(y[:, 0], x[:, 0], atol=0)  # position 0 is the identity
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+    # relative position: <R_m q, R_n k> depends only on m - n
+    q, k = x[0, 0], x[1, 0]
+    def dot_at(m, n):
+        c, s = ref.rope_table(1, D, 10000.0, m)
+        c2, s2 = ref.rope_table(1, D, 10000.0, n)
+        return float(ref.rope(q[None], c, s)[0] @ ref.rope(k[None], c2, s2)[0])
+    assert abs(dot_at(5, 2) - dot_at(13, 10)) < 1e-4
+
+
+# ---- attention / blocks -------------------------------------------------------------------
+def _mha_brute(x, wqkv, bqkv, wo, bo, H, decoder):
+    B, T, C = x.shape
+    D = C // H
+    x64 = x.astype(np.float64)
+    qkv = x64 @ wqkv + bqkv
+    out = np.zeros((B, T, C))
+    for b in range(B):
+        heads = np.zeros((T, C))
+        for h in range(H):
+            q = qkv[b, :, h * D:(h + 1) * D]
+            k = qkv[b, :, C + h * D:C + (h + 1) * D]
+            v = qkv[b, :, 2 * C + h * D:2 * C + (h + 1) * D]
+            for i in range(T):
+                s = [sum(q[i, d] * k[j, d] for d in range(D)) / math.sqrt(D) for j in range(T)]
+                lim = i + 1 if decoder else T
+                m = max(s[:lim])
+                e = [math.exp(s[j] - m) if j < lim else 0.0 for j in range(T)]
+                tot = sum(e)
+                for d in range(D):
+                    heads[i, h * D + d] = sum(e[j] / tot * v[j, d] for j in range(T))
+        out[b] = heads @ wo + bo
+    return out
+
+
+@pytest.mark.parametrize("decoder", [True, False])
+def test_mha_brute_force(decoder):
+    rng = np.random.default_rng(4)
+    B, T, C, H = 2, 5, 8, 2
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    wqkv = rng.standard_normal((C, 3 * C)).astype(F32) * F32(0.3)
+    bqkv = rng.standard_normal(3 * C).astype(F32) * F32(0.1)
+    wo = rng.standard_normal((C, C)).astype(F32) * F32(0.3)
+    bo = rng.standard_normal(C).astype(F32) * F32(0.1)
+    got = ref.mha(x, wqkv, bqkv, wo, bo, H, decoder, context_length=T + 3)
+    np.testing.assert_allclose(got, _mha_brute(x, wqkv, bqkv, wo, bo, H, decoder), rtol=1e-4, atol=1e-5)
+
+
+def test_mha_head_order_with_permutation_weights():
+    """Q = K = 0 makes attention uniform (causal: mean over the prefix); with V = x and an
+    identity output projection the result is the running mean of x, whatever H is. Swapping
+    head blocks in V and Wo together must leave the output unchanged; swapping only V must
+    permute it, pinning the split/merge order."""
+    rng = np.random.default_rng(5)
+    B, T, C, H = 1, 4, 6, 3
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    wqkv = np.zeros((C, 3 * C), F32)
+    wqkv[:, 2 * C:] = np.eye(C, dtype=F32)
+    y = ref.mha(x, wqkv, np.zeros(3 * C, F32), np.eye(C, dtype=F32), np.zeros(C, F32), H, True)
+    running = np.cumsum(x, axis=1) / np.arange(1, T + 1)[None, :, None]
+    np.testing.assert_allclose(y, running, rtol=1e-5, atol=1e-6)
+    perm = np.array([2, 3, 0, 1, 4, 5])  # swap head 0 and head 1 (D=2)
+    w2 = wqkv.copy()
+    w2[:, 2 * C:] = np.eye(C, dtype=F32)[:, perm]
+    y2 = ref.mha(x, w2, np.zeros(3 * C, F32), np.eye(C, dtype=F32), np.zeros(C, F32), H, True)
+    np.testing.assert_allclose(y2, running[..., perm], rtol=1e-5, atol=1e-6)
+
+
+def test_causal_mask_values():
+    m = ref.causal_mask(3)
+    assert m.dtype == F32
+    assert m.tolist() == [[0, -1e9, -1e9], [0, 0, -1e9], [0, 0, 0]]
+
+
+def test_embed_front_and_back_brute_force():
+    rng = np.random.default_rng(6)
+    table = rng.standard_normal((11, 4)).astype(F32)
+    pos = rng.standard_normal((6, 4)).astype(F32)
+    ids = np.array([[3, 0, 10], [1, 1, 7]])
+    y = ref.embed_front(ids, table, pos)
+    for b in range(2):
+        for t in range(3):
+            assert np.array_equal(y[b, t], table[ids[b, t]] + pos[t])
+    logits = ref.embed_back(y, table)
+    for b in range(2):
+        for t in range(3):
+            for v in range(11):
+                assert abs(logits[b, t, v] - float(np.dot(y[b, t].astype(np.float64), table[v]))) < 1e-4
+
+
+def test_sinusoidal_positions_closed_form():
+    tab = ref.sinusoidal_positions(7, 6)
+    for p in range(7):
+        for i in range(6):
+            ang = p / 10000 ** (2 * (i // 2) / 6)
+            want = math.sin(ang) if i % 2 == 0 else math.cos(ang)
+            assert abs(tab[p, i] - want) < 1e-6
+
+
+def test_argmax_semantics():
+    x = np.array([[1, 3, 3, 0], [np.nan, 1, np.nan, 2], [-1, -1, -1, -1]], dtype=F32)
+    assert ref.argmax(x).tolist() == [1, 0, 0]
+
+
+def test_gpt_param_order_matches_layer_order():
+    cfg = dict(vocab=7, ctx=4, layers=2, d=4, heads=2)
+    names = [n for n, _ in ref.gpt_param_shapes(cfg)]
+    assert names[:2] == ["pos", "table"]
+    assert names[2:14] == [f"b0.{k}" for k in ("g1", "be1", "wqkv", "bqkv", "wo", "bo", "g2",
+                                               "be2", "w1", "bb1", "w2", "bb2")]
+    assert names[-2:] == ["lnf.g", "lnf.be"]
+    p = ref.gpt_params(cfg, 0)
+    assert abs(float(p["b0.g1"].mean()) - 1.0) < 0.05 and abs(float(p["b0.be1"].mean())) < 0.05

@@ -1,0 +1,914 @@
+// Row and elementwise kernels of the forward path: embedding gather, LayerNorm, RMSNorm,
+// (causal) softmax, RoPE, GeLU/SiLU, argmax, plus fill/cast/transpose/add helpers.
+//
+// All of them are HBM-bound. The fast variants give one wavefront (64 lanes) to a row,
+// keep the row in registers as 16-byte chunks (4 fp32 or 8 bf16 per chunk) so HBM is read
+// once and written once, and reduce with cross-lane shuffles. Rows longer than a wavefront
+// can hold go to a workgroup-per-row variant, and shapes whose pitch or alignment rules
+// out 16-byte access use a plain scalar variant.
+#include <cmath>
+#include <cstring>
+#include <type_traits>
+
+#include "tl_internal.hpp"
+
+namespace tl {
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static inline uint16_t host_f2bf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline unsigned grid_for(tl_ctx* ctx, int64_t work_items, int block) {
+  int64_t blocks = (work_items + block - 1) / block;
+  int64_t cap = (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  return (unsigned)blocks;
+}
+
+// ------------------------------------------------------------------------------------
+// fill / cast / add / transpose
+// ------------------------------------------------------------------------------------
+template <typename T>
+__global__ void fill_kernel(T* y, int64_t n, T v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = v;
+}
+
+template <typename TX, typename TY>
+__global__ void cast_kernel(const TX* x, TY* y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    Elem<TY>::store(y + i, Elem<TX>::load(x + i));
+}
+
+template <typename T>
+__global__ void add_kernel(const T* a, const T* b, T* y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    Elem<T>::store(y + i, Elem<T>::load(a + i) + Elem<T>::load(b + i));
+}
+
+// 64x64 tiles through LDS; element type is moved as raw bits.
+template <typename U>
+__global__ __launch_bounds__(256) void transpose_kernel(const U* x, U* y, int64_t rows,
+                                                        int64_t cols, int64_t ldx, int64_t ldy) {
+  __shared__ U tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int r = ty + 4 * i;
+    if (r0 + r < rows && c0 + tx < cols) tile[r][tx] = x[(r0 + r) * ldx + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int c = ty + 4 * i;
+    if (c0 + c < cols && r0 + tx < rows) y[(c0 + c) * ldy + r0 + tx] = tile[tx][c];
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// embedding gather + positional add (reference transformer_adapters.py:150-151)
+// ------------------------------------------------------------------------------------
+template <typename T, typename I, bool VEC>
+__global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table, const T* pos,
+                                                    T* out, int64_t n_tok, int64_t seq_len,
+                                                    int64_t pos0, int64_t vocab, int64_t dim,
+                                                    int64_t ld_out, int32_t* status) {
+  constexpr int VW = Elem<T>::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= n_tok) return;
+  const int64_t id = (int64_t)ids[tok];
+  T* o = out + tok * ld_out;
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(status, 1);
+    for (int64_t c = lane; c < dim; c += 64) Elem<T>::store(o + c, 0.0f);
+    return;
+  }
+  const T* tr = table + id * dim;
+  const T* pr = pos ? pos + (pos0 + tok % seq_len) * dim : nullptr;
+  if (VEC) {
+    for (int64_t c = (int64_t)lane * VW; c < dim; c += 64 * VW) {
+      float a[VW], b[VW];
+      load_chunk(tr + c, a);
+      if (pr) {
+        load_chunk(pr + c, b);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) a[e] = a[e] + b[e];
+      }
+      store_chunk(o + c, a);
+    }
+  } else {
+    for (int64_t c = lane; c < dim; c += 64) {
+      float a = Elem<T>::load(tr + c);
+      if (pr) a = a + Elem<T>::load(pr + c);
+      Elem<T>::store(o + c, a);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// LayerNorm / RMSNorm (reference layers.py:415-428)
+// ------------------------------------------------------------------------------------
+// One wavefront per row, CH 16-byte chunks per lane held in registers.
+template <typename T, int CH, bool RMS>
+__global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
+                                                        const T* __restrict__ g,
+                                                        const T* __restrict__ b,
+                                                        T* __restrict__ y, int64_t rows, int cols,
+                                                        int64_t ldx, int64_t ldy, float eps,
+                                                        float goff) {
+  constexpr int VW = Elem<T>::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * ldx;
+  float v[CH][VW];
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+    if (col < cols) {
+      load_chunk(xr + col, v[c]);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) s += RMS ? v[c][e] * v[c][e] : v[c][e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[c][e] = 0.f;
+    }
+  }
+  const float inv_n = 1.0f / (float)cols;
+  float mean = 0.f, rstd;
+  if (RMS) {
+    rstd = 1.0f / sqrtf(wave_sum(s) * inv_n + eps);
+  } else {
+    mean = wave_sum(s) / (float)cols;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * 64 + lane) * VW;
+      if (col < cols) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          const float d = v[c][e] - mean;
+          q += d * d;
+        }
+      }
+    }
+    rstd = 1.0f / sqrtf(wave_sum(q) / (float)cols + eps);
+  }
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+    if (col < cols) {
+      float gv[VW], bv[VW], o[VW];
+      load_chunk(g + col, gv);
+      if (!RMS) load_chunk(b + col, bv);
+#pragma unroll
+      for (int e = 0; e < VW; ++e)
+        o[e] = RMS ? (v[c][e] * rstd) * (goff + gv[e]) : gv[e] * ((v[c][e] - mean) * rstd) + bv[e];
+      store_chunk(yr + col, o);
+    }
+  }
+}
+
+// Any shape: one workgroup per row, three passes over the row in global memory.
+template <typename T, bool RMS>
+__global__ __launch_bounds__(256) void norm_generic_kernel(const T* x, const T* g, const T* b,
+                                                           T* y, int64_t rows, int64_t cols,
+                                                           int64_t ldx, int64_t ldy, float eps,
+                                                           float goff) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  auto block_sum = [&](float v) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    return red[0] + red[1] + red[2] + red[3];
+  };
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float v = Elem<T>::load(xr + c);
+    s += RMS ? v * v : v;
+  }
+  s = block_sum(s);
+  float mean = 0.f, rstd;
+  if (RMS) {
+    rstd = 1.0f / sqrtf(s / (float)cols + eps);
+  } else {
+    mean = s / (float)cols;
+    float q = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const float d = Elem<T>::load(xr + c) - mean;
+      q += d * d;
+    }
+    rstd = 1.0f / sqrtf(block_sum(q) / (float)cols + eps);
+  }
+  T* yr = y + row * ldy;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float v = Elem<T>::load(xr + c);
+    const float gv = Elem<T>::load(g + c);
+    const float o = RMS ? (v * rstd) * (goff + gv) : gv * ((v - mean) * rstd) + Elem<T>::load(b + c);
+    Elem<T>::store(yr + c, o);
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// softmax (reference layers.py:295-300, activations.py:57-64)
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ float softmax_exp(float z, float temp) {
+  if (temp != 1.0f) z = z / temp;
+  return __expf(z);
+}
+
+// Row r keeps columns j < valid(r); the rest are written as exact zeros (the reference's
+// additive -1e9 mask underflows exp to 0). Lanes skip loading masked chunks, so a causal
+// row reads its lower-triangle part only.
+template <typename T, int CH, bool CAUSAL>
+__global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__ x,
+                                                           T* __restrict__ y, int64_t rows,
+                                                           int cols, int64_t ldx, int64_t ldy,
+                                                           float temp, int64_t period,
+                                                           int64_t offset) {
+  constexpr int VW = Elem<T>::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  int valid = cols;
+  if (CAUSAL) {
+    const int64_t lim = row % period + offset + 1;
+    valid = lim < cols ? (int)lim : cols;
+  }
+  const T* xr = x + row * ldx;
+  float v[CH][VW];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+    if (col + VW <= valid) {
+      load_chunk(xr + col, v[c]);
+    } else if (col < valid) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e)
+        v[c][e] = (col + e < valid) ? Elem<T>::load(xr + col + e) : -INFINITY;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[c][e] = -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[c][e]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float ex = (col + e < valid) ? softmax_exp(v[c][e] - mx, temp) : 0.f;
+      v[c][e] = ex;
+      s += ex;
+    }
+  }
+  const float r = 1.0f / wave_sum(s);
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+    float o[VW];
+#pragma unroll
+    for (int e = 0; e < VW; ++e) o[e] = v[c][e] * r;
+    if (col + VW <= cols) {
+      store_chunk(yr + col, o);
+    } else if (col < cols) {
+      for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
+    }
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  v = is_max ? wave_max(v) : wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  return r;
+}
+
+// One workgroup of NT threads per row (vocabulary-sized rows), row held in registers.
+template <typename T, int NT, int CH, bool CAUSAL>
+__global__ __launch_bounds__(NT) void softmax_block_kernel(const T* __restrict__ x,
+                                                           T* __restrict__ y, int64_t rows,
+                                                           int cols, int64_t ldx, int64_t ldy,
+                                                           float temp, int64_t period,
+                                                           int64_t offset) {
+  constexpr int VW = Elem<T>::kVec;
+  __shared__ float red[NT / 64];
+  const int64_t row = blockIdx.x;
+  int valid = cols;
+  if (CAUSAL) {
+    const int64_t lim = row % period + offset + 1;
+    valid = lim < cols ? (int)lim : cols;
+  }
+  const T* xr = x + row * ldx;
+  float v[CH][VW];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * NT + threadIdx.x) * VW;
+    if (col + VW <= valid) {
+      load_chunk(xr + col, v[c]);
+    } else if (col < valid) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e)
+        v[c][e] = (col + e < valid) ? Elem<T>::load(xr + col + e) : -INFINITY;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[c][e] = -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[c][e]);
+  }
+  mx = block_reduce<NT>(mx, true, red);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * NT + threadIdx.x) * VW;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float ex = (col + e < valid) ? softmax_exp(v[c][e] - mx, temp) : 0.f;
+      v[c][e] = ex;
+      s += ex;
+    }
+  }
+  const float r = 1.0f / block_reduce<NT>(s, false, red);
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * NT + threadIdx.x) * VW;
+    float o[VW];
+#pragma unroll
+    for (int e = 0; e < VW; ++e) o[e] = v[c][e] * r;
+    if (col + VW <= cols) {
+      store_chunk(yr + col, o);
+    } else if (col < cols) {
+      for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
+    }
+  }
+}
+
+// Any shape: one workgroup per row; pass 1 keeps a running (max, sum), pass 2 writes.
+template <typename T, bool CAUSAL>
+__global__ __launch_bounds__(256) void softmax_generic_kernel(const T* x, T* y, int64_t rows,
+                                                              int64_t cols, int64_t ldx,
+                                                              int64_t ldy, float temp,
+                                                              int64_t period, int64_t offset) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  int64_t valid = cols;
+  if (CAUSAL) {
+    const int64_t lim = row % period + offset + 1;
+    valid = lim < cols ? lim : cols;
+  }
+  const T* xr = x + row * ldx;
+  float mx = -INFINITY;
+  for (int64_t c = threadIdx.x; c < valid; c += 256) mx = fmaxf(mx, Elem<T>::load(xr + c));
+  mx = block_reduce<256>(mx, true, red);
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < valid; c += 256) s += softmax_exp(Elem<T>::load(xr + c) - mx, temp);
+  const float r = 1.0f / block_reduce<256>(s, false, red);
+  T* yr = y + row * ldy;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float o = c < valid ? softmax_exp(Elem<T>::load(xr + c) - mx, temp) * r : 0.f;
+    Elem<T>::store(yr + c, o);
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// RoPE (rotate-half)
+// ------------------------------------------------------------------------------------
+__global__ void rope_table_kernel(float* table, int64_t seq_len, int64_t head_dim, double base,
+                                  int64_t pos0) {
+  const int64_t half = head_dim / 2;
+  const int64_t n = seq_len * half;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = idx / half, i = idx % half;
+    const double inv_freq = pow(base, -(double)(2 * i) / (double)head_dim);
+    const double ang = (double)(pos0 + t) * inv_freq;
+    table[idx] = (float)cos(ang);
+    table[n + idx] = (float)sin(ang);
+  }
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                   const float* __restrict__ table,
+                                                   int64_t n_seq, int64_t seq_len,
+                                                   int64_t head_dim) {
+  constexpr int VW = VEC ? Elem<T>::kVec : 1;
+  const int64_t half = head_dim / 2;
+  const int64_t per_row = half / VW;
+  const int64_t total = n_seq * seq_len * per_row;
+  const int64_t tsz = seq_len * half;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = idx / per_row;
+    const int64_t i = (idx % per_row) * VW;
+    const int64_t t = row % seq_len;
+    const T* xr = x + row * head_dim;
+    T* yr = y + row * head_dim;
+    const float* cs = table + t * half + i;
+    const float* sn = table + tsz + t * half + i;
+    float a[VW], b[VW], c[VW], s[VW], o1[VW], o2[VW];
+    if (VEC) {
+      load_chunk(xr + i, a);
+      load_chunk(xr + half + i, b);
+#pragma unroll
+      for (int e = 0; e < VW; e += 4) {
+        const float4 c4 = *reinterpret_cast<const float4*>(cs + e);
+        const float4 s4 = *reinterpret_cast<const float4*>(sn + e);
+        c[e] = c4.x; c[e + 1] = c4.y; c[e + 2] = c4.z; c[e + 3] = c4.w;
+        s[e] = s4.x; s[e + 1] = s4.y; s[e + 2] = s4.z; s[e + 3] = s4.w;
+      }
+    } else {
+      a[0] = Elem<T>::load(xr + i);
+      b[0] = Elem<T>::load(xr + half + i);
+      c[0] = cs[0];
+      s[0] = sn[0];
+    }
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      o1[e] = a[e] * c[e] - b[e] * s[e];
+      o2[e] = b[e] * c[e] + a[e] * s[e];
+    }
+    if (VEC) {
+      store_chunk(yr + i, o1);
+      store_chunk(yr + half + i, o2);
+    } else {
+      Elem<T>::store(yr + i, o1[0]);
+      Elem<T>::store(yr + half + i, o2[0]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// activations (reference activations.py:24-28, 41-45)
+// ------------------------------------------------------------------------------------
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void act_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                  int64_t n, int act) {
+  constexpr int VW = VEC ? Elem<T>::kVec : 1;
+  const int64_t nv = n / VW;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float v[VW];
+    if (VEC) {
+      load_chunk(x + i * VW, v);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[e] = apply_act(v[e], act);
+      store_chunk(y + i * VW, v);
+    } else {
+      Elem<T>::store(y + i, apply_act(Elem<T>::load(x + i), act));
+    }
+  }
+  if (VEC && blockIdx.x == 0) {
+    for (int64_t i = nv * VW + threadIdx.x; i < n; i += blockDim.x)
+      Elem<T>::store(y + i, apply_act(Elem<T>::load(x + i), act));
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// argmax (reference network.py:315, 338: xp.argmax(axis=-1), first index on ties)
+// ------------------------------------------------------------------------------------
+// True when (va, ia) should win over (vb, ib): NaN beats everything (NumPy returns the
+// first NaN), then larger value, then smaller index.
+__device__ __forceinline__ bool argmax_better(float va, int64_t ia, float vb, int64_t ib) {
+  const bool na = va != va, nb = vb != vb;
+  if (na || nb) return na && (!nb || ia < ib);
+  if (va != vb) return va > vb;
+  return ia < ib;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t rows,
+                                                     int64_t cols, int64_t ldx,
+                                                     int64_t* __restrict__ out) {
+  constexpr int VW = VEC ? Elem<T>::kVec : 1;
+  __shared__ float rv[4];
+  __shared__ int64_t ri[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  float best = -INFINITY;
+  int64_t bi = INT64_MAX;
+  for (int64_t c0 = (int64_t)threadIdx.x * VW; c0 < cols; c0 += 256 * VW) {
+    float v[VW];
+    if (VEC && c0 + VW <= cols) {
+      load_chunk(xr + c0, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[e] = (c0 + e < cols) ? Elem<T>::load(xr + c0 + e) : -INFINITY;
+    }
+#pragma unroll
+    for (int e = 0; e < VW; ++e)
+      if (c0 + e < cols && argmax_better(v[e], c0 + e, best, bi)) {
+        best = v[e];
+        bi = c0 + e;
+      }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int64_t oi = __shfl_xor(bi, o, 64);
+    if (argmax_better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) {
+    rv[w] = best;
+    ri[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < 4; ++i)
+      if (argmax_better(rv[i], ri[i], best, bi)) {
+        best = rv[i];
+        bi = ri[i];
+      }
+    out[row] = bi;
+  }
+}
+
+}  // namespace tl
+
+// ------------------------------------------------------------------------------------
+// host-side launchers (templated on the element type)
+// ------------------------------------------------------------------------------------
+namespace tl {
+
+template <typename T>
+static void launch_embed(tl_ctx* ctx, int ids_dtype, const void* ids, const void* table,
+                         const void* pos, void* out, int64_t n_tok, int64_t seq_len,
+                         int64_t pos0, int64_t vocab, int64_t dim, int64_t ld_out) {
+  const bool vec = dim % Elem<T>::kVec == 0 && ld_out % Elem<T>::kVec == 0 &&
+                   aligned16(table) && aligned16(out) && (!pos || aligned16(pos));
+  const unsigned g = (unsigned)((n_tok + 3) / 4);
+  auto go = [&](auto id_tag) {
+    typedef decltype(id_tag) I;
+    if (vec)
+      embed_kernel<T, I, true><<<g, 256, 0, ctx->stream>>>((const I*)ids, (const T*)table,
+          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, ctx->status);
+    else
+      embed_kernel<T, I, false><<<g, 256, 0, ctx->stream>>>((const I*)ids, (const T*)table,
+          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, ctx->status);
+  };
+  if (ids_dtype == TL_U8) go(uint8_t());
+  else if (ids_dtype == TL_I32) go(int32_t());
+  else go(int64_t());
+}
+
+template <typename T, bool RMS>
+static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b, void* y,
+                        int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float eps,
+                        float goff) {
+  constexpr int VW = Elem<T>::kVec;
+  const bool vec = cols % VW == 0 && ldx % VW == 0 && ldy % VW == 0 && aligned16(x) &&
+                   aligned16(y) && aligned16(g) && (RMS || aligned16(b));
+  const int64_t chunks = (cols / VW + 63) / 64;
+  const unsigned gw = (unsigned)((rows + 3) / 4);
+  auto wave = [&](auto ch_tag) {
+    constexpr int CH = decltype(ch_tag)::value;
+    norm_wave_kernel<T, CH, RMS><<<gw, 256, 0, ctx->stream>>>(
+        (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff);
+  };
+  if (vec && chunks <= 1) wave(std::integral_constant<int, 1>());
+  else if (vec && chunks <= 2) wave(std::integral_constant<int, 2>());
+  else if (vec && chunks <= 4) wave(std::integral_constant<int, 4>());
+  else if (vec && chunks <= 8) wave(std::integral_constant<int, 8>());
+  else if (vec && chunks <= 16) wave(std::integral_constant<int, 16>());
+  else
+    norm_generic_kernel<T, RMS><<<(unsigned)rows, 256, 0, ctx->stream>>>(
+        (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, cols, ldx, ldy, eps, goff);
+}
+
+template <typename T, bool CAUSAL>
+static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                           int64_t ldx, int64_t ldy, float temp, int64_t period, int64_t offset) {
+  constexpr int VW = Elem<T>::kVec;
+  const bool vec = ldx % VW == 0 && ldy % VW == 0 && aligned16(x) && aligned16(y);
+  const int64_t chunks = (cols + VW - 1) / VW;
+  const unsigned gw = (unsigned)((rows + 3) / 4);
+  auto wave = [&](auto ch_tag) {
+    constexpr int CH = decltype(ch_tag)::value;
+    softmax_wave_kernel<T, CH, CAUSAL><<<gw, 256, 0, ctx->stream>>>(
+        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+  };
+  auto block = [&](auto ch_tag) {
+    constexpr int CH = decltype(ch_tag)::value;
+    softmax_block_kernel<T, 1024, CH, CAUSAL><<<(unsigned)rows, 1024, 0, ctx->stream>>>(
+        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+  };
+  if (vec && chunks <= 64) wave(std::integral_constant<int, 1>());
+  else if (vec && chunks <= 128) wave(std::integral_constant<int, 2>());
+  else if (vec && chunks <= 256) wave(std::integral_constant<int, 4>());
+  else if (vec && chunks <= 512) wave(std::integral_constant<int, 8>());
+  else if (vec && chunks <= 1024 * 4) block(std::integral_constant<int, 4>());
+  else if (vec && chunks <= 1024 * 8) block(std::integral_constant<int, 8>());
+  else if (vec && chunks <= 1024 * 16) block(std::integral_constant<int, 16>());
+  else
+    softmax_generic_kernel<T, CAUSAL><<<(unsigned)rows, 256, 0, ctx->stream>>>(
+        (const T*)x, (T*)y, rows, cols, ldx, ldy, temp, period, offset);
+}
+
+template <typename T>
+static void launch_rope(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
+                        int64_t seq_len, int64_t head_dim) {
+  constexpr int VW = Elem<T>::kVec;
+  const int64_t half = head_dim / 2;
+  const bool vec = half % VW == 0 && aligned16(x) && aligned16(y) && aligned16(table) &&
+                   (seq_len * half) % 4 == 0;
+  const int64_t work = n_seq * seq_len * (vec ? half / VW : half);
+  const unsigned g = grid_for(ctx, work, 256);
+  if (vec)
+    rope_kernel<T, true><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
+                                                      n_seq, seq_len, head_dim);
+  else
+    rope_kernel<T, false><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
+                                                       n_seq, seq_len, head_dim);
+}
+
+template <typename T>
+static void launch_act(tl_ctx* ctx, const void* x, void* y, int64_t n, int act) {
+  const bool vec = aligned16(x) && aligned16(y);
+  const unsigned g = grid_for(ctx, vec ? n / Elem<T>::kVec + 1 : n, 256);
+  if (vec) act_kernel<T, true><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, n, act);
+  else act_kernel<T, false><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, n, act);
+}
+
+template <typename T>
+static void launch_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                          void* out) {
+  const bool vec = ldx % Elem<T>::kVec == 0 && aligned16(x);
+  if (vec)
+    argmax_kernel<T, true><<<(unsigned)rows, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out);
+  else
+    argmax_kernel<T, false><<<(unsigned)rows, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out);
+}
+
+template <bool RMS>
+static int norm_entry(tl_ctx* ctx, const void* x, const void* g, const void* b, void* y,
+                      int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float eps,
+                      float goff, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(dtype_is_float(dtype), "dtype %d is not a float type", dtype);
+  TL_REQUIRE(rows >= 0 && cols > 0, "bad sizes");
+  if (rows == 0) return TL_OK;
+  TL_REQUIRE(x && g && y && (RMS || b), "null pointer");
+  TL_REQUIRE(ldx >= cols && ldy >= cols, "leading dimension smaller than cols");
+  TL_REQUIRE(rows < (int64_t)0x7fffffff && cols < (int64_t)0x7fffffff, "too large");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, RMS ? TL_KF_RMSNORM : TL_KF_LAYERNORM, 0,
+                 es * (2.0 * rows * cols + (RMS ? 1 : 2) * cols));
+  if (dtype == TL_F32) launch_norm<float, RMS>(ctx, x, g, b, y, rows, cols, ldx, ldy, eps, goff);
+  else launch_norm<bf16_t, RMS>(ctx, x, g, b, y, rows, cols, ldx, ldy, eps, goff);
+  return ls.finish(RMS ? "rmsnorm_fwd" : "layernorm_fwd");
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+#define TL_REQUIRE_FLOAT(dtype) TL_REQUIRE(dtype_is_float(dtype), "dtype %d is not a float type", (int)(dtype))
+
+extern "C" {
+
+int tl_fill(tl_ctx* ctx, void* y, int64_t n, int32_t dtype, double value) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(n >= 0, "negative size");
+  const size_t es = dtype_size(dtype);
+  TL_REQUIRE(es, "bad dtype %d", dtype);
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(y, "null pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, (double)n * es);
+  const unsigned g = grid_for(ctx, n, 256);
+  switch (dtype) {
+    case TL_F32: fill_kernel<float><<<g, 256, 0, ctx->stream>>>((float*)y, n, (float)value); break;
+    case TL_BF16: fill_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>((uint16_t*)y, n, host_f2bf((float)value)); break;
+    case TL_I32: fill_kernel<int32_t><<<g, 256, 0, ctx->stream>>>((int32_t*)y, n, (int32_t)value); break;
+    case TL_I64: fill_kernel<int64_t><<<g, 256, 0, ctx->stream>>>((int64_t*)y, n, (int64_t)value); break;
+    case TL_U8: fill_kernel<uint8_t><<<g, 256, 0, ctx->stream>>>((uint8_t*)y, n, (uint8_t)value); break;
+  }
+  return ls.finish("fill");
+}
+
+int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dx, int32_t dy) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(n >= 0, "negative size");
+  TL_REQUIRE(dtype_is_float(dx) && dtype_is_float(dy), "cast supports fp32 and bf16 only");
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(x && y, "null pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, (double)n * (dtype_size(dx) + dtype_size(dy)));
+  const unsigned g = grid_for(ctx, n, 256);
+  if (dx == TL_F32 && dy == TL_BF16)
+    cast_kernel<float, bf16_t><<<g, 256, 0, ctx->stream>>>((const float*)x, (bf16_t*)y, n);
+  else if (dx == TL_BF16 && dy == TL_F32)
+    cast_kernel<bf16_t, float><<<g, 256, 0, ctx->stream>>>((const bf16_t*)x, (float*)y, n);
+  else if (dx == TL_F32)
+    cast_kernel<float, float><<<g, 256, 0, ctx->stream>>>((const float*)x, (float*)y, n);
+  else
+    cast_kernel<bf16_t, bf16_t><<<g, 256, 0, ctx->stream>>>((const bf16_t*)x, (bf16_t*)y, n);
+  return ls.finish("cast");
+}
+
+int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n >= 0, "negative size");
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(a && b && y, "null pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 3.0 * n * dtype_size(dtype));
+  const unsigned g = grid_for(ctx, n, 256);
+  if (dtype == TL_F32)
+    add_kernel<float><<<g, 256, 0, ctx->stream>>>((const float*)a, (const float*)b, (float*)y, n);
+  else
+    add_kernel<bf16_t><<<g, 256, 0, ctx->stream>>>((const bf16_t*)a, (const bf16_t*)b, (bf16_t*)y, n);
+  return ls.finish("add");
+}
+
+int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t ldy, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(rows >= 0 && cols >= 0, "negative size");
+  const size_t es = dtype_size(dtype);
+  TL_REQUIRE(es == 2 || es == 4, "transpose supports 2- and 4-byte types");
+  if (rows == 0 || cols == 0) return TL_OK;
+  TL_REQUIRE(x && y && x != y, "null or aliased pointer");
+  TL_REQUIRE(ldx >= cols && ldy >= rows, "leading dimension too small");
+  TL_REQUIRE((cols + 63) / 64 <= 0x7fffffff && (rows + 63) / 64 <= 65535, "matrix too large");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 2.0 * rows * cols * es);
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (es == 2)
+    transpose_kernel<uint16_t><<<grid, 256, 0, ctx->stream>>>((const uint16_t*)x, (uint16_t*)y, rows, cols, ldx, ldy);
+  else
+    transpose_kernel<uint32_t><<<grid, 256, 0, ctx->stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols, ldx, ldy);
+  return ls.finish("transpose2d");
+}
+
+int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* table,
+                 const void* pos, void* out, int64_t n_tok, int64_t seq_len, int64_t pos0,
+                 int64_t vocab, int64_t dim, int64_t ld_out, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n_tok >= 0 && vocab > 0 && dim > 0, "bad sizes");
+  if (n_tok == 0) return TL_OK;
+  TL_REQUIRE(ids && table && out, "null pointer");
+  TL_REQUIRE(seq_len > 0 && pos0 >= 0 && ld_out >= dim, "bad seq_len/pos0/ld_out");
+  TL_REQUIRE(ids_dtype == TL_U8 || ids_dtype == TL_I32 || ids_dtype == TL_I64, "ids must be u8, i32 or i64");
+  TL_REQUIRE(n_tok / 4 + 1 < 0x7fffffff, "too many tokens");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_EMBED, 0,
+                 (double)n_tok * (dtype_size(ids_dtype) + (pos ? 3 : 2) * dim * es));
+  if (dtype == TL_F32)
+    launch_embed<float>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out);
+  else
+    launch_embed<bf16_t>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out);
+  return ls.finish("embed_fwd");
+}
+
+int tl_layernorm_fwd(tl_ctx* ctx, const void* x, const void* gamma, const void* beta, void* y,
+                     int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float eps,
+                     int32_t dtype) {
+  return norm_entry<false>(ctx, x, gamma, beta, y, rows, cols, ldx, ldy, eps, 0.f, dtype);
+}
+
+int tl_rmsnorm_fwd(tl_ctx* ctx, const void* x, const void* gamma, void* y, int64_t rows,
+                   int64_t cols, int64_t ldx, int64_t ldy, float eps, float gamma_offset,
+                   int32_t dtype) {
+  return norm_entry<true>(ctx, x, gamma, nullptr, y, rows, cols, ldx, ldy, eps, gamma_offset, dtype);
+}
+
+int tl_softmax_fwd(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                   int64_t ldx, int64_t ldy, float temperature, int32_t causal, int64_t period,
+                   int64_t offset, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(rows >= 0 && cols > 0, "bad sizes");
+  if (rows == 0) return TL_OK;
+  TL_REQUIRE(x && y, "null pointer");
+  TL_REQUIRE(ldx >= cols && ldy >= cols, "leading dimension smaller than cols");
+  TL_REQUIRE(temperature > 0.f, "temperature must be positive");
+  TL_REQUIRE(!causal || (period > 0 && offset >= 0), "causal softmax needs period > 0, offset >= 0");
+  TL_REQUIRE(rows < (int64_t)0x7fffffff && cols < (int64_t)0x7fffffff, "too large");
+  if (!causal) {
+    period = 1;
+    offset = 0;
+  }
+  // algorithmic bytes: the kept part of each row is read, the whole row written
+  double kept = (double)rows * cols;
+  if (causal) {
+    auto tri = [&](int64_t n) {  // sum over i in [0, n) of min(cols, i + offset + 1)
+      double s = 0;
+      for (int64_t i = 0; i < n; ++i) s += (double)std::min<int64_t>(cols, i + offset + 1);
+      return s;
+    };
+    kept = (double)(rows / period) * tri(period) + tri(rows % period);
+  }
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_SOFTMAX, 0, es * (kept + (double)rows * cols));
+  if (dtype == TL_F32) {
+    if (causal) launch_softmax<float, true>(ctx, x, y, rows, cols, ldx, ldy, temperature, period, offset);
+    else launch_softmax<float, false>(ctx, x, y, rows, cols, ldx, ldy, temperature, period, offset);
+  } else {
+    if (causal) launch_softmax<bf16_t, true>(ctx, x, y, rows, cols, ldx, ldy, temperature, period, offset);
+    else launch_softmax<bf16_t, false>(ctx, x, y, rows, cols, ldx, ldy, temperature, period, offset);
+  }
+  return ls.finish("softmax_fwd");
+}
+
+int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
+                  int64_t pos0) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(table, "null pointer");
+  TL_REQUIRE(seq_len > 0 && head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and positive");
+  TL_REQUIRE(base > 0 && pos0 >= 0, "bad base/pos0");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 4.0 * seq_len * head_dim);
+  rope_table_kernel<<<grid_for(ctx, seq_len * head_dim / 2, 256), 256, 0, ctx->stream>>>(
+      (float*)table, seq_len, head_dim, base, pos0);
+  return ls.finish("rope_table");
+}
+
+int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
+                int64_t seq_len, int64_t head_dim, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n_seq >= 0 && seq_len > 0 && head_dim > 0 && head_dim % 2 == 0, "bad sizes");
+  if (n_seq == 0) return TL_OK;
+  TL_REQUIRE(x && y && table, "null pointer");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * n_seq * seq_len * head_dim);
+  if (dtype == TL_F32) launch_rope<float>(ctx, x, y, table, n_seq, seq_len, head_dim);
+  else launch_rope<bf16_t>(ctx, x, y, table, n_seq, seq_len, head_dim);
+  return ls.finish("rope_fwd");
+}
+
+int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n >= 0, "negative size");
+  TL_REQUIRE(act == TL_ACT_NONE || act == TL_ACT_GELU || act == TL_ACT_SILU, "bad activation %d", act);
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(x && y, "null pointer");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_ACT, 0, 2.0 * es * n);
+  if (dtype == TL_F32) launch_act<float>(ctx, x, y, n, act);
+  else launch_act<bf16_t>(ctx, x, y, n, act);
+  return ls.finish("act_fwd");
+}
+
+int tl_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+              int32_t dtype, void* out_ids) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(rows >= 0 && cols > 0, "bad sizes");
+  if (rows == 0) return TL_OK;
+  TL_REQUIRE(x && out_ids, "null pointer");
+  TL_REQUIRE(ldx >= cols, "leading dimension smaller than cols");
+  TL_REQUIRE(rows < (int64_t)0x7fffffff, "too many rows");
+  LaunchScope ls(ctx, TL_KF_ARGMAX, 0, (double)dtype_size(dtype) * rows * cols + 8.0 * rows);
+  if (dtype == TL_F32) launch_argmax<float>(ctx, x, rows, cols, ldx, out_ids);
+  else launch_argmax<bf16_t>(ctx, x, rows, cols, ldx, out_ids);
+  return ls.finish("argmax");
+}
+
+}  // extern "C"

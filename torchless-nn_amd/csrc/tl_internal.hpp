@@ -1,0 +1,186 @@
+// Shared internals of libtl: the context, error reporting, launch profiling and the
+// device-side helpers (bf16 conversion, 16-byte vector I/O, wavefront reductions).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "libtl.h"
+
+// ---------------------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------------------
+namespace tl {
+
+// Records the message for tl_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...);
+void clear_error();
+
+struct KprofRecord {
+  int family;
+  hipEvent_t start, stop;
+  double flops, bytes;
+};
+
+struct KprofTotals {
+  int64_t launches = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
+}  // namespace tl
+
+struct tl_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int32_t* status = nullptr;  // device word latched by kernels that see invalid data
+  // caching allocator: free blocks keyed by size, live blocks by pointer
+  std::multimap<size_t, void*> free_blocks;
+  std::unordered_map<void*, size_t> live;
+  size_t bytes_in_use = 0, bytes_cached = 0;
+  // launch profiler
+  uint32_t kprof_mask = 0;
+  std::vector<hipEvent_t> event_pool;
+  std::vector<tl::KprofRecord> kprof_pending;
+  tl::KprofTotals kprof_totals[TL_KF_COUNT];
+  int num_cus = 0;
+};
+
+namespace tl {
+
+inline bool dtype_is_float(int dt) { return dt == TL_F32 || dt == TL_BF16; }
+inline size_t dtype_size(int dt) {
+  switch (dt) {
+    case TL_F32: return 4;
+    case TL_BF16: return 2;
+    case TL_I32: return 4;
+    case TL_I64: return 8;
+    case TL_U8: return 1;
+  }
+  return 0;
+}
+
+// Checks the context, binds its device and clears the thread's error message.
+int enter(tl_ctx* ctx);
+
+// Brackets one kernel launch with profiler events when its family is enabled.
+struct LaunchScope {
+  tl_ctx* ctx;
+  int family;
+  double flops, bytes;
+  hipEvent_t start = nullptr;
+  LaunchScope(tl_ctx* c, int fam, double fl, double by);
+  // Checks the launch and closes the profiler record; returns a tl_status.
+  int finish(const char* what);
+};
+
+}  // namespace tl
+
+#define TL_CHECK_HIP(expr)                                                         \
+  do {                                                                             \
+    hipError_t _e = (expr);                                                        \
+    if (_e != hipSuccess)                                                          \
+      return tl::fail(TL_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));  \
+  } while (0)
+
+#define TL_REQUIRE(cond, ...)                                  \
+  do {                                                         \
+    if (!(cond)) return tl::fail(TL_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------
+// device side
+// ---------------------------------------------------------------------------------------
+namespace tl {
+
+typedef uint16_t bf16_t;  // raw bf16 storage
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf2f(bf16_t v) { return __uint_as_float((uint32_t)v << 16); }
+// Round-to-nearest-even (the gfx950 hardware conversion).
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(bf16_t, b);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kVec = 4;  // elements per 16-byte chunk
+  __device__ __forceinline__ static float load(const float* p) { return *p; }
+  __device__ __forceinline__ static void store(float* p, float v) { *p = v; }
+  __device__ __forceinline__ static void unpack(const uint4& u, float* v) {
+    v[0] = __uint_as_float(u.x); v[1] = __uint_as_float(u.y);
+    v[2] = __uint_as_float(u.z); v[3] = __uint_as_float(u.w);
+  }
+  __device__ __forceinline__ static uint4 pack(const float* v) {
+    return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                      __float_as_uint(v[3]));
+  }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kVec = 8;
+  __device__ __forceinline__ static float load(const bf16_t* p) { return bf2f(*p); }
+  __device__ __forceinline__ static void store(bf16_t* p, float v) { *p = f2bf(v); }
+  __device__ __forceinline__ static void unpack(const uint4& u, float* v) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static uint4 pack(const float* v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)f2bf(v[2 * i]) | ((uint32_t)f2bf(v[2 * i + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ void load_chunk(const T* p, float* v) {
+  Elem<T>::unpack(*reinterpret_cast<const uint4*>(p), v);
+}
+template <typename T>
+__device__ __forceinline__ void store_chunk(T* p, const float* v) {
+  *reinterpret_cast<uint4*>(p) = Elem<T>::pack(v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// tanh-approximation GeLU, reference activations.py:24-28:
+//   0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k = 0.7978845608028654f;  // sqrt(2/pi) rounded to fp32
+  float t = tanhf(k * (x + 0.044715f * (x * x * x)));
+  return 0.5f * x * (1.0f + t);
+}
+// SiLU through tanh, reference activations.py:41-45: x * (1 + tanh(x/2)) / 2
+__device__ __forceinline__ float silu_tanh(float x) {
+  float s = (1.0f + tanhf(x * 0.5f)) * 0.5f;
+  return x * s;
+}
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == TL_ACT_GELU) return gelu_tanh(v);
+  if (act == TL_ACT_SILU) return silu_tanh(v);
+  return v;
+}
+
+}  // namespace tl

@@ -1,0 +1,288 @@
+"""Transformer layers on the MI355X runtime (reference layers.py:195-476).
+
+Same classes, constructor arguments, parameter lists and `forward(x) -> y` contract as the
+reference; every forward is a handful of libtl kernel launches on one HIP stream:
+
+  Dense / FFN / projections -> tl_gemm with bias, activation and residual epilogues
+  MultiHeadAttention        -> QKV GEMM that scatters head-major Q, K and V^T, then the
+                               batched QK^T GEMM (scale epilogue), the causal softmax row
+                               kernel and the batched P.V GEMM that writes merged heads
+  LayerNorm / RMSNorm       -> one row kernel each
+
+bf16 weights are used by the MFMA GEMM in a K-contiguous copy ([out, in]) that is packed
+on the device the first time a weight is used and again whenever it is modified; fp32
+weights are read in place by the fp32 GEMM.
+"""
+import numpy as np
+
+import backend
+import tl_hip as xp
+from utils import Layer
+from activations import act_code_of
+
+__all__ = ["Dense", "Dropout", "MultiHeadAttention", "TransformerFeedForward", "LayerNorm",
+           "RMSNorm", "TransformerBlock", "linear"]
+
+
+def _round_up(n, m):
+    return (n + m - 1) // m * m
+
+
+def _packed_nk(w):
+    """[K, N] weight -> [N, K] (K-contiguous) copy for the MFMA GEMM, cached on the
+    weight until its contents change."""
+    if w._aux is not None and w._aux[0] == w._version:
+        return w._aux[1]
+    packed = xp.transpose2d(w)
+    w._aux = (w._version, packed)
+    return packed
+
+
+def linear(x2d, w, bias=None, act=xp.TL_ACT_NONE, residual=None, out=None, qkv=None,
+           family="gemm_mfma"):
+    """y = act(x2d @ w + bias) (+ residual), x2d [M, K], w [K, N] (reference `x @ W + b`)."""
+    M, K = x2d.shape
+    Kw, N = w.shape
+    if Kw != K:
+        raise ValueError(f"matmul shape mismatch: {x2d.shape} @ {w.shape}")
+    if qkv is None and out is None:
+        out = xp.empty((M, N), x2d.dtype)
+    if w.dtype is xp.bfloat16:
+        B, ldb, layout = _packed_nk(w), K, xp.TL_B_NK
+    else:
+        B, ldb, layout = w, w.pitch, xp.TL_B_KN
+    xp.gemm(x2d, B, M=M, N=N, K=K, lda=x2d.pitch, ldb=ldb, b_layout=layout, C=out,
+            ldc=(out.pitch if out is not None else 0), bias=bias, act=act, residual=residual,
+            ldr=(residual.pitch if residual is not None else 0), qkv=qkv, family=family)
+    return out
+
+
+class Dense(Layer):
+    """x @ W + b, W [in, out] (reference layers.py:195-209)."""
+
+    def __init__(self, input_size, output_size):
+        super(Dense, self).__init__()
+        self.weights = backend.init_random_tensor((input_size, output_size),
+                                                  divisor=(0.5 * input_size) ** 0.5)
+        self.bias = backend.init_zeros_tensor(output_size)
+        self.weight_grads = self.register_param(self.weights)
+        self.bias_grads = self.register_param(self.bias)
+
+    def forward(self, input):
+        self.input = input
+        x2 = input.reshape(-1, input.shape[-1])
+        y = linear(x2, self.weights, self.bias)
+        self.output = y.reshape(*input.shape[:-1], self.weights.shape[1])
+        return self.output
+
+
+class Dropout(Layer):
+    """Identity at inference (reference layers.py:217-233). Sampling a mask is a training
+    feature this runtime does not provide, so a non-zero rate outside eval mode raises."""
+
+    def __init__(self, dropout_rate):
+        super(Dropout, self).__init__()
+        self.dropout_rate = dropout_rate
+
+    def forward(self, input):
+        self.input = input
+        if self.dropout_rate > 0.0 and self.eval_mode is False:
+            raise NotImplementedError(
+                "Dropout with rate > 0 in training mode is not supported by the MI355X "
+                "runtime; call set_eval(True) (inference) or build with rate 0")
+        self.output = self.input
+        return self.output
+
+
+class MultiHeadAttention(Layer):
+    """Fused-QKV multi-head attention (reference layers.py:241-307).
+
+    Device layout per call: Q and K as [B, H, T, D], V transposed as [B, H, D, T] (the K
+    operand of P.V must be contiguous along T), scores/probabilities as [B, H, T, T] with
+    the row pitch rounded up to 8 elements, merged heads as [B, T, C]."""
+
+    def __init__(self, embedding_dim, context_length, num_heads, decoder=False,
+                 attn_dropout_rate=0.0, res_dropout_rate=0.0):
+        super(MultiHeadAttention, self).__init__()
+        self.embedding_dim = embedding_dim
+        self.context_length = context_length
+        self.num_heads = num_heads
+        self.heads_dim = embedding_dim // num_heads
+        self.is_decoder = decoder
+
+        self.query = None
+        self.key_t = None
+        self.value = None
+        self.softmax = None
+        self.heads_out = None
+
+        self.attn_dropout = Dropout(attn_dropout_rate)
+        self.res_dropout = Dropout(res_dropout_rate)
+
+        C = embedding_dim
+        self.qkv_weights = backend.init_random_tensor((C, 3 * C), divisor=(0.5 * C) ** 0.5)
+        self.qkv_bias = backend.init_zeros_tensor(3 * C)
+        self.out_weights = backend.init_random_tensor((C, C), divisor=(0.5 * C) ** 0.5)
+        self.out_bias = backend.init_zeros_tensor(C)
+
+        self.qkv_weight_grads = self.register_param(self.qkv_weights)
+        self.qkv_bias_grads = self.register_param(self.qkv_bias)
+        self.out_weight_grads = self.register_param(self.out_weights)
+        self.out_bias_grads = self.register_param(self.out_bias)
+
+    def forward(self, input):
+        return self._forward(input, None)
+
+    def _forward(self, input, residual):
+        """Returns heads @ W_o + b_o, plus `residual` when given (fused in the epilogue)."""
+        self.input = input
+        B, T, C = input.shape
+        H, D = self.num_heads, self.heads_dim
+        if self.is_decoder and T > self.context_length:
+            raise ValueError(f"sequence length {T} exceeds the context length "
+                             f"{self.context_length} of the causal mask")
+        dt = input.dtype
+        x2 = input.reshape(B * T, C)
+        q = xp.empty((B, H, T, D), dt)
+        k = xp.empty((B, H, T, D), dt)
+        vt = xp.empty((B, H, D, T), dt)
+        linear(x2, self.qkv_weights, self.qkv_bias, qkv=(q, k, vt, T, H, H, D))
+        self.query, self.key_t, self.value = q, k, vt
+
+        ldS = _round_up(T, 8)
+        scores = xp.empty((B, H, T, T), dt, pitch=ldS)
+        # (Q @ K^T) / sqrt(D): reference layers.py:293 divides after the product
+        xp.gemm(q, k, M=T, N=T, K=D, lda=D, ldb=D, b_layout=xp.TL_B_NK, C=scores, ldc=ldS,
+                batch=B * H, sa=(T * D, 0), sb=(T * D, 0), sc=(T * ldS, 0),
+                divisor=float(np.float32(D ** 0.5)), family="gemm_batched")
+        # additive -1e9 causal mask + softmax (reference layers.py:295-300), in place
+        probs = xp.softmax(scores, causal=self.is_decoder, period=T, offset=0, out=scores)
+        self.softmax = self.attn_dropout.forward(probs)
+
+        heads = xp.empty((B, T, C), dt)
+        # P @ V with the head merge folded into the store (reference layers.py:303-304)
+        xp.gemm(self.softmax, vt, M=T, N=D, K=T, lda=ldS, ldb=T, b_layout=xp.TL_B_NK, C=heads,
+                ldc=C, batch=B * H, batch_inner=H, sa=(H * T * ldS, T * ldS),
+                sb=(H * D * T, D * T), sc=(T * C, D), family="gemm_batched")
+        self.heads_out = heads
+
+        out = linear(heads.reshape(B * T, C), self.out_weights, self.out_bias,
+                     residual=(residual.reshape(B * T, C) if residual is not None else None))
+        self.output = out.reshape(B, T, C)
+        return self.res_dropout.forward(self.output)
+
+    def set_eval(self, eval_mode):
+        self.attn_dropout.set_eval(eval_mode)
+        self.res_dropout.set_eval(eval_mode)
+
+
+class TransformerFeedForward(Layer):
+    """act(x W1 + b1) W2 + b2 with a 4x hidden layer (reference layers.py:346-375). GeLU
+    and SiLU run in the first GEMM's epilogue."""
+
+    def __init__(self, num_channels, activation, res_dropout_rate=0.0):
+        super(TransformerFeedForward, self).__init__()
+        self.activation: Layer = activation()
+        self.act_code = act_code_of(activation)
+        self.dropout = Dropout(res_dropout_rate)
+        self.hidden_output = None
+        C = num_channels
+        self.weights1 = backend.init_random_tensor((C, 4 * C), divisor=(0.5 * C) ** 0.5)
+        self.bias1 = backend.init_zeros_tensor(4 * C)
+        self.weights2 = backend.init_random_tensor((4 * C, C), divisor=(2 * C) ** 0.5)
+        self.bias2 = backend.init_zeros_tensor(C)
+        self.weight_grads1 = self.register_param(self.weights1)
+        self.bias_grads1 = self.register_param(self.bias1)
+        self.weight_grads2 = self.register_param(self.weights2)
+        self.bias_grads2 = self.register_param(self.bias2)
+
+    def forward(self, input):
+        return self._forward(input, None)
+
+    def _forward(self, input, residual):
+        self.input = input
+        shape = input.shape
+        C = shape[-1]
+        x2 = input.reshape(-1, C)
+        if self.act_code is not None:
+            h = linear(x2, self.weights1, self.bias1, act=self.act_code)
+        else:
+            h = self.activation.forward(linear(x2, self.weights1, self.bias1))
+        self.hidden_output = h
+        y = linear(h, self.weights2, self.bias2,
+                   residual=(residual.reshape(-1, C) if residual is not None else None))
+        self.output = self.dropout.forward(y.reshape(*shape))
+        return self.output
+
+    def set_eval(self, eval_mode):
+        self.dropout.set_eval(eval_mode)
+
+
+class LayerNorm(Layer):
+    """(x - mean) / sqrt(var + 1e-5) * gamma + beta over the last axis, population
+    variance (reference layers.py:395-428)."""
+
+    def __init__(self, num_channels):
+        super(LayerNorm, self).__init__()
+        self.channels = num_channels
+        self.eps = np.float32(1e-5)
+        self.gamma = backend.init_zeros_tensor(num_channels).fill(1)
+        self.beta = backend.init_zeros_tensor(num_channels)
+        self.gamma_grads = self.register_param(self.gamma)
+        self.beta_grads = self.register_param(self.beta)
+
+    def forward(self, input):
+        self.input = input
+        self.output = xp.layernorm(input, self.gamma, self.beta, self.eps)
+        return self.output
+
+
+class RMSNorm(Layer):
+    """x / sqrt(mean(x^2) + eps) * (gamma_offset + gamma). Absent from the reference
+    (layers.py:394 is a TODO); gamma_offset=1 with gamma=0 init gives Gemma's convention."""
+
+    def __init__(self, num_channels, eps=1e-6, gamma_offset=0.0):
+        super(RMSNorm, self).__init__()
+        self.channels = num_channels
+        self.eps = np.float32(eps)
+        self.gamma_offset = float(gamma_offset)
+        self.gamma = backend.init_zeros_tensor(num_channels)
+        if self.gamma_offset == 0.0:
+            self.gamma.fill(1)
+        self.gamma_grads = self.register_param(self.gamma)
+
+    def forward(self, input):
+        self.input = input
+        self.output = xp.rmsnorm(input, self.gamma, self.eps, self.gamma_offset)
+        return self.output
+
+
+class TransformerBlock(Layer):
+    """Pre-LN block x + MHA(LN1 x), then + FFN(LN2 .) (reference layers.py:444-467). Both
+    residual adds run in the epilogues of the out-projection and second FFN GEMMs, so
+    `attn_block.output` and `ffn.output` hold the residual stream after each add."""
+
+    def __init__(self, embed_dim, context_length, num_heads, activation, decoder=False,
+                 attn_dropout_rate=0.0, res_dropout_rate=0.0):
+        super(TransformerBlock, self).__init__()
+        self.pre_attn_norm = LayerNorm(embed_dim)
+        self.attn_block = MultiHeadAttention(embed_dim, context_length, num_heads,
+                                             decoder=decoder,
+                                             attn_dropout_rate=attn_dropout_rate,
+                                             res_dropout_rate=res_dropout_rate)
+        self.pre_ffn_norm = LayerNorm(embed_dim)
+        self.ffn = TransformerFeedForward(embed_dim, activation,
+                                          res_dropout_rate=res_dropout_rate)
+        self.parameters = [*self.pre_attn_norm.parameters, *self.attn_block.parameters,
+                           *self.pre_ffn_norm.parameters, *self.ffn.parameters]
+
+    def forward(self, input):
+        self.input = input
+        y = self.attn_block._forward(self.pre_attn_norm.forward(input), residual=input)
+        self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), residual=y)
+        return self.output
+
+    def set_eval(self, eval_mode):
+        self.eval_mode = eval_mode
+        self.attn_block.set_eval(eval_mode)
+        self.ffn.set_eval(eval_mode)
