@@ -96,7 +96,7 @@ def row_kernel_bench(xp, reps=20):
     return out
 
 
-def cpu_baseline(sample_seqs=1, sample_T=SEQ):
+def cpu_baseline(sample_seqs=5, sample_T=SEQ):
     """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
     of the workload: `sample_seqs` sequences of T tokens of the same model."""
     from oracle import numpy_ref as ref
@@ -126,6 +126,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-row-kernels", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain fp32 copy kernel of 256 MiB three times (the "
+                         "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -135,6 +138,14 @@ def main():
     import tl_hip as xp
     import gpt
     xp.ctx()
+    if args.calibrate_copy:
+        n = 64 << 20  # 64 Mi fp32 = 256 MiB read + 256 MiB written per dispatch
+        src, dst = xp.empty((n,), "fp32").fill(1.0), xp.empty((n,), "fp32")
+        for _ in range(3):
+            xp.check(xp.lib().tl_cast(xp.ctx().handle, src.ptr, dst.ptr, n, 0, 0))
+        xp.synchronize()
+        del src, dst
+        log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
     log("building GPT-2-small-shape model (bf16) and seeding weights")
     net, _ = gpt.build_gpt(CFG, dtype="bf16")
     gpt.seed_parameters(net, 0)
