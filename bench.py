@@ -96,6 +96,57 @@ def row_kernel_bench(xp, reps=20):
     return out
 
 
+def gemm_sweep(xp, reps=10):
+    """Times every MFMA tile shape on the five dense GEMMs of one forward (with their real
+    epilogues) and prints TFLOP/s per (shape, tile); used to tune the tile heuristic."""
+    rng = np.random.default_rng(0)
+    M, C, V = BATCH * SEQ, CFG["d"], CFG["vocab"]
+    H, D = CFG["heads"], CFG["d"] // CFG["heads"]
+
+    def dev(shape, scale=0.02):
+        return xp.array(rng.standard_normal(shape).astype(np.float32) * np.float32(scale), dtype="bf16")
+
+    x, x4 = dev((M, C), 1.0), dev((M, 4 * C), 1.0)
+    res = dev((M, C), 1.0)
+    w = {"qkv": dev((3 * C, C)), "out": dev((C, C)), "ffn1": dev((4 * C, C)), "ffn2": dev((C, 4 * C)),
+         "head": dev((V, C))}
+    b = {k: dev((w[k].shape[0],)) for k in w}
+    q, k, vt = (xp.empty((BATCH, H, SEQ, D), "bf16"), xp.empty((BATCH, H, SEQ, D), "bf16"),
+                xp.empty((BATCH, H, D, SEQ), "bf16"))
+    out_c, out_4c = xp.empty((M, C), "bf16"), xp.empty((M, 4 * C), "bf16")
+    logits = xp.empty((M, V), "bf16", pitch=(V + 7) // 8 * 8)
+    shapes = {
+        "qkv": lambda t: xp.gemm(x, w["qkv"], M=M, N=3 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                 bias=b["qkv"], qkv=(q, k, vt, SEQ, H, H, D), tile=t),
+        "out_proj": lambda t: xp.gemm(x, w["out"], M=M, N=C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                      C=out_c, ldc=C, bias=b["out"], residual=res, ldr=C, tile=t),
+        "ffn1": lambda t: xp.gemm(x, w["ffn1"], M=M, N=4 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                  C=out_4c, ldc=4 * C, bias=b["ffn1"], act=xp.TL_ACT_GELU, tile=t),
+        "ffn2": lambda t: xp.gemm(x4, w["ffn2"], M=M, N=C, K=4 * C, lda=4 * C, ldb=4 * C,
+                                  b_layout=xp.TL_B_NK, C=out_c, ldc=C, bias=b["ffn2"], residual=res,
+                                  ldr=C, tile=t),
+        "lm_head": lambda t: xp.gemm(x, w["head"], M=M, N=V, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                     C=logits, ldc=logits.pitch, tile=t),
+    }
+    flops = {"qkv": 2 * M * 3 * C * C, "out_proj": 2 * M * C * C, "ffn1": 2 * M * 4 * C * C,
+             "ffn2": 2 * M * C * 4 * C, "lm_head": 2 * M * V * C}
+    table = {}
+    for name, fn in shapes.items():
+        table[name] = {}
+        for t in ["auto"] + [t for t in xp.GEMM_TILES if t != "auto"]:
+            for _ in range(2):
+                fn(t)
+            e0, e1 = xp.Event(), xp.Event()
+            e0.record()
+            for _ in range(reps):
+                fn(t)
+            e1.record()
+            ms = e0.elapsed_ms(e1) / reps
+            table[name][t] = {"us": round(ms * 1e3, 1), "tflops": round(flops[name] / (ms * 1e-3) / 1e12, 1)}
+        log(f"gemm sweep {name}: " + ", ".join(f"{t} {v['tflops']}" for t, v in table[name].items()))
+    return table
+
+
 def cpu_baseline(sample_seqs=5, sample_T=SEQ):
     """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
     of the workload: `sample_seqs` sequences of T tokens of the same model."""
@@ -126,6 +177,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-row-kernels", action="store_true")
+    ap.add_argument("--sweep-gemm", action="store_true",
+                    help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
                          "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -146,6 +199,9 @@ def main():
         xp.synchronize()
         del src, dst
         log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
+    if args.sweep_gemm:
+        print(json.dumps({"gemm_sweep": gemm_sweep(xp)}), flush=True)
+        return
     log("building GPT-2-small-shape model (bf16) and seeding weights")
     net, _ = gpt.build_gpt(CFG, dtype="bf16")
     gpt.seed_parameters(net, 0)

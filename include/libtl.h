@@ -58,6 +58,16 @@ enum tl_epilogue {
   TL_EPI_QKV_SPLIT = 1  /* scatter [M, (Hq+2*Hkv)*Dh] into q [B,Hq,T,Dh], k [B,Hkv,T,Dh], vt [B,Hkv,Dh,T] */
 };
 
+/* Output tile shapes (rows x columns) of the bf16 MFMA GEMM, for tl_gemm_desc.tile. */
+enum tl_gemm_tile {
+  TL_TILE_AUTO = 0,
+  TL_TILE_256x256 = 1,
+  TL_TILE_256x128 = 2,
+  TL_TILE_128x128 = 3,
+  TL_TILE_128x64 = 4,
+  TL_TILE_64x64 = 5
+};
+
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */
 enum tl_kfamily {
   TL_KF_GEMM_MFMA = 0,  /* bf16 MFMA GEMM, dense projections and LM head */
@@ -97,6 +107,8 @@ typedef struct tl_gemm_desc {
   void* q; void* k; void* vt;           /* TL_EPI_QKV_SPLIT outputs */
   int64_t seq_len, n_heads_q, n_heads_kv, head_dim;
   int32_t family;                       /* enum tl_kfamily used by the profiler */
+  int32_t tile;                         /* MFMA tile hint: 0 = choose automatically, else
+                                           enum tl_gemm_tile */
 } tl_gemm_desc;
 
 /* ---- runtime ------------------------------------------------------------------------ */

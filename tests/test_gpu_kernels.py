@@ -315,3 +315,99 @@ def test_gemm_qkv_split(xp, dt, heads):
     want_vt = y[..., qw + kw:].reshape(B, T, Hkv, D).transpose(0, 2, 3, 1)
     for got, want in ((q, want_q), (k, want_k), (vt, want_vt)):
         assert ref.max_rel(got.get(), want) <= TOL[dt]
+
+
+@pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64"])
+@pytest.mark.parametrize("mnk", [(300, 520, 200), (64, 64, 64), (513, 129, 776)])
+def test_gemm_every_tile_shape(xp, tile, mnk):
+    """Forces each MFMA tile shape on ragged M/N and a K tail, with a full epilogue."""
+    M, N, K = mnk
+    rng = np.random.default_rng(M + N + K)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+    wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    res = ref.round_bf16(rng.standard_normal((M, N)).astype(F32))
+    ldc = (N + 7) // 8 * 8
+    out = xp.empty((M, N), "bf16", pitch=ldc)
+    dres = xp.empty((M, N), "bf16", pitch=ldc)
+    dres.set(res)
+    xp.gemm(up(xp, a, "bf16"), up(xp, wt, "bf16"), M=M, N=N, K=K, lda=K, ldb=K,
+            b_layout=xp.TL_B_NK, C=out, ldc=ldc, bias=up(xp, bias, "bf16"), act=xp.TL_ACT_GELU,
+            residual=dres, ldr=ldc, tile=tile)
+    want = gemm_ref(a, wt.T, bias, "gelu", res)
+    assert ref.max_rel(out.get(), ref.round_bf16(want)) <= 2e-2, (tile, mnk)
+    # QKV split under the same tile
+    T, Hq, Hkv, D = 25, 2, 1, 16
+    Nq = (Hq + 2 * Hkv) * D
+    x = ref.round_bf16(rng.standard_normal((2 * T, 48)).astype(F32))
+    w2 = ref.round_bf16(rng.standard_normal((Nq, 48)).astype(F32))
+    q, k, vt = xp.empty((2, Hq, T, D), "bf16"), xp.empty((2, Hkv, T, D), "bf16"), xp.empty((2, Hkv, D, T), "bf16")
+    xp.gemm(up(xp, x, "bf16"), up(xp, w2, "bf16"), M=2 * T, N=Nq, K=48, lda=48, ldb=48,
+            b_layout=xp.TL_B_NK, qkv=(q, k, vt, T, Hq, Hkv, D), tile=tile)
+    y = ref.round_bf16(gemm_ref(x, w2.T)).reshape(2, T, Nq)
+    assert ref.max_rel(q.get(), y[..., :Hq * D].reshape(2, T, Hq, D).transpose(0, 2, 1, 3)) <= 2e-2
+    assert ref.max_rel(vt.get(), y[..., (Hq + Hkv) * D:].reshape(2, T, Hkv, D).transpose(0, 2, 3, 1)) <= 2e-2
+
+
+# ---- fused attention ---------------------------------------------------------------------
+def attention_ref(q, k, vt, Hq, Hkv, divisor, causal, offset):
+    """float64 scores / divisor, -inf above the (offset) diagonal, softmax, times V; out
+    [B, Tq, Hq*D] (the reference's layers.py:293-304 with its -1e9 mask)."""
+    B, _, Tq, D = q.shape
+    Tk = k.shape[2]
+    g = Hq // Hkv
+    out = np.zeros((B, Tq, Hq * D))
+    for b in range(B):
+        for h in range(Hq):
+            s = q[b, h].astype(np.float64) @ k[b, h // g].astype(np.float64).T / divisor
+            if causal:
+                s = s + np.where(np.arange(Tk)[None, :] <= np.arange(Tq)[:, None] + offset, 0, -1e9)
+            e = np.exp(s - s.max(-1, keepdims=True))
+            p = e / e.sum(-1, keepdims=True)
+            out[b, :, h * D:(h + 1) * D] = p @ vt[b, h // g].astype(np.float64).T
+    return out
+
+
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("T", [8, 136, 520])
+def test_attention_fused(xp, D, causal, T):
+    B, H = 2, 3
+    rng = np.random.default_rng(D + T)
+    q = ref.round_bf16(rng.standard_normal((B, H, T, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, H, T, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, H, D, T)).astype(F32))
+    out = xp.empty((B, T, H * D), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=H,
+                 n_heads_kv=H, divisor=divisor, causal=causal)
+    want = attention_ref(q, k, vt, H, H, divisor, causal, 0)
+    assert ref.max_rel(out.get(), want) <= 2e-2, (D, causal, T)
+
+
+@pytest.mark.parametrize("heads", [(8, 1), (4, 2)])
+def test_attention_fused_grouped_heads_and_offset(xp, heads):
+    """Multi-/grouped-query heads and a query block that sits at the end of a longer key
+    sequence (decode / chunked prefill: query t is at position t + offset)."""
+    Hq, Hkv = heads
+    B, Tq, Tk, D = 2, 40, 96, 64
+    rng = np.random.default_rng(Hq)
+    q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, Hkv, Tk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Tk)).astype(F32))
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=8.0, causal=True, offset=Tk - Tq)
+    want = attention_ref(q, k, vt, Hq, Hkv, 8.0, True, Tk - Tq)
+    assert ref.max_rel(out.get(), want) <= 2e-2
+
+
+def test_attention_fused_rejects_unsupported(xp):
+    q = xp.empty((1, 1, 12, 64), "bf16").fill(0)
+    with pytest.raises(xp.TLError):
+        xp.attention(q, q, xp.empty((1, 1, 64, 12), "bf16"), xp.empty((1, 12, 64), "bf16"),
+                     n_heads_q=1, n_heads_kv=1, divisor=8.0)  # Tk % 8 != 0
+    q32 = xp.empty((1, 1, 16, 64), "fp32").fill(0)
+    with pytest.raises(xp.TLError):
+        xp.attention(q32, q32, xp.empty((1, 1, 64, 16), "fp32"), xp.empty((1, 16, 64), "fp32"),
+                     n_heads_q=1, n_heads_kv=1, divisor=8.0)

@@ -2,11 +2,18 @@
 //
 // gemm_mfma_kernel: bf16 operands, fp32 accumulation on the gfx950 matrix cores
 //   (v_mfma_f32_16x16x32_bf16). A is [M, K] and B is given K-contiguous as Bt [N, K], so
-//   both tiles stream from HBM as 16-byte rows. BM x BN x 64 tiles are double-buffered in
-//   LDS (one barrier per K step); 16-byte chunks are XOR-swizzled by row so the fragment
-//   reads of 16 consecutive rows hit distinct banks. The MFMA is issued with Bt as its
-//   first operand, so the 16x16 result tile lands transposed: each lane holds 4 consecutive
-//   output columns of one row, which the epilogue stores as one 8- or 16-byte write.
+//   both tiles stream from memory as 16-byte chunks of K. Four wavefronts split a BM x BN
+//   output tile 2 x 2; each holds a (BM/2) x (BN/2) accumulator block, up to 128 x 128 (256
+//   fp32 accumulators per lane) so that one K step of 64 is 128 MFMAs per wave, long enough
+//   to cover the latency of the next step's global loads, which are issued before it.
+//   Operand tiles are double-buffered in LDS (one barrier per K step); the 16-byte chunks
+//   of a row are XOR-swizzled by row so fragment reads of 16 consecutive rows hit distinct
+//   banks. The MFMA takes Bt as its first operand, so each lane's 4 results are 4
+//   consecutive output columns of one row, stored as one 8- or 16-byte write.
+//   Output tiles are visited in an XCD-aware grouped order: workgroups are dispatched
+//   round-robin over the 8 XCDs, so block ids are remapped to give every XCD a contiguous
+//   run of tiles, and tiles run in groups of 8 tile-rows so the A and B panels a group
+//   shares stay in that XCD's L2.
 // gemm_simt_kernel: any dtype, layout or alignment, fp32 FMA on the vector ALUs. It
 //   serves the fp32 model and shapes the MFMA kernel's 16-byte loads cannot take.
 #include <algorithm>
@@ -33,8 +40,8 @@ struct GemmParams {
   void* q;
   void* k;
   void* vt;
-  int64_t T, Hq, Hkv, Dh;
-  int tiles_m, tiles_n;
+  int T, Hq, Hkv, Dh;
+  int tiles_m, tiles_n, group_m;
 };
 
 // Applies the epilogue to 4 consecutive columns n0..n0+3 of row m and stores them.
@@ -43,11 +50,18 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
                                           int64_t n0, float v[4]) {
   if (m >= p.M || n0 >= p.N) return;
   const int cnt = p.N - n0 >= 4 ? 4 : (int)(p.N - n0);
+  if (p.divisor != 1.0f) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    if (p.divisor != 1.0f) v[e] = v[e] / p.divisor;
-    if (p.bias && e < cnt) v[e] = v[e] + Elem<TI>::load((const TI*)p.bias + n0 + e);
-    v[e] = apply_act(v[e], p.act);
+    for (int e = 0; e < 4; ++e) v[e] = v[e] / p.divisor;
+  }
+  if (p.bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (e < cnt) v[e] = v[e] + Elem<TI>::load((const TI*)p.bias + n0 + e);
+  }
+  if (p.act != TL_ACT_NONE) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], p.act);
   }
   if (p.res) {
     const TO* r = (const TO*)p.res + zo * p.sr_o + zi * p.sr_i + m * p.ldr + n0;
@@ -56,20 +70,33 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
       if (e < cnt) v[e] = v[e] + Elem<TO>::load(r + e);
   }
   if (p.qkv) {
-    const int64_t b = m / p.T, t = m % p.T;
-    const int64_t qw = p.Hq * p.Dh, kw = p.Hkv * p.Dh;
-    for (int e = 0; e < cnt; ++e) {
-      const int64_t n = n0 + e;
-      if (n < qw) {
-        const int64_t h = n / p.Dh, d = n % p.Dh;
-        Elem<TO>::store((TO*)p.q + ((b * p.Hq + h) * p.T + t) * p.Dh + d, v[e]);
-      } else if (n < qw + kw) {
-        const int64_t h = (n - qw) / p.Dh, d = (n - qw) % p.Dh;
-        Elem<TO>::store((TO*)p.k + ((b * p.Hkv + h) * p.T + t) * p.Dh + d, v[e]);
-      } else {
-        const int64_t h = (n - qw - kw) / p.Dh, d = (n - qw - kw) % p.Dh;
-        Elem<TO>::store((TO*)p.vt + ((b * p.Hkv + h) * p.Dh + d) * p.T + t, v[e]);
-      }
+    // Dh % 4 == 0 (checked on the host), so the 4 columns share one head of one part.
+    const int mi = (int)m, ni = (int)n0;
+    const int b = mi / p.T, t = mi - b * p.T;
+    const int qw = p.Hq * p.Dh, kw = p.Hkv * p.Dh;
+    TO* dst;
+    int64_t step;
+    if (ni < qw) {
+      const int h = ni / p.Dh, d = ni - h * p.Dh;
+      dst = (TO*)p.q + ((int64_t)(b * p.Hq + h) * p.T + t) * p.Dh + d;
+      step = 1;
+    } else if (ni < qw + kw) {
+      const int nn = ni - qw, h = nn / p.Dh, d = nn - h * p.Dh;
+      dst = (TO*)p.k + ((int64_t)(b * p.Hkv + h) * p.T + t) * p.Dh + d;
+      step = 1;
+    } else {
+      const int nn = ni - qw - kw, h = nn / p.Dh, d = nn - h * p.Dh;
+      dst = (TO*)p.vt + ((int64_t)(b * p.Hkv + h) * p.Dh + d) * p.T + t;
+      step = p.T;
+    }
+    if (step == 1 && sizeof(TO) == 2) {
+      uint2 w;
+      w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+      w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+      *reinterpret_cast<uint2*>(dst) = w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Elem<TO>::store(dst + e * step, v[e]);
     }
     return;
   }
@@ -88,12 +115,28 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
   }
 }
 
+// Block id -> output tile (tm, tn): XCD-contiguous runs, then groups of group_m tile-rows
+// walked row-fastest.
+__device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, int& tn) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int x = bid & 7, local = bid >> 3;
+  const int q = ntiles >> 3, r = ntiles & 7;
+  const int i = x * q + min(x, r) + local;
+  const int per_group = p.group_m * p.tiles_n;
+  const int g = i / per_group;
+  const int first_m = g * p.group_m;
+  const int gm = min(p.tiles_m - first_m, p.group_m);
+  const int k = i - g * per_group;
+  tm = first_m + k % gm;
+  tn = k / gm;
+}
+
 template <typename TO, int BM, int BN>
 __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
-  constexpr int BK = 64;               // bf16 elements of K per tile (8 chunks of 16 B)
+  constexpr int BK = 64;                   // bf16 elements of K per step: 8 chunks of 16 B
   constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks per thread and tile
+  constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks per thread and step
   constexpr int B_CH = BN * BK / 8 / 256;
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
   __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * BK];
@@ -102,42 +145,55 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t z = blockIdx.z;
-  const int64_t zo = z / p.batch_inner, zi = z % p.batch_inner;
-  const int tile = blockIdx.x;
-  const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
-  const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
-  const bf16_t* A = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i;
-  const bf16_t* B = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i;
+  const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
+  int tm, tn;
+  map_tile(blockIdx.x, p, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int64_t M = p.M, N = p.N, K = p.K;
 
-  uint4 ra[A_CH], rb[B_CH];
-  auto load_tile = [&](int64_t k0) {
+  // Per-thread source rows (clamped rows are computed but never stored) and LDS slots.
+  const bf16_t* a_src[A_CH];
+  const bf16_t* b_src[B_CH];
+  int a_dst[A_CH], b_dst[B_CH], a_col[A_CH], b_col[B_CH];
+  {
+    const bf16_t* A = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i;
+    const bf16_t* B = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      const int64_t gm = min(m0 + r, M - 1);  // clamped rows are computed, never stored
-      const int64_t gk = k0 + c * 8;
-      ra[i] = gk < K ? *reinterpret_cast<const uint4*>(A + gm * p.lda + gk) : make_uint4(0, 0, 0, 0);
+      a_src[i] = A + min(m0 + r, M - 1) * p.lda + c * 8;
+      a_col[i] = c * 8;
+      a_dst[i] = r * BK + ((c ^ (r & 7)) << 3);
     }
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      const int64_t gn = min(n0 + r, N - 1);
-      const int64_t gk = k0 + c * 8;
-      rb[i] = gk < K ? *reinterpret_cast<const uint4*>(B + gn * p.ldb + gk) : make_uint4(0, 0, 0, 0);
+      b_src[i] = B + min(n0 + r, N - 1) * p.ldb + c * 8;
+      b_col[i] = c * 8;
+      b_dst[i] = r * BK + ((c ^ (r & 7)) << 3);
+    }
+  }
+  uint4 ra[A_CH], rb[B_CH];
+  auto load_tile = [&](int64_t k0) {
+    if (k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(a_src[i] + k0);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const uint4*>(b_src[i] + k0);
+    } else {  // K tail: K % 8 == 0, so a chunk is either fully inside K or fully outside
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i)
+        ra[i] = k0 + a_col[i] < K ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i)
+        rb[i] = k0 + b_col[i] < K ? *reinterpret_cast<const uint4*>(b_src[i] + k0) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      *reinterpret_cast<uint4*>(&As[buf][r * BK + ((c ^ (r & 7)) << 3)]) = ra[i];
-    }
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<uint4*>(&As[buf][a_dst[i]]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      *reinterpret_cast<uint4*>(&Bs[buf][r * BK + ((c ^ (r & 7)) << 3)]) = rb[i];
-    }
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<uint4*>(&Bs[buf][b_dst[i]]) = rb[i];
   };
 
   f32x4 acc[TM][TN];
@@ -243,6 +299,35 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+struct TileShape {
+  int bm, bn, per_cu;  // workgroups of this shape that fit on one CU (LDS / registers)
+};
+static const TileShape kTiles[] = {
+    {0, 0, 0}, {256, 256, 1}, {256, 128, 1}, {128, 128, 2}, {128, 64, 3}, {64, 64, 4}};
+
+// Tile choice, from a sweep of the five GPT-2-small GEMMs (M = 8192) on an MI355X:
+// 128x128 wins when the grid is many waves of CUs deep (LM head: 580 TFLOP/s against 459
+// for 128x64), 128x64 otherwise (QKV, FFN1, and the N = 768 projections), 64x64 when
+// even 128x64 leaves CUs idle. The 256-wide tiles are reachable through the hint only.
+static int choose_tile(int64_t M, int64_t N, int64_t batch, int cus) {
+  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+  const int64_t t64 = ((M + 127) / 128) * ((N + 63) / 64) * batch;
+  if (t128 >= 16LL * cus) return TL_TILE_128x128;
+  if (t64 >= (int64_t)cus) return TL_TILE_128x64;
+  return TL_TILE_64x64;
+}
+
+template <typename TO>
+static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
+  switch (tile) {
+    case TL_TILE_256x256: gemm_mfma_kernel<TO, 256, 256><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_256x128: gemm_mfma_kernel<TO, 256, 128><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_128x128: gemm_mfma_kernel<TO, 128, 128><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_128x64: gemm_mfma_kernel<TO, 128, 64><<<grid, 256, 0, st>>>(p); break;
+    default: gemm_mfma_kernel<TO, 64, 64><<<grid, 256, 0, st>>>(p); break;
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
@@ -253,11 +338,13 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d, "null descriptor");
   TL_REQUIRE(d->M > 0 && d->N > 0 && d->K > 0, "GEMM sizes must be positive (M=%lld N=%lld K=%lld)",
              (long long)d->M, (long long)d->N, (long long)d->K);
+  TL_REQUIRE(d->M < (1LL << 31) && d->N < (1LL << 31), "M and N must be below 2^31");
   TL_REQUIRE(d->A && d->B, "null operand");
   TL_REQUIRE(dtype_is_float(d->dtype_in) && dtype_is_float(d->dtype_out), "GEMM dtypes must be fp32 or bf16");
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_64x64, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -269,10 +356,11 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     TL_REQUIRE(d->q && d->k && d->vt, "QKV split needs q, k and vt");
     TL_REQUIRE(batch == 1 && !d->residual, "QKV split is unbatched and has no residual");
     TL_REQUIRE(d->seq_len > 0 && d->M % d->seq_len == 0, "M must be a multiple of seq_len");
-    TL_REQUIRE(d->head_dim > 0 && d->n_heads_q > 0 && d->n_heads_kv > 0 &&
-                   d->n_heads_q % d->n_heads_kv == 0,
-               "bad head configuration");
+    TL_REQUIRE(d->head_dim > 0 && d->head_dim % 4 == 0 && d->n_heads_q > 0 &&
+                   d->n_heads_kv > 0 && d->n_heads_q % d->n_heads_kv == 0,
+               "bad head configuration (head_dim must be a multiple of 4)");
     TL_REQUIRE(d->N == (d->n_heads_q + 2 * d->n_heads_kv) * d->head_dim, "N != (Hq + 2 Hkv) * Dh");
+    TL_REQUIRE(d->seq_len < (1LL << 31) && d->N * d->seq_len < (1LL << 40), "QKV split too large");
   } else {
     TL_REQUIRE(d->C, "null output");
     TL_REQUIRE(d->ldc >= d->N, "ldc < N");
@@ -288,10 +376,11 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.bias = d->bias; p.res = d->residual; p.ldr = d->ldr; p.sr_o = d->sr_o; p.sr_i = d->sr_i;
   p.divisor = d->divisor; p.act = d->act; p.b_kn = d->b_layout == TL_B_KN;
   p.qkv = qkv; p.q = d->q; p.k = d->k; p.vt = d->vt;
-  p.T = d->seq_len; p.Hq = d->n_heads_q; p.Hkv = d->n_heads_kv; p.Dh = d->head_dim;
+  p.T = (int)d->seq_len; p.Hq = (int)d->n_heads_q; p.Hkv = (int)d->n_heads_kv; p.Dh = (int)d->head_dim;
   const size_t eo = dtype_size(d->dtype_out);
   p.vec_store = !qkv && d->ldc % 4 == 0 && ((uintptr_t)d->C % (4 * eo)) == 0 &&
                 d->sc_o % 4 == 0 && d->sc_i % 4 == 0;
+  p.group_m = 8;
 
   // The MFMA kernel streams 16-byte rows of A and Bt: K-contiguous, 8-element aligned.
   const bool mfma = d->dtype_in == TL_BF16 && d->b_layout == TL_B_NK && d->K % 8 == 0 &&
@@ -304,30 +393,24 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
                                 (double)eo * d->M * d->N * (d->residual ? 2 : 1));
   const int family = mfma ? d->family : TL_KF_GEMM_SIMT;
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
-  LaunchScope ls(ctx, family, flops, bytes);
   const bool f32out = d->dtype_out == TL_F32;
   if (mfma) {
-    // 128x128 tiles, or 64x64 when 128x128 leaves most of the 256 CUs idle.
-    const int64_t t128 = ((d->M + 127) / 128) * ((d->N + 127) / 128) * batch;
-    const bool small = t128 < 2LL * (ctx->num_cus > 0 ? ctx->num_cus : 256);
-    const int bm = small ? 64 : 128, bn = bm;
-    p.tiles_m = (int)((d->M + bm - 1) / bm);
-    p.tiles_n = (int)((d->N + bn - 1) / bn);
+    const int tile = d->tile ? d->tile : choose_tile(d->M, d->N, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
+    const TileShape& s = kTiles[tile];
+    p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
+    p.tiles_n = (int)((d->N + s.bn - 1) / s.bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-    if (small) {
-      if (f32out) gemm_mfma_kernel<float, 64, 64><<<grid, 256, 0, ctx->stream>>>(p);
-      else gemm_mfma_kernel<bf16_t, 64, 64><<<grid, 256, 0, ctx->stream>>>(p);
-    } else {
-      if (f32out) gemm_mfma_kernel<float, 128, 128><<<grid, 256, 0, ctx->stream>>>(p);
-      else gemm_mfma_kernel<bf16_t, 128, 128><<<grid, 256, 0, ctx->stream>>>(p);
-    }
+    LaunchScope ls(ctx, family, flops, bytes);
+    if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
+    else launch_mfma<bf16_t>(tile, grid, ctx->stream, p);
     return ls.finish("gemm_mfma");
   }
   p.tiles_m = (int)((d->M + 63) / 64);
   p.tiles_n = (int)((d->N + 63) / 64);
   TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  LaunchScope ls(ctx, family, flops, bytes);
   if (d->dtype_in == TL_F32) {
     if (f32out) gemm_simt_kernel<float, float><<<grid, 256, 0, ctx->stream>>>(p);
     else gemm_simt_kernel<float, bf16_t><<<grid, 256, 0, ctx->stream>>>(p);

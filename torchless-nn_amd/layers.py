@@ -4,9 +4,10 @@ Same classes, constructor arguments, parameter lists and `forward(x) -> y` contr
 reference; every forward is a handful of libtl kernel launches on one HIP stream:
 
   Dense / FFN / projections -> tl_gemm with bias, activation and residual epilogues
-  MultiHeadAttention        -> QKV GEMM that scatters head-major Q, K and V^T, then the
-                               batched QK^T GEMM (scale epilogue), the causal softmax row
-                               kernel and the batched P.V GEMM that writes merged heads
+  MultiHeadAttention        -> QKV GEMM that scatters head-major Q, K and V^T, then (bf16)
+                               one fused attention kernel that writes merged heads, or
+                               (fp32 and shapes it does not take) the batched QK^T GEMM,
+                               the causal softmax row kernel and the batched P.V GEMM
   LayerNorm / RMSNorm       -> one row kernel each
 
 bf16 weights are used by the MFMA GEMM in a K-contiguous copy ([out, in]) that is packed
@@ -98,8 +99,11 @@ class MultiHeadAttention(Layer):
     """Fused-QKV multi-head attention (reference layers.py:241-307).
 
     Device layout per call: Q and K as [B, H, T, D], V transposed as [B, H, D, T] (the K
-    operand of P.V must be contiguous along T), scores/probabilities as [B, H, T, T] with
-    the row pitch rounded up to 8 elements, merged heads as [B, T, C]."""
+    operand of P.V must be contiguous along T), merged heads as [B, T, C]. The fused path
+    never materialises the [B, H, T, T] probabilities, so `softmax` stays None; the unfused
+    path keeps them (row pitch rounded up to 8 elements). `fused = False` forces the latter.
+    """
+    fused = True
 
     def __init__(self, embedding_dim, context_length, num_heads, decoder=False,
                  attn_dropout_rate=0.0, res_dropout_rate=0.0):
@@ -149,12 +153,30 @@ class MultiHeadAttention(Layer):
         linear(x2, self.qkv_weights, self.qkv_bias, qkv=(q, k, vt, T, H, H, D))
         self.query, self.key_t, self.value = q, k, vt
 
+        divisor = float(np.float32(D ** 0.5))  # reference layers.py:293 divides by sqrt(D)
+        if self.fused and xp.attention_supported(dt, D, T):
+            heads = xp.empty((B, T, C), dt)
+            if self.attn_dropout.dropout_rate > 0.0 and not self.attn_dropout.eval_mode:
+                self.attn_dropout.forward(heads)  # raises: no dropout sampling at inference
+            xp.attention(q, k, vt, heads, n_heads_q=H, n_heads_kv=H, divisor=divisor,
+                         causal=self.is_decoder, offset=0)
+            self.softmax = None
+        else:
+            heads = self._unfused(q, k, vt, B, T, C, H, D, dt, divisor)
+        self.heads_out = heads
+
+        out = linear(heads.reshape(B * T, C), self.out_weights, self.out_bias,
+                     residual=(residual.reshape(B * T, C) if residual is not None else None))
+        self.output = out.reshape(B, T, C)
+        return self.res_dropout.forward(self.output)
+
+    def _unfused(self, q, k, vt, B, T, C, H, D, dt, divisor):
         ldS = _round_up(T, 8)
         scores = xp.empty((B, H, T, T), dt, pitch=ldS)
         # (Q @ K^T) / sqrt(D): reference layers.py:293 divides after the product
         xp.gemm(q, k, M=T, N=T, K=D, lda=D, ldb=D, b_layout=xp.TL_B_NK, C=scores, ldc=ldS,
                 batch=B * H, sa=(T * D, 0), sb=(T * D, 0), sc=(T * ldS, 0),
-                divisor=float(np.float32(D ** 0.5)), family="gemm_batched")
+                divisor=divisor, family="gemm_batched")
         # additive -1e9 causal mask + softmax (reference layers.py:295-300), in place
         probs = xp.softmax(scores, causal=self.is_decoder, period=T, offset=0, out=scores)
         self.softmax = self.attn_dropout.forward(probs)
@@ -164,12 +186,7 @@ class MultiHeadAttention(Layer):
         xp.gemm(self.softmax, vt, M=T, N=D, K=T, lda=ldS, ldb=T, b_layout=xp.TL_B_NK, C=heads,
                 ldc=C, batch=B * H, batch_inner=H, sa=(H * T * ldS, T * ldS),
                 sb=(H * D * T, D * T), sc=(T * C, D), family="gemm_batched")
-        self.heads_out = heads
-
-        out = linear(heads.reshape(B * T, C), self.out_weights, self.out_bias,
-                     residual=(residual.reshape(B * T, C) if residual is not None else None))
-        self.output = out.reshape(B, T, C)
-        return self.res_dropout.forward(self.output)
+        return heads
 
     def set_eval(self, eval_mode):
         self.attn_dropout.set_eval(eval_mode)

@@ -23,6 +23,7 @@ TL_OK, TL_ERR_INVALID, TL_ERR_HIP, TL_ERR_OOM, TL_ERR_NO_DEVICE, TL_ERR_BAD_INPU
 TL_ACT_NONE, TL_ACT_GELU, TL_ACT_SILU = 0, 1, 2
 TL_B_NK, TL_B_KN = 0, 1
 TL_EPI_STORE, TL_EPI_QKV_SPLIT = 0, 1
+GEMM_TILES = {"auto": 0, "256x256": 1, "256x128": 2, "128x128": 3, "128x64": 4, "64x64": 5}
 KFAMILY = {
     "gemm_mfma": 0, "gemm_batched": 1, "gemm_simt": 2, "layernorm": 3, "rmsnorm": 4,
     "softmax": 5, "rope": 6, "act": 7, "embed": 8, "argmax": 9, "attention": 10, "misc": 11,
@@ -123,7 +124,7 @@ class _GemmDesc(ctypes.Structure):
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("vt", ctypes.c_void_p),
         ("seq_len", ctypes.c_int64), ("n_heads_q", ctypes.c_int64),
         ("n_heads_kv", ctypes.c_int64), ("head_dim", ctypes.c_int64),
-        ("family", ctypes.c_int32),
+        ("family", ctypes.c_int32), ("tile", ctypes.c_int32),
     ]
 
 
@@ -503,7 +504,7 @@ def _c():
 def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=None, ldc=0,
          out_dtype=None, batch=1, batch_inner=1, sa=(0, 0), sb=(0, 0), sc=(0, 0), bias=None,
          residual=None, ldr=0, sr=(0, 0), act=TL_ACT_NONE, divisor=1.0, qkv=None,
-         family="gemm_mfma"):
+         family="gemm_mfma", tile="auto"):
     d = _GemmDesc()
     d.M, d.N, d.K = M, N, K
     d.A, d.lda, d.B, d.ldb, d.b_layout = A.ptr, lda, B.ptr, ldb, b_layout
@@ -520,6 +521,7 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
     d.sr_o, d.sr_i = sr
     d.act, d.divisor = act, float(divisor)
     d.family = KFAMILY[family]
+    d.tile = GEMM_TILES[tile]
     if qkv is not None:
         q, k, vt, T, Hq, Hkv, Dh = qkv
         d.epilogue = TL_EPI_QKV_SPLIT
@@ -591,6 +593,26 @@ def embed(ids: DeviceTensor, table: DeviceTensor, pos, seq_len, pos0=0, out_shap
                             pos.ptr if pos is not None else None, out.ptr, ids.size, seq_len,
                             pos0, V, C, out.pitch, table.dtype.code))
     return out
+
+
+def attention(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTensor, *,
+              n_heads_q, n_heads_kv, divisor, causal=True, offset=0):
+    """Fused attention: q [B, Hq, Tq, D], k [B, Hkv, Tk, D], vt [B, Hkv, D, Tk] -> out
+    [B, Tq, Hq*D] (row pitch out.pitch). Raises TLError(TL_ERR_UNSUPPORTED) for shapes
+    the kernel does not take."""
+    B, Hq, Tq, D = q.shape
+    Tk = k.shape[2]
+    lib_, h = _c()
+    check(lib_.tl_attention_fwd(h, q.ptr, k.ptr, vt.ptr, out.ptr, B, n_heads_q, n_heads_kv, Tq,
+                                Tk, D, out.pitch, int(offset), float(divisor), int(bool(causal)),
+                                q.dtype.code))
+    return out
+
+
+def attention_supported(dtype, head_dim, seq_k) -> bool:
+    """Whether tl_attention_fwd takes this configuration (bf16, D in {32, 64, 128, 256},
+    key length a multiple of 8)."""
+    return as_dtype(dtype) is bfloat16 and head_dim in (32, 64, 128, 256) and seq_k % 8 == 0
 
 
 def transpose2d(x: DeviceTensor) -> DeviceTensor:
