@@ -96,7 +96,7 @@ def row_kernel_bench(xp, reps=20):
     return out
 
 
-def gemm_sweep(xp, reps=10):
+def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None):
     """Times every MFMA tile shape on the five dense GEMMs of one forward (with their real
     epilogues) and prints TFLOP/s per (shape, tile); used to tune the tile heuristic."""
     rng = np.random.default_rng(0)
@@ -132,8 +132,12 @@ def gemm_sweep(xp, reps=10):
              "ffn2": 2 * M * C * 4 * C, "lm_head": 2 * M * V * C}
     table = {}
     for name, fn in shapes.items():
+        if only_shapes and name not in only_shapes:
+            continue
         table[name] = {}
         for t in ["auto"] + [t for t in xp.GEMM_TILES if t != "auto"]:
+            if only_tiles and t not in only_tiles:
+                continue
             for _ in range(2):
                 fn(t)
             e0, e1 = xp.Event(), xp.Event()
@@ -179,6 +183,8 @@ def main():
     ap.add_argument("--no-row-kernels", action="store_true")
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
+    ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
+    ap.add_argument("--sweep-tiles", default="", help="comma list of tiles for --sweep-gemm")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
                          "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -200,7 +206,9 @@ def main():
         del src, dst
         log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
     if args.sweep_gemm:
-        print(json.dumps({"gemm_sweep": gemm_sweep(xp)}), flush=True)
+        print(json.dumps({"gemm_sweep": gemm_sweep(
+            xp, only_shapes=[x for x in args.sweep_shapes.split(",") if x],
+            only_tiles=[x for x in args.sweep_tiles.split(",") if x])}), flush=True)
         return
     log("building GPT-2-small-shape model (bf16) and seeding weights")
     net, _ = gpt.build_gpt(CFG, dtype="bf16")

@@ -65,7 +65,14 @@ enum tl_gemm_tile {
   TL_TILE_256x128 = 2,
   TL_TILE_128x128 = 3,
   TL_TILE_128x64 = 4,
-  TL_TILE_64x64 = 5
+  TL_TILE_64x64 = 5,
+  TL_TILE_256x256_W4 = 6, /* 256x256 with 4 waves (128x128 per wave); TL_TILE_256x256 uses 8 */
+  TL_TILE_256x128_W8 = 7, /* 256x128 with 8 waves (64x64 per wave); TL_TILE_256x128 uses 4 */
+  /* direct global->LDS variants (K % 64 == 0; other K fall back to TL_TILE_128x128) */
+  TL_TILE_DMA_128x128 = 8,     /* 2 stages */
+  TL_TILE_DMA_256x128_W8 = 9,  /* 8 waves, 3 stages */
+  TL_TILE_DMA_128x64_S3 = 10,  /* 3 stages */
+  TL_TILE_DMA_128x128_S3 = 11  /* 3 stages */
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

@@ -115,6 +115,22 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
   }
 }
 
+// The kernel's only argument is a GemmParams by value, at offset 0 of the kernarg segment.
+// The epilogue re-reads it through an opaque copy of the segment pointer: those loads
+// cannot be hoisted to the kernel entry, so the ~40 scalar registers of epilogue fields
+// are not held across the K loop (holding them made the large tiles spill to scratch).
+typedef __attribute__((address_space(4))) const uint32_t ConstU32;
+__device__ __forceinline__ GemmParams late_params() {
+  static_assert(sizeof(GemmParams) % 4 == 0, "GemmParams must be whole dwords");
+  ConstU32* src = (ConstU32*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(src));
+  GemmParams e;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(&e);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(GemmParams) / 4); ++i) dst[i] = src[i];
+  return e;
+}
+
 // Block id -> output tile (tm, tn): XCD-contiguous runs, then groups of group_m tile-rows
 // walked row-fastest.
 __device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, int& tn) {
@@ -131,69 +147,68 @@ __device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, 
   tn = k / gm;
 }
 
-template <typename TO, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
+template <typename TO, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p) {
+  constexpr int NT = 64 * WGM * WGN;       // WGM x WGN waves
   constexpr int BK = 64;                   // bf16 elements of K per step: 8 chunks of 16 B
-  constexpr int WM = BM / 2, WN = BN / 2;  // 2 x 2 waves
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks per thread and step
-  constexpr int B_CH = BN * BK / 8 / 256;
-  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
+  constexpr int RPP = NT / 8;              // tile rows one load pass covers (8 chunks per row)
+  constexpr int A_CH = BM / RPP, B_CH = BN / RPP;
+  static_assert(BM % RPP == 0 && BN % RPP == 0 && RPP % 8 == 0, "bad tile/thread split");
+  static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
   __shared__ __attribute__((aligned(16))) bf16_t As[2][BM * BK];
   __shared__ __attribute__((aligned(16))) bf16_t Bs[2][BN * BK];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave - wm * WGN;
   const int64_t z = blockIdx.z;
   const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
   int tm, tn;
   map_tile(blockIdx.x, p, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t M = p.M, N = p.N, K = p.K;
+  const int64_t K = p.K;
 
-  // Per-thread source rows (clamped rows are computed but never stored) and LDS slots.
-  const bf16_t* a_src[A_CH];
-  const bf16_t* b_src[B_CH];
-  int a_dst[A_CH], b_dst[B_CH], a_col[A_CH], b_col[B_CH];
+  // Uniform tile bases plus 32-bit per-pass element offsets (rows past M or N are clamped
+  // to the last row: computed, never stored). Every pass shares one LDS swizzle slot
+  // because RPP is a multiple of 8.
+  const bf16_t* Ab = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i + m0 * p.lda;
+  const bf16_t* Bb = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i + n0 * p.ldb;
+  const int lr = tid >> 3, lc = tid & 7;
+  const int slot = lr * BK + ((lc ^ (lr & 7)) << 3);
+  uint32_t a_off[A_CH], b_off[B_CH];
   {
-    const bf16_t* A = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i;
-    const bf16_t* B = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i;
+    const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
+    const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      a_src[i] = A + min(m0 + r, M - 1) * p.lda + c * 8;
-      a_col[i] = c * 8;
-      a_dst[i] = r * BK + ((c ^ (r & 7)) << 3);
-    }
+    for (int i = 0; i < A_CH; ++i) a_off[i] = (uint32_t)(min(i * RPP + lr, a_last) * p.lda + lc * 8);
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      b_src[i] = B + min(n0 + r, N - 1) * p.ldb + c * 8;
-      b_col[i] = c * 8;
-      b_dst[i] = r * BK + ((c ^ (r & 7)) << 3);
-    }
+    for (int i = 0; i < B_CH; ++i) b_off[i] = (uint32_t)(min(i * RPP + lr, b_last) * p.ldb + lc * 8);
   }
   uint4 ra[A_CH], rb[B_CH];
   auto load_tile = [&](int64_t k0) {
+    const bf16_t* a = Ab + k0;
+    const bf16_t* b = Bb + k0;
     if (k0 + BK <= K) {
 #pragma unroll
-      for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(a_src[i] + k0);
+      for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(a + a_off[i]);
 #pragma unroll
-      for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const uint4*>(b_src[i] + k0);
+      for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const uint4*>(b + b_off[i]);
     } else {  // K tail: K % 8 == 0, so a chunk is either fully inside K or fully outside
+      const bool in = k0 + lc * 8 < K;
 #pragma unroll
       for (int i = 0; i < A_CH; ++i)
-        ra[i] = k0 + a_col[i] < K ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : make_uint4(0, 0, 0, 0);
+        ra[i] = in ? *reinterpret_cast<const uint4*>(a + a_off[i]) : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int i = 0; i < B_CH; ++i)
-        rb[i] = k0 + b_col[i] < K ? *reinterpret_cast<const uint4*>(b_src[i] + k0) : make_uint4(0, 0, 0, 0);
+        rb[i] = in ? *reinterpret_cast<const uint4*>(b + b_off[i]) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<uint4*>(&As[buf][a_dst[i]]) = ra[i];
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<uint4*>(&As[buf][slot + i * RPP * BK]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<uint4*>(&Bs[buf][b_dst[i]]) = rb[i];
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<uint4*>(&Bs[buf][slot + i * RPP * BK]) = rb[i];
   };
 
   f32x4 acc[TM][TN];
@@ -207,23 +222,21 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
   store_tile(0);
   __syncthreads();
   const int fr = lane & 15, fc = lane >> 4;
+  // fragment rows are fr + multiples of 16, so their swizzle depends on fr only
+  const int a_frag = (wm * WM + fr) * BK, b_frag = (wn * WN + fr) * BK;
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) load_tile((int64_t)(kt + 1) * BK);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      const int c = s * 4 + fc;
+      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
       bf16x8 af[TM], bfr[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WM + i * 16 + fr;
-        af[i] = *reinterpret_cast<const bf16x8*>(&As[cur][r * BK + ((c ^ (r & 7)) << 3)]);
-      }
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&As[cur][a_frag + i * 16 * BK + sw]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WN + j * 16 + fr;
-        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[cur][r * BK + ((c ^ (r & 7)) << 3)]);
-      }
+      for (int j = 0; j < TN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(&Bs[cur][b_frag + j * 16 * BK + sw]);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -234,6 +247,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
     __syncthreads();
   }
 
+  const GemmParams e = late_params();
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -241,7 +255,140 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmParams p) {
       const int64_t m = m0 + wm * WM + i * 16 + fr;
       const int64_t n = n0 + wn * WN + j * 16 + 4 * fc;
       float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      epilogue4<bf16_t, TO>(p, zo, zi, m, n, v);
+      epilogue4<bf16_t, TO>(e, zo, zi, m, n, v);
+    }
+}
+
+// gemm_dma_kernel: same tiling and epilogue as gemm_mfma_kernel, for K % 64 == 0. Operand
+// tiles move from global memory straight into LDS (global_load_lds_dwordx4: each lane of a
+// wave writes its 16 bytes at LDS base + 16 * lane), so the pipeline can run STAGES - 1
+// K steps ahead without holding any registers for them. Loaded memory latency on MI355X is
+// a few K steps of MFMA work, which a one-step register prefetch cannot cover. Each stage
+// is a separate LDS array and the K loop is unrolled over the stages, so the compiler's
+// wait counters can tell the stage being read from the stages being filled. Before reading
+// a stage a wave waits until only the later stages' loads are outstanding (vmcnt counts
+// its own loads in issue order) and its LDS reads are done, then meets the other waves at
+// a barrier. A load group is 8 tile rows x 8 chunks = 1 KB: lane l fills row l / 8, slot
+// l % 8, which holds logical chunk (l % 8) ^ (row % 8), the XOR swizzle the fragment
+// reads undo.
+// One global_load_lds_dwordx4 through inline asm: the compiler does not track these loads,
+// so it adds no wait of its own before reading the other stages (it cannot tell the stage
+// arrays apart and would drain every load in flight); the kernel orders them with
+// dma_stage_sync. M0 (the LDS base of the 64 lanes' 16-byte slots) is saved and restored.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+__device__ __forceinline__ void dma_load16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void dma_stage_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void gemm_dma_kernel(GemmParams p) {
+  constexpr int NW = WGM * WGN, BK = 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+  constexpr int GA = BM / 8, GB = BN / 8, L = (GA + GB) / NW;  // 1 KB groups per wave
+  static_assert((GA + GB) % NW == 0 && TM >= 1 && TN >= 1, "bad tile/wave split");
+  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 stages");
+  static_assert(L * (STAGES - 2) <= 63, "vmcnt range");
+  constexpr int SZ = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) bf16_t S0[SZ];
+  __shared__ __attribute__((aligned(16))) bf16_t S1[SZ];
+  __shared__ __attribute__((aligned(16))) bf16_t S2[STAGES > 2 ? SZ : 8];
+  auto stage = [&](int i) -> bf16_t* { return i == 0 ? S0 : (i == 1 ? S1 : S2); };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave - wm * WGN;
+  const int64_t z = blockIdx.z;
+  const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
+  int tm, tn;
+  map_tile(blockIdx.x, p, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const bf16_t* Ab = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i + m0 * p.lda;
+  const bf16_t* Bb = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i + n0 * p.ldb;
+  uint32_t off[L];
+  {
+    const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
+    const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
+    const int rin = lane >> 3, c = (lane & 7) ^ rin;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int g = wave * L + j;
+      off[j] = g < GA ? (uint32_t)(min(8 * g + rin, a_last) * p.lda + c * 8)
+                      : (uint32_t)(min(8 * (g - GA) + rin, b_last) * p.ldb + c * 8);
+    }
+  }
+  auto issue = [&](bf16_t* S, int64_t k0) {
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int g = wave * L + j;
+      const bf16_t* src = (g < GA ? Ab : Bb) + k0 + off[j];
+      dma_load16(src, lds_offset(S + g * 512));
+    }
+  };
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int fr = lane & 15, fc = lane >> 4;
+  const int a_frag = (wm * WM + fr) * BK, b_frag = BM * BK + (wn * WN + fr) * BK;
+  auto compute = [&](const bf16_t* S) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
+      bf16x8 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + sw]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + sw]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const int nk = (int)(p.K / BK);
+#pragma unroll
+  for (int i = 0; i < STAGES - 1; ++i)
+    if (i < nk) issue(stage(i), (int64_t)i * BK);
+  for (int kt = 0; kt < nk; kt += STAGES) {
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u) {
+      const int t = kt + u;
+      if (t >= nk) break;
+      // tiles t+1 .. t+STAGES-2 may stay in flight
+      if (STAGES == 3 && t + 1 < nk) dma_stage_sync<L * (STAGES - 2)>();
+      else dma_stage_sync<0>();
+      if (t + STAGES - 1 < nk) issue(stage((u + STAGES - 1) % STAGES), (int64_t)(t + STAGES - 1) * BK);
+      compute(stage(u));
+    }
+  }
+
+  const GemmParams e = late_params();
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t m = m0 + wm * WM + i * 16 + fr;
+      const int64_t n = n0 + wn * WN + j * 16 + 4 * fc;
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      epilogue4<bf16_t, TO>(e, zo, zi, m, n, v);
     }
 }
 
@@ -300,19 +447,26 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 struct TileShape {
-  int bm, bn, per_cu;  // workgroups of this shape that fit on one CU (LDS / registers)
+  int bm, bn, threads;
 };
-static const TileShape kTiles[] = {
-    {0, 0, 0}, {256, 256, 1}, {256, 128, 1}, {128, 128, 2}, {128, 64, 3}, {64, 64, 4}};
+static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 256},
+                                   {128, 128, 256}, {128, 64, 256},  {64, 64, 256},
+                                   {256, 256, 256}, {256, 128, 512}, {128, 128, 256},
+                                   {256, 128, 512}, {128, 64, 256},  {128, 128, 256}};
 
-// Tile choice, from a sweep of the five GPT-2-small GEMMs (M = 8192) on an MI355X:
-// 128x128 wins when the grid is many waves of CUs deep (LM head: 580 TFLOP/s against 459
-// for 128x64), 128x64 otherwise (QKV, FFN1, and the N = 768 projections), 64x64 when
-// even 128x64 leaves CUs idle. The 256-wide tiles are reachable through the hint only.
-static int choose_tile(int64_t M, int64_t N, int64_t batch, int cus) {
+// Tile choice, from sweeps of the five GPT-2-small GEMMs (M = 8192) on an MI355X
+// (TFLOP/s): the LM head (N = 50257) runs best as 8-wave 256x128 direct-to-LDS tiles with
+// 3 stages (707 vs 642 for 128x128); QKV, FFN1 and FFN2 as 2-stage direct-to-LDS 128x128
+// (393 / 402 / 594); the short-K N = 768 out-projection as 128x64 register-prefetch tiles
+// (283), whose 3 tiles per CU balance better than 1.5. The direct-to-LDS kernels need
+// K % 64 == 0; 64x64 covers grids too small to fill the GPU.
+static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
   const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
   const int64_t t64 = ((M + 127) / 128) * ((N + 63) / 64) * batch;
+  const bool dma = K % 64 == 0;
+  if (dma && t128 >= 16LL * cus) return TL_TILE_DMA_256x128_W8;
   if (t128 >= 16LL * cus) return TL_TILE_128x128;
+  if (dma && t128 >= cus && !(t128 < 2LL * cus && K <= 1024)) return TL_TILE_DMA_128x128;
   if (t64 >= (int64_t)cus) return TL_TILE_128x64;
   return TL_TILE_64x64;
 }
@@ -320,11 +474,17 @@ static int choose_tile(int64_t M, int64_t N, int64_t batch, int cus) {
 template <typename TO>
 static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
   switch (tile) {
-    case TL_TILE_256x256: gemm_mfma_kernel<TO, 256, 256><<<grid, 256, 0, st>>>(p); break;
-    case TL_TILE_256x128: gemm_mfma_kernel<TO, 256, 128><<<grid, 256, 0, st>>>(p); break;
-    case TL_TILE_128x128: gemm_mfma_kernel<TO, 128, 128><<<grid, 256, 0, st>>>(p); break;
-    case TL_TILE_128x64: gemm_mfma_kernel<TO, 128, 64><<<grid, 256, 0, st>>>(p); break;
-    default: gemm_mfma_kernel<TO, 64, 64><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_256x256: gemm_mfma_kernel<TO, 256, 256, 2, 4><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_256x128: gemm_mfma_kernel<TO, 256, 128, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_128x128: gemm_mfma_kernel<TO, 128, 128, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_128x64: gemm_mfma_kernel<TO, 128, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_256x256_W4: gemm_mfma_kernel<TO, 256, 256, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_256x128_W8: gemm_mfma_kernel<TO, 256, 128, 4, 2><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_DMA_128x128: gemm_dma_kernel<TO, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_DMA_256x128_W8: gemm_dma_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_DMA_128x64_S3: gemm_dma_kernel<TO, 128, 64, 2, 2, 2, 3><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_DMA_128x128_S3: gemm_dma_kernel<TO, 128, 128, 2, 2, 1, 3><<<grid, 256, 0, st>>>(p); break;
+    default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
   }
 }
 
@@ -344,7 +504,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_64x64, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_128x128_S3, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -380,7 +540,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   const size_t eo = dtype_size(d->dtype_out);
   p.vec_store = !qkv && d->ldc % 4 == 0 && ((uintptr_t)d->C % (4 * eo)) == 0 &&
                 d->sc_o % 4 == 0 && d->sc_i % 4 == 0;
-  p.group_m = 8;
+  p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
 
   // The MFMA kernel streams 16-byte rows of A and Bt: K-contiguous, 8-element aligned.
   const bool mfma = d->dtype_in == TL_BF16 && d->b_layout == TL_B_NK && d->K % 8 == 0 &&
@@ -395,7 +555,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
   const bool f32out = d->dtype_out == TL_F32;
   if (mfma) {
-    const int tile = d->tile ? d->tile : choose_tile(d->M, d->N, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
+    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
+    if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
     const TileShape& s = kTiles[tile];
     p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
     p.tiles_n = (int)((d->N + s.bn - 1) / s.bn);

@@ -1,6 +1,7 @@
 // libtl runtime: context, errors, caching allocator, copies, events and the per-launch
 // event profiler. One in-order HIP stream per context; every op is enqueued on it.
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
 
 #include "tl_internal.hpp"
@@ -144,6 +145,7 @@ int tl_init(int device, tl_ctx** out) {
   tl_ctx* ctx = new tl_ctx();
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
+  if (const char* g = std::getenv("TL_GEMM_GROUP_M")) ctx->gemm_group_m = std::atoi(g);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

@@ -49,6 +49,7 @@ struct tl_ctx {
   std::vector<tl::KprofRecord> kprof_pending;
   tl::KprofTotals kprof_totals[TL_KF_COUNT];
   int num_cus = 0;
+  int gemm_group_m = 0;  // tile-rows per group in the GEMM tile order (TL_GEMM_GROUP_M)
 };
 
 namespace tl {
