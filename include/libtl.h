@@ -72,7 +72,10 @@ enum tl_gemm_tile {
   TL_TILE_DMA_128x128 = 8,     /* 2 stages */
   TL_TILE_DMA_256x128_W8 = 9,  /* 8 waves, 3 stages */
   TL_TILE_DMA_128x64_S3 = 10,  /* 3 stages */
-  TL_TILE_DMA_128x128_S3 = 11  /* 3 stages */
+  TL_TILE_DMA_128x128_S3 = 11, /* 3 stages */
+  /* persistent direct-to-LDS variants (one workgroup per resident slot; batch 1) */
+  TL_TILE_PERSIST_256x128_W8 = 12,
+  TL_TILE_PERSIST_128x128 = 13
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

@@ -22,6 +22,24 @@
 
 namespace tl {
 
+// Division by a run-time invariant d with a multiply-high and a shift (the round-up
+// method of Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): s = ceil(log2 d), mul = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, mul) + n) >> s for 0 <= n < 2^31.
+struct FastDiv {
+  uint32_t mul, shr;
+};
+static inline FastDiv make_fastdiv(uint32_t d) {
+  if (d <= 1) return FastDiv{0u, 0u};
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t mul = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{(uint32_t)mul, s};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.mul) + n) >> f.shr;
+}
+
 struct GemmParams {
   const void* A;
   const void* B;
@@ -42,6 +60,7 @@ struct GemmParams {
   void* vt;
   int T, Hq, Hkv, Dh;
   int tiles_m, tiles_n, group_m;
+  FastDiv div_T, div_Dh;
 };
 
 // Applies the epilogue to 4 consecutive columns n0..n0+3 of row m and stores them.
@@ -131,13 +150,117 @@ __device__ __forceinline__ GemmParams late_params() {
   return e;
 }
 
-// Block id -> output tile (tm, tn): XCD-contiguous runs, then groups of group_m tile-rows
-// walked row-fastest.
-__device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, int& tn) {
-  const int ntiles = p.tiles_m * p.tiles_n;
-  const int x = bid & 7, local = bid >> 3;
-  const int q = ntiles >> 3, r = ntiles & 7;
-  const int i = x * q + min(x, r) + local;
+// Epilogue of an MFMA accumulator block: acc[i][j] holds rows mb + 16 i and columns
+// nb + 16 j .. +3 of this lane. Bias is loaded once per column fragment, 64-bit row
+// addresses once per row, and the head scatter splits rows (batch, time) and columns
+// (part, head, d) with one fast division each.
+template <typename TO, int TM, int TN>
+__device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, int64_t zi,
+                                              int64_t mb, int64_t nb, f32x4 (&acc)[TM][TN]) {
+  int cnt[TN];
+  float bias[TN][4];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t n = nb + 16 * j;
+    cnt[j] = n >= e.N ? 0 : (e.N - n >= 4 ? 4 : (int)(e.N - n));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      bias[j][q] = (e.bias && q < cnt[j]) ? bf2f(((const bf16_t*)e.bias)[n + q]) : 0.f;
+  }
+  auto finish = [&](float (&v)[4], int j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (e.divisor != 1.0f) v[q] = v[q] / e.divisor;
+      v[q] = v[q] + bias[j][q];
+      if (e.act != TL_ACT_NONE) v[q] = apply_act(v[q], e.act);
+    }
+  };
+  if (e.qkv) {
+    // column split, once per fragment: part (Q, K or V), head h, offset d
+    const int qw = e.Hq * e.Dh, kw = e.Hkv * e.Dh;
+    TO* cbase[TN];
+    int part[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = (int)(nb + 16 * j);
+      part[j] = n < qw ? 0 : (n < qw + kw ? 1 : 2);
+      const int nn = n - (part[j] == 0 ? 0 : (part[j] == 1 ? qw : qw + kw));
+      const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
+      cbase[j] = part[j] == 0 ? (TO*)e.q + ((int64_t)h * e.T) * e.Dh + d
+               : part[j] == 1 ? (TO*)e.k + ((int64_t)h * e.T) * e.Dh + d
+                              : (TO*)e.vt + ((int64_t)h * e.Dh + d) * e.T;
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = mb + 16 * i;
+      if (m >= e.M) continue;
+      const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
+      const int64_t rq = ((int64_t)b * e.Hq * e.T + t) * e.Dh;
+      const int64_t rk = ((int64_t)b * e.Hkv * e.T + t) * e.Dh;
+      const int64_t rv = (int64_t)b * e.Hkv * e.Dh * e.T + t;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (cnt[j] == 0) continue;
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        finish(v, j);
+        if (part[j] < 2) {
+          TO* dst = cbase[j] + (part[j] == 0 ? rq : rk);
+          if (sizeof(TO) == 2) {
+            uint2 w;
+            w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+            w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+            *reinterpret_cast<uint2*>(dst) = w;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + q, v[q]);
+          }
+        } else {
+          TO* dst = cbase[j] + rv;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + (int64_t)q * e.T, v[q]);
+        }
+      }
+    }
+    return;
+  }
+  TO* cz = (TO*)e.C + zo * e.sc_o + zi * e.sc_i;
+  const TO* rz = e.res ? (const TO*)e.res + zo * e.sr_o + zi * e.sr_i : nullptr;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t m = mb + 16 * i;
+    if (m >= e.M) continue;
+    TO* crow = cz + m * e.ldc + nb;
+    const TO* rrow = rz ? rz + m * e.ldr + nb : nullptr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if (cnt[j] == 0) continue;
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      finish(v, j);
+      if (rrow) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (q < cnt[j]) v[q] = v[q] + Elem<TO>::load(rrow + 16 * j + q);
+      }
+      TO* c = crow + 16 * j;
+      if (cnt[j] == 4 && e.vec_store) {
+        if (sizeof(TO) == 4) {
+          *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          uint2 w;
+          w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+          w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+          *reinterpret_cast<uint2*>(c) = w;
+        }
+      } else {
+        for (int q = 0; q < cnt[j]; ++q) Elem<TO>::store(c + q, v[q]);
+      }
+    }
+  }
+}
+
+// Position i of the grouped tile order -> output tile (tm, tn): groups of group_m
+// tile-rows, walked row-fastest.
+__device__ __forceinline__ void grouped_tile(int i, const GemmParams& p, int& tm, int& tn) {
   const int per_group = p.group_m * p.tiles_n;
   const int g = i / per_group;
   const int first_m = g * p.group_m;
@@ -145,6 +268,16 @@ __device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, 
   const int k = i - g * per_group;
   tm = first_m + k % gm;
   tn = k / gm;
+}
+
+// Block id -> output tile: workgroups are dispatched round-robin over the 8 XCDs, so XCD x
+// runs blocks x, x+8, ...; give it the contiguous run [x q + min(x, r), ...) of the
+// grouped order.
+__device__ __forceinline__ void map_tile(int bid, const GemmParams& p, int& tm, int& tn) {
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int x = bid & 7, local = bid >> 3;
+  const int q = ntiles >> 3, r = ntiles & 7;
+  grouped_tile(x * q + min(x, r) + local, p, tm, tn);
 }
 
 template <typename TO, int BM, int BN, int WGM, int WGN>
@@ -248,15 +381,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
   }
 
   const GemmParams e = late_params();
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t m = m0 + wm * WM + i * 16 + fr;
-      const int64_t n = n0 + wn * WN + j * 16 + 4 * fc;
-      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      epilogue4<bf16_t, TO>(e, zo, zi, m, n, v);
-    }
+  mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
 }
 
 // gemm_dma_kernel: same tiling and epilogue as gemm_mfma_kernel, for K % 64 == 0. Operand
@@ -346,21 +471,32 @@ void gemm_dma_kernel(GemmParams p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, fc = lane >> 4;
   const int a_frag = (wm * WM + fr) * BK, b_frag = BM * BK + (wn * WN + fr) * BK;
+  // Both 32-wide K halves' fragments are read before the first MFMA when the wave tile is
+  // small enough (their LDS latency then overlaps the first half's MFMAs); larger wave
+  // tiles read and consume one half at a time to bound register use.
   auto compute = [&](const bf16_t* S) {
+    constexpr bool kBoth = TM * TN <= 16;
+    bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
-      bf16x8 af[TM], bfr[TN];
+      if (s == 0 || !kBoth) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + sw]);
+        for (int h = s; h < (kBoth ? 2 : s + 1); ++h) {
+          const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + sw]);
+          for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
+        }
+      }
+      (void)sw;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s][j], af[s][i], acc[i][j], 0, 0, 0);
+      if (!kBoth) __builtin_amdgcn_sched_barrier(0);
     }
   };
   const int nk = (int)(p.K / BK);
@@ -381,15 +517,122 @@ void gemm_dma_kernel(GemmParams p) {
   }
 
   const GemmParams e = late_params();
+  mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
+}
+
+// gemm_dma_persistent_kernel: gemm_dma_kernel with one workgroup per resident slot
+// (gridDim.x = CUs x workgroups per CU, a multiple of 8). Workgroup b runs on XCD b % 8 and
+// walks that XCD's contiguous run of the grouped tile order with stride gridDim.x / 8.
+// Its K steps form one flattened pipeline across its tiles: the first steps of the next
+// tile are loaded while the current tile finishes and stores its epilogue, so a short K
+// loop (12 steps at K = 768) no longer pays the load latency once per tile. Batch == 1.
+template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void gemm_dma_persistent_kernel(GemmParams p) {
+  constexpr int NW = WGM * WGN, BK = 64;
+  constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
+  constexpr int GA = BM / 8, GB = BN / 8, L = (GA + GB) / NW;
+  static_assert((GA + GB) % NW == 0 && TM >= 1 && TN >= 1, "bad tile/wave split");
+  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 stages");
+  constexpr int SZ = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) bf16_t S0[SZ];
+  __shared__ __attribute__((aligned(16))) bf16_t S1[SZ];
+  __shared__ __attribute__((aligned(16))) bf16_t S2[STAGES > 2 ? SZ : 8];
+  auto stage = [&](int i) -> bf16_t* { return i == 0 ? S0 : (i == 1 ? S1 : S2); };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave - wm * WGN;
+  const int ntiles = p.tiles_m * p.tiles_n;
+  const int bid = blockIdx.x, x = bid & 7, lb = bid >> 3, per_x = (int)gridDim.x >> 3;
+  const int q = ntiles >> 3, r = ntiles & 7;
+  const int cs = x * q + min(x, r), cn = q + (x < r ? 1 : 0);
+  const int my_tiles = lb < cn ? (cn - lb + per_x - 1) / per_x : 0;
+  const int nk = (int)(p.K / BK);
+  const int total = my_tiles * nk;
+  auto tile_origin = [&](int rr, int64_t& m0, int64_t& n0) {
+    int tm, tn;
+    grouped_tile(cs + lb + rr * per_x, p, tm, tn);
+    m0 = (int64_t)tm * BM;
+    n0 = (int64_t)tn * BN;
+  };
+  const int rin = lane >> 3, cch = (lane & 7) ^ rin;
+  auto issue_step = [&](bf16_t* S, int h) {
+    const int rr = h / nk, kk = h - rr * nk;
+    int64_t m0, n0;
+    tile_origin(rr, m0, n0);
+    const bf16_t* Ab = (const bf16_t*)p.A + m0 * p.lda + (int64_t)kk * BK;
+    const bf16_t* Bb = (const bf16_t*)p.B + n0 * p.ldb + (int64_t)kk * BK;
+    const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
+    const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int g = wave * L + j;
+      const bf16_t* src = g < GA ? Ab + min(8 * g + rin, a_last) * p.lda + cch * 8
+                                 : Bb + min(8 * (g - GA) + rin, b_last) * p.ldb + cch * 8;
+      dma_load16(src, lds_offset(S + g * 512));
+    }
+  };
+  f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t m = m0 + wm * WM + i * 16 + fr;
-      const int64_t n = n0 + wn * WN + j * 16 + 4 * fc;
-      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      epilogue4<bf16_t, TO>(e, zo, zi, m, n, v);
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int fr = lane & 15, fc = lane >> 4;
+  const int a_frag = (wm * WM + fr) * BK, b_frag = BM * BK + (wn * WN + fr) * BK;
+  // Both 32-wide K halves' fragments are read before the first MFMA when the wave tile is
+  // small enough (their LDS latency then overlaps the first half's MFMAs); larger wave
+  // tiles read and consume one half at a time to bound register use.
+  auto compute = [&](const bf16_t* S) {
+    constexpr bool kBoth = TM * TN <= 16;
+    bf16x8 af[2][TM], bfr[2][TN];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
+      if (s == 0 || !kBoth) {
+#pragma unroll
+        for (int h = s; h < (kBoth ? 2 : s + 1); ++h) {
+          const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
+#pragma unroll
+          for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
+        }
+      }
+      (void)sw;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s][j], af[s][i], acc[i][j], 0, 0, 0);
+      if (!kBoth) __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  auto finish_tile = [&](int rr) {
+    int64_t m0, n0;
+    tile_origin(rr, m0, n0);
+    const GemmParams e = late_params();
+    mfma_epilogue<TO, TM, TN>(e, 0, 0, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+#pragma unroll
+  for (int i = 0; i < STAGES - 1; ++i)
+    if (i < total) issue_step(stage(i), i);
+  for (int g0 = 0; g0 < total; g0 += STAGES) {
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u) {
+      const int g = g0 + u;
+      if (g >= total) break;
+      if (STAGES == 3 && g + 1 < total) dma_stage_sync<L * (STAGES - 2)>();
+      else dma_stage_sync<0>();
+      if (g + STAGES - 1 < total) issue_step(stage((u + STAGES - 1) % STAGES), g + STAGES - 1);
+      compute(stage(u));
+      if ((g + 1) % nk == 0) finish_tile(g / nk);
+    }
+  }
 }
 
 template <typename TI, typename TO>
@@ -452,7 +695,10 @@ struct TileShape {
 static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 256},
                                    {128, 128, 256}, {128, 64, 256},  {64, 64, 256},
                                    {256, 256, 256}, {256, 128, 512}, {128, 128, 256},
-                                   {256, 128, 512}, {128, 64, 256},  {128, 128, 256}};
+                                   {256, 128, 512}, {128, 64, 256},  {128, 128, 256},
+                                   {256, 128, 512}, {128, 128, 256}};
+// resident workgroups per CU of the persistent variants (LDS: 144 KB and 64 KB)
+static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_256x128_W8 ? 1 : 2; }
 
 // Tile choice, from sweeps of the five GPT-2-small GEMMs (M = 8192) on an MI355X
 // (TFLOP/s): the LM head (N = 50257) runs best as 8-wave 256x128 direct-to-LDS tiles with
@@ -484,6 +730,8 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
     case TL_TILE_DMA_256x128_W8: gemm_dma_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_DMA_128x64_S3: gemm_dma_kernel<TO, 128, 64, 2, 2, 2, 3><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_128x128_S3: gemm_dma_kernel<TO, 128, 128, 2, 2, 1, 3><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_PERSIST_256x128_W8: gemm_dma_persistent_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_PERSIST_128x128: gemm_dma_persistent_kernel<TO, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
   }
 }
@@ -504,7 +752,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_128x128_S3, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_PERSIST_128x128, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -541,6 +789,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.vec_store = !qkv && d->ldc % 4 == 0 && ((uintptr_t)d->C % (4 * eo)) == 0 &&
                 d->sc_o % 4 == 0 && d->sc_i % 4 == 0;
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
+  p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
+  p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
 
   // The MFMA kernel streams 16-byte rows of A and Bt: K-contiguous, 8-element aligned.
   const bool mfma = d->dtype_in == TL_BF16 && d->b_layout == TL_B_NK && d->K % 8 == 0 &&
@@ -557,11 +807,19 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (mfma) {
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
+    const bool persistent = tile >= TL_TILE_PERSIST_256x128_W8;
+    if (persistent && batch != 1) tile = tile == TL_TILE_PERSIST_128x128 ? TL_TILE_DMA_128x128 : TL_TILE_DMA_256x128_W8;
     const TileShape& s = kTiles[tile];
     p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
     p.tiles_n = (int)((d->N + s.bn - 1) / s.bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+    if (tile >= TL_TILE_PERSIST_256x128_W8) {
+      const int64_t slots = (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * persistent_per_cu(tile);
+      const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
+      grid.x = (unsigned)(std::min(slots, (ntiles + 7) / 8 * 8) / 8 * 8);
+      if (grid.x == 0) grid.x = 8;
+    }
     LaunchScope ls(ctx, family, flops, bytes);
     if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
     else launch_mfma<bf16_t>(tile, grid, ctx->stream, p);

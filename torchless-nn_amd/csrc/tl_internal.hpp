@@ -166,18 +166,23 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// (1 + tanh(u)) / 2 == 1 / (1 + exp(-2u)): both activations below are evaluated in this
+// logistic form with the hardware exp2 and reciprocal (one transcendental each) instead of
+// a tanh routine; the two forms are equal in exact arithmetic and differ by a few fp32 ulps
+// of the result. exp2 overflow to +inf gives 0 and underflow to 0 gives x, the limits.
+__device__ __forceinline__ float logistic_times(float x, float two_u) {
+  const float e = __builtin_amdgcn_exp2f(-two_u * 1.4426950408889634f);
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
 // tanh-approximation GeLU, reference activations.py:24-28:
 //   0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
 __device__ __forceinline__ float gelu_tanh(float x) {
   const float k = 0.7978845608028654f;  // sqrt(2/pi) rounded to fp32
-  float t = tanhf(k * (x + 0.044715f * (x * x * x)));
-  return 0.5f * x * (1.0f + t);
+  const float u = k * (x + 0.044715f * (x * x * x));
+  return logistic_times(x, 2.0f * u);
 }
 // SiLU through tanh, reference activations.py:41-45: x * (1 + tanh(x/2)) / 2
-__device__ __forceinline__ float silu_tanh(float x) {
-  float s = (1.0f + tanhf(x * 0.5f)) * 0.5f;
-  return x * s;
-}
+__device__ __forceinline__ float silu_tanh(float x) { return logistic_times(x, x); }
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == TL_ACT_GELU) return gelu_tanh(v);
   if (act == TL_ACT_SILU) return silu_tanh(v);
