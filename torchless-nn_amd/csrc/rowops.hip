@@ -375,6 +375,82 @@ __global__ __launch_bounds__(NT) void softmax_block_kernel(const T* __restrict__
   }
 }
 
+// Long rows (vocabulary softmax): 256 threads per row keep the row as packed 16-byte
+// chunks (raw bf16 or fp32 bits, 4 registers per chunk) instead of unpacked floats, so
+// several rows fit per CU and one row's loads overlap another's reductions and stores.
+// A partial last chunk is padded with -inf; exp is evaluated again in the output pass.
+template <typename T>
+__device__ __forceinline__ uint4 neg_inf_chunk() {
+  return sizeof(T) == 2 ? make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u)
+                        : make_uint4(0xFF800000u, 0xFF800000u, 0xFF800000u, 0xFF800000u);
+}
+
+template <typename T, int NT, int CH>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 1024 ? 4 : 3, 8)))
+void softmax_rowreg_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
+                           int64_t ldx, int64_t ldy, float temp) {
+  constexpr int VW = Elem<T>::kVec;
+  __shared__ float red[NT / 64];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  uint4 raw[CH];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * NT + threadIdx.x) * VW;
+    if (col + VW <= cols) {
+      raw[c] = *reinterpret_cast<const uint4*>(xr + col);
+    } else if (col < cols) {
+      float t[VW];
+#pragma unroll
+      for (int e = 0; e < VW; ++e) t[e] = col + e < cols ? Elem<T>::load(xr + col + e) : -INFINITY;
+      raw[c] = Elem<T>::pack(t);
+    } else {
+      raw[c] = neg_inf_chunk<T>();
+    }
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[e]);
+  }
+  // The empty asm makes the packed chunks opaque between passes, so each pass unpacks
+  // them again instead of keeping every unpacked float live (which would spill).
+  auto opaque = [&]() {
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+      asm volatile("" : "+v"(raw[c].x), "+v"(raw[c].y), "+v"(raw[c].z), "+v"(raw[c].w));
+  };
+  mx = block_reduce<NT>(mx, true, red);
+  opaque();
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) s += softmax_exp(v[e] - mx, temp);
+  }
+  const float r = 1.0f / block_reduce<NT>(s, false, red);
+  opaque();
+  T* yr = y + row * ldy;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * NT + threadIdx.x) * VW;
+    if (col >= cols) continue;
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) v[e] = softmax_exp(v[e] - mx, temp) * r;
+    if (col + VW <= cols) {
+      store_chunk(yr + col, v);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e)
+        if (col + e < cols) Elem<T>::store(yr + col + e, v[e]);
+    }
+  }
+}
+
 // Any shape: one workgroup per row; pass 1 keeps a running (max, sum), pass 2 writes.
 template <typename T, bool CAUSAL>
 __global__ __launch_bounds__(256) void softmax_generic_kernel(const T* x, T* y, int64_t rows,
@@ -628,13 +704,30 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
     softmax_block_kernel<T, 1024, CH, CAUSAL><<<(unsigned)rows, 1024, 0, ctx->stream>>>(
         (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
   };
+  auto rowreg = [&](auto nt_tag, auto ch_tag) {
+    constexpr int NT = decltype(nt_tag)::value, CH = decltype(ch_tag)::value;
+    softmax_rowreg_kernel<T, NT, CH><<<(unsigned)rows, NT, 0, ctx->stream>>>(
+        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp);
+  };
+  using I256 = std::integral_constant<int, 256>;
+  using I512 = std::integral_constant<int, 512>;
+  using I1024 = std::integral_constant<int, 1024>;
+  using C8 = std::integral_constant<int, 8>;
+  using C16 = std::integral_constant<int, 16>;
+  using C24 = std::integral_constant<int, 24>;
+  constexpr bool bf = sizeof(T) == 2;  // fp32 spills at 24 chunks per thread or 1024 threads
   if (vec && chunks <= 64) wave(std::integral_constant<int, 1>());
   else if (vec && chunks <= 128) wave(std::integral_constant<int, 2>());
   else if (vec && chunks <= 256) wave(std::integral_constant<int, 4>());
   else if (vec && chunks <= 512) wave(std::integral_constant<int, 8>());
+  else if (vec && !CAUSAL && chunks <= 256 * 8) rowreg(I256(), C8());
+  else if (vec && !CAUSAL && chunks <= 256 * 16) rowreg(I256(), C16());
+  else if (vec && !CAUSAL && bf && chunks <= 256 * 24) rowreg(I256(), C24());
+  else if (vec && !CAUSAL && chunks <= 512 * 16) rowreg(I512(), C16());
+  else if (vec && !CAUSAL && bf && chunks <= 512 * 24) rowreg(I512(), C24());
+  else if (vec && !CAUSAL && bf && chunks <= 1024 * 16) rowreg(I1024(), C16());
   else if (vec && chunks <= 1024 * 4) block(std::integral_constant<int, 4>());
   else if (vec && chunks <= 1024 * 8) block(std::integral_constant<int, 8>());
-  else if (vec && chunks <= 1024 * 16) block(std::integral_constant<int, 16>());
   else
     softmax_generic_kernel<T, CAUSAL><<<(unsigned)rows, 256, 0, ctx->stream>>>(
         (const T*)x, (T*)y, rows, cols, ldx, ldy, temp, period, offset);
