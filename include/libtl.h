@@ -55,7 +55,12 @@ enum tl_b_layout {
 /* Epilogue variants of tl_gemm. */
 enum tl_epilogue {
   TL_EPI_STORE = 0,     /* C[m,n] = f(acc) */
-  TL_EPI_QKV_SPLIT = 1  /* scatter [M, (Hq+2*Hkv)*Dh] into q [B,Hq,T,Dh], k [B,Hkv,T,Dh], vt [B,Hkv,Dh,T] */
+  /* scatter [M = B*T, (Hq+2*Hkv)*Dh] into q [B,Hq,T,Dh] and a key/value cache
+   * k [B,Hkv,L,Dh], vt [B,Hkv,Dh,L] (L = kv_len, rows written at kv_pos0 + t) */
+  TL_EPI_QKV_SPLIT = 1,
+  /* GeGLU: B rows interleave gate and up projections (row 2f = gate f, 2f+1 = up f);
+   * C[m, f] = gelu(acc[m, 2f]) * acc[m, 2f+1], C is [M, N/2] */
+  TL_EPI_GEGLU = 2
 };
 
 /* Output tile shapes (rows x columns) of the bf16 MFMA GEMM, for tl_gemm_desc.tile. */
@@ -116,6 +121,7 @@ typedef struct tl_gemm_desc {
   int32_t epilogue;                     /* enum tl_epilogue */
   void* q; void* k; void* vt;           /* TL_EPI_QKV_SPLIT outputs */
   int64_t seq_len, n_heads_q, n_heads_kv, head_dim;
+  int64_t kv_len, kv_pos0;              /* cache capacity (0: seq_len) and write position */
   int32_t family;                       /* enum tl_kfamily used by the profiler */
   int32_t tile;                         /* MFMA tile hint: 0 = choose automatically, else
                                            enum tl_gemm_tile */
@@ -171,12 +177,12 @@ int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
 int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype);
 
 /* ---- the hot path --------------------------------------------------------------------- */
-/* out[i, :] = table[ids[i], :] + pos[pos0 + i % seq_len, :]  (pos may be NULL).
- * Replaces GPTEmbedFront.forward (reference transformer_adapters.py:148-153). Ids outside
- * [0, vocab) zero the row and latch TL_ERR_BAD_INPUT. */
+/* out[i, :] = table[ids[i], :] * scale + pos[pos0 + i % seq_len, :]  (pos may be NULL).
+ * Replaces GPTEmbedFront.forward (reference transformer_adapters.py:148-153; scale 1 there).
+ * Ids outside [0, vocab) zero the row and latch TL_ERR_BAD_INPUT. */
 int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* table,
                  const void* pos, void* out, int64_t n_tokens, int64_t seq_len, int64_t pos0,
-                 int64_t vocab, int64_t dim, int64_t ld_out, int32_t dtype);
+                 int64_t vocab, int64_t dim, int64_t ld_out, float scale, int32_t dtype);
 /* y = (x - mean) / sqrt(var + eps) * gamma + beta per row (population variance).
  * Replaces LayerNorm.forward (reference layers.py:415-428). */
 int tl_layernorm_fwd(tl_ctx* ctx, const void* x, const void* gamma, const void* beta, void* y,
@@ -198,10 +204,11 @@ int tl_softmax_fwd(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
  * evaluated in fp64. No reference counterpart (positions are absolute there). */
 int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
                   int64_t pos0);
-/* Rotate-half RoPE over x [n_seq, T, D] (row pitch D): for i < D/2,
- * y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i+D/2] cos + x[i] sin. */
+/* Rotate-half RoPE over x [n_seq][seq_stride] holding T rows of D (row pitch D) per
+ * sequence (seq_stride = T*D when packed; a cache slice uses its capacity * D): for i < D/2,
+ * y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i+D/2] cos + x[i] sin. In place is allowed. */
 int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
-                int64_t seq_len, int64_t head_dim, int32_t dtype);
+                int64_t seq_len, int64_t head_dim, int64_t seq_stride, int32_t dtype);
 /* Replaces GeLU.forward / SiLU.forward (reference activations.py:24-28, 41-45). */
 int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype);
 /* out[r] = first index of the maximum of row r (NaN counts as the maximum), int64.
@@ -211,14 +218,16 @@ int tl_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ld
 /* Every matmul of the forward: reference layers.py:208, 286, 293, 303, 306, 372, 373,
  * transformer_adapters.py:49, 93, 176. */
 int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* desc);
-/* Fused causal attention for q [BH, T, D], k [BH/g, Tk, D], vt [BH/g, D, Tk] (g query heads
- * share one kv head): out[b, t, h*D + d] with row pitch ld_out, scores divided by
- * `divisor`; query t sits at key position t + offset. Replaces reference
- * layers.py:293-304 (scores, mask, softmax, P.V, head merge) in one kernel. */
+/* Fused causal attention for q [B, Hq, Tq, D], k [B, Hkv, Lk, D], vt [B, Hkv, D, Lk] of which
+ * the first seq_k keys are valid (Lk = kv_capacity, 0 meaning seq_k; a key/value cache
+ * beyond seq_k must hold finite values): out[b, t, h*D + d] with row pitch ld_out, scores
+ * divided by `divisor`; query head h reads kv head h / (Hq / Hkv); query t sits at key
+ * position t + offset. Replaces reference layers.py:293-304 (scores, mask, softmax, P.V,
+ * head merge) in one kernel. */
 int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, void* out,
                      int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                      int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
-                     float divisor, int32_t causal, int32_t dtype);
+                     float divisor, int32_t causal, int64_t kv_capacity, int32_t dtype);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,13 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
   rmsnorm          brute-force float64 loops; invariance to positive row scaling
   rope             complex-multiplication form, identity at position 0, pair norms
                    preserved, <R_m q, R_n k> depends only on m - n
+  geglu_ffn        brute-force float64 scalar loops at a tiny shape
+  mqa              without RoPE and with Hkv = Hq equals mha (zero biases, [Q|K|V]
+                   columns), itself pinned; Hkv = 1 equals Hkv = Hq with the key/value
+                   weights replicated per head (pins the head -> kv-head map); a cached
+                   two-call run equals one call over the whole sequence
+  gemma_forward    incremental (cached) logits equal recomputed ones; composition of the
+                   pinned pieces above; gemma_greedy ids are argmax of its own rows
   mha              brute-force per-head loops in float64 (golden fixture); permutation
                    weights pin the head split/merge order
   embed_front      brute-force gather + add
@@ -258,3 +265,115 @@ def gpt_forward(ids, params, cfg, bf16=False, return_logits=False):
     logits = r(embed_back(x, params["table"]))
     probs = r(softmax(logits))
     return (probs, logits) if return_logits else probs
+
+
+# ---- Gemma-style decoder pieces (no reference counterpart) ------------------------------
+def geglu_ffn(x, wg, wu, wd, activation="gelu", rnd=None):
+    """Gated FFN (Shazeer 2020): (act(x Wg) * (x Wu)) Wd, no biases; act is the tanh GeLU
+    of activations.py:24-28 (GeGLU) or SiLU (SwiGLU)."""
+    r = rnd or (lambda a: a)
+    x = np.asarray(x, dtype=F32)
+    h = r(act(x @ wg, activation) * (x @ wu))
+    return h @ wd
+
+
+def mqa(x, wqkv, wo, num_heads, num_kv_heads, head_dim, pos0=0, rope_base=10000.0,
+        past_k=None, past_v=None, rnd=None, use_rope=True):
+    """Multi-/grouped-query causal attention with rotate-half RoPE (Shazeer 2019; Ainslie
+    et al. 2023; Su et al. 2021). wqkv [C, (Hq + 2 Hkv) D] with columns [Q | K | V]; query
+    head h reads key/value head h // (Hq / Hkv). x holds positions pos0 .. pos0 + T - 1;
+    past_k/past_v [B, Hkv, pos0, D] are the rotated keys and values of earlier positions.
+    Returns (y, k_all, v_all) with k_all/v_all [B, Hkv, pos0 + T, D]."""
+    r = rnd or (lambda a: a)
+    x = np.asarray(x, dtype=F32)
+    B, T, C = x.shape
+    Hq, Hkv, D = num_heads, num_kv_heads, head_dim
+    if (past_k.shape[2] if past_k is not None else 0) != pos0:
+        raise ValueError("pos0 must equal the number of cached positions")
+    qkv = r(x @ wqkv)
+    q = qkv[..., : Hq * D].reshape(B, T, Hq, D).transpose(0, 2, 1, 3)
+    k = qkv[..., Hq * D: (Hq + Hkv) * D].reshape(B, T, Hkv, D).transpose(0, 2, 1, 3)
+    v = qkv[..., (Hq + Hkv) * D:].reshape(B, T, Hkv, D).transpose(0, 2, 1, 3)
+    if use_rope:
+        cos, sin = rope_table(T, D, rope_base, pos0)
+        q, k = r(rope(q, cos, sin)), r(rope(k, cos, sin))
+    if past_k is not None:
+        k = np.concatenate([past_k, k], axis=2)
+        v = np.concatenate([past_v, v], axis=2)
+    Tk = pos0 + T
+    g = Hq // Hkv
+    kk = np.repeat(k, g, axis=1)
+    vv = np.repeat(v, g, axis=1)
+    s = (q @ kk.transpose(0, 1, 3, 2)) / F32(D ** 0.5)
+    qpos = pos0 + np.arange(T)[:, None]
+    s = np.where(np.arange(Tk)[None, :] <= qpos, s, F32(-1e9)).astype(F32)
+    s = s - np.max(s, axis=-1, keepdims=True)
+    e = np.exp(s)
+    p = e / np.sum(e, axis=-1, keepdims=True)
+    heads = r(p @ vv).transpose(0, 2, 1, 3).reshape(B, T, Hq * D)
+    return heads @ wo, k, v
+
+
+def gemma_param_shapes(cfg):
+    """Parameter shapes in GemmaDecoder layer order: table, then per block [attn-norm
+    gamma, Wqkv, Wo, ffn-norm gamma, Wgate, Wup, Wdown], then the final-norm gamma."""
+    V, C, L = cfg["vocab"], cfg["d"], cfg["layers"]
+    Hq, Hkv, D, F = cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["ffn"]
+    shapes = [("table", (V, C))]
+    for l in range(L):
+        shapes += [(f"b{l}.g1", (C,)), (f"b{l}.wqkv", (C, (Hq + 2 * Hkv) * D)),
+                   (f"b{l}.wo", (Hq * D, C)), (f"b{l}.g2", (C,)), (f"b{l}.wg", (C, F)),
+                   (f"b{l}.wu", (C, F)), (f"b{l}.wd", (F, C))]
+    shapes += [("normf.g", (C,))]
+    return shapes
+
+
+def gemma_params(cfg, seed, scale=0.02, bf16=False):
+    """Seeded N(0,1)*scale in parameter order from default_rng(seed) (gammas included:
+    RMSNorm scales by 1 + gamma)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in gemma_param_shapes(cfg):
+        a = rng.standard_normal(shape, dtype=F32) * F32(scale)
+        out[name] = round_bf16(a) if bf16 else a
+    return out
+
+
+def gemma_forward(ids, params, cfg, bf16=False, pos0=0, cache=None):
+    """Logits [B, T, V] of the Gemma-style decoder for ids at positions pos0.. . `cache`
+    (a dict filled in place, layer -> (k, v)) carries rotated keys/values between calls;
+    None recomputes from scratch with pos0 = 0."""
+    rnd = round_bf16 if bf16 else None
+    r = rnd or (lambda a: a)
+    ids = np.asarray(ids)
+    C = cfg["d"]
+    x = r(params["table"][ids] * np.sqrt(F32(C)))
+    for l in range(cfg["layers"]):
+        past = cache.get(l) if cache is not None else None
+        h, k, v = mqa(r(rmsnorm(x, params[f"b{l}.g1"], F32(1e-6), 1.0)), params[f"b{l}.wqkv"],
+                      params[f"b{l}.wo"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"], pos0,
+                      cfg.get("rope_base", 10000.0), *(past or (None, None)), rnd=rnd)
+        if cache is not None:
+            cache[l] = (k, v)
+        y = r(x + h)
+        x = r(y + geglu_ffn(r(rmsnorm(y, params[f"b{l}.g2"], F32(1e-6), 1.0)), params[f"b{l}.wg"],
+                            params[f"b{l}.wu"], params[f"b{l}.wd"], "gelu", rnd))
+    x = r(rmsnorm(x, params["normf.g"], F32(1e-6), 1.0))
+    return r(embed_back(x, params["table"]))
+
+
+def gemma_greedy(ids, params, cfg, n_new, bf16=False):
+    """Greedy decoding by recomputation (the reference's generate loop, demo.ipynb:1526-1533,
+    with argmax in place of sampling): each step reruns the whole sequence and appends
+    argmax of the last logits row. Returns (new ids [B, n_new], last-row logits
+    [n_new, B, V])."""
+    seq = np.asarray(ids)
+    new, rows = [], []
+    for _ in range(n_new):
+        logits = gemma_forward(seq, params, cfg, bf16)
+        last = logits[:, -1, :]
+        nxt = argmax(last)
+        new.append(nxt)
+        rows.append(last)
+        seq = np.concatenate([seq, nxt[:, None]], axis=1)
+    return np.stack(new, axis=1), np.stack(rows)

@@ -225,3 +225,121 @@ def test_gpt_param_order_matches_layer_order():
     assert names[-2:] == ["lnf.g", "lnf.be"]
     p = ref.gpt_params(cfg, 0)
     assert abs(float(p["b0.g1"].mean()) - 1.0) < 0.05 and abs(float(p["b0.be1"].mean())) < 0.05
+
+
+# ---- Gemma-style pieces -------------------------------------------------------------------
+def test_geglu_brute_force():
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((2, 3, 5)).astype(F32)
+    wg, wu = rng.standard_normal((2, 5, 4)).astype(F32)
+    wd = rng.standard_normal((4, 5)).astype(F32)
+    want = np.zeros((2, 3, 5))
+    for b in range(2):
+        for t in range(3):
+            h = []
+            for f in range(4):
+                g = sum(float(x[b, t, c]) * float(wg[c, f]) for c in range(5))
+                u = sum(float(x[b, t, c]) * float(wu[c, f]) for c in range(5))
+                gl = 0.5 * g * (1 + math.tanh(math.sqrt(2 / math.pi) * (g + 0.044715 * g ** 3)))
+                h.append(gl * u)
+            for c in range(5):
+                want[b, t, c] = sum(h[f] * float(wd[f, c]) for f in range(4))
+    assert ref.max_rel(ref.geglu_ffn(x, wg, wu, wd), want) < 1e-5
+    # SwiGLU variant: silu(g) = g * sigmoid(g)
+    g, u = x @ wg, x @ wu
+    sw = (g / (1 + np.exp(-g.astype(np.float64)))) * u
+    assert ref.max_rel(ref.geglu_ffn(x, wg, wu, wd, "silu"), sw @ wd) < 1e-5
+
+
+def test_mqa_without_rope_equals_mha_when_heads_match():
+    rng = np.random.default_rng(32)
+    B, T, H, D = 2, 6, 3, 4
+    C = H * D
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    wqkv = rng.standard_normal((C, 3 * C)).astype(F32) * F32(0.3)
+    wo = rng.standard_normal((C, C)).astype(F32) * F32(0.3)
+    got, _, _ = ref.mqa(x, wqkv, wo, H, H, D, use_rope=False)
+    want = ref.mha(x, wqkv, np.zeros(3 * C, F32), wo, np.zeros(C, F32), H, decoder=True)
+    assert ref.max_rel(got, want) < 1e-5
+
+
+def test_mqa_shared_kv_head_equals_replicated_weights():
+    """Hkv = 1 must equal Hkv = Hq with the key/value columns copied to every head: pins
+    the query-head -> kv-head map and the [Q | K | V] column split."""
+    rng = np.random.default_rng(33)
+    B, T, Hq, D = 2, 5, 4, 8
+    C = 16
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    wq = rng.standard_normal((C, Hq * D)).astype(F32) * F32(0.4)
+    wk = rng.standard_normal((C, D)).astype(F32) * F32(0.4)
+    wv = rng.standard_normal((C, D)).astype(F32) * F32(0.4)
+    wo = rng.standard_normal((Hq * D, C)).astype(F32) * F32(0.4)
+    got, k1, _ = ref.mqa(x, np.concatenate([wq, wk, wv], 1), wo, Hq, 1, D)
+    rep = np.concatenate([wq, np.tile(wk, (1, Hq)), np.tile(wv, (1, Hq))], 1)
+    want, kq, _ = ref.mqa(x, rep, wo, Hq, Hq, D)
+    assert ref.max_rel(got, want) < 1e-6
+    assert k1.shape == (B, 1, T, D) and np.array_equal(kq[:, 2], k1[:, 0])
+    # grouped: Hq = 4, Hkv = 2 -> heads 0,1 read kv head 0 and heads 2,3 read kv head 1
+    wk2 = rng.standard_normal((C, 2 * D)).astype(F32) * F32(0.4)
+    wv2 = rng.standard_normal((C, 2 * D)).astype(F32) * F32(0.4)
+    got2, _, _ = ref.mqa(x, np.concatenate([wq, wk2, wv2], 1), wo, Hq, 2, D)
+    rep2 = np.concatenate([wq, wk2[:, :D], wk2[:, :D], wk2[:, D:], wk2[:, D:],
+                           wv2[:, :D], wv2[:, :D], wv2[:, D:], wv2[:, D:]], 1)
+    want2, _, _ = ref.mqa(x, rep2, wo, Hq, Hq, D)
+    assert ref.max_rel(got2, want2) < 1e-6
+
+
+def test_mqa_rope_identity_at_position_zero():
+    """A single token at position 0 is not rotated, so RoPE on and off agree; at later
+    positions they differ (the rotation is applied)."""
+    rng = np.random.default_rng(34)
+    x = rng.standard_normal((1, 5, 16)).astype(F32)
+    w = rng.standard_normal((16, 6 * 8)).astype(F32) * F32(0.4)
+    wo = rng.standard_normal((32, 16)).astype(F32) * F32(0.4)
+    one, _, _ = ref.mqa(x[:, :1], w, wo, 4, 1, 8)
+    none, _, _ = ref.mqa(x[:, :1], w, wo, 4, 1, 8, use_rope=False)
+    assert ref.max_rel(one, none) < 1e-6
+    a, _, _ = ref.mqa(x, w, wo, 4, 1, 8)
+    b, _, _ = ref.mqa(x, w, wo, 4, 1, 8, use_rope=False)
+    assert ref.max_rel(a, b) > 1e-3
+
+
+def test_mqa_cached_calls_equal_one_call():
+    rng = np.random.default_rng(35)
+    x = rng.standard_normal((2, 9, 16)).astype(F32)
+    w = rng.standard_normal((16, 6 * 8)).astype(F32) * F32(0.4)
+    wo = rng.standard_normal((32, 16)).astype(F32) * F32(0.4)
+    full, kf, vf = ref.mqa(x, w, wo, 4, 1, 8)
+    a, k, v = ref.mqa(x[:, :6], w, wo, 4, 1, 8)
+    b, k2, v2 = ref.mqa(x[:, 6:], w, wo, 4, 1, 8, pos0=6, past_k=k, past_v=v)
+    assert ref.max_rel(np.concatenate([a, b], 1), full) < 1e-6
+    assert ref.max_rel(k2, kf) == 0 and ref.max_rel(v2, vf) == 0
+
+
+GEMMA_TINY = dict(vocab=40, ctx=32, layers=2, d=32, heads=4, kv_heads=1, head_dim=16, ffn=48)
+
+
+def test_gemma_param_order():
+    shapes = ref.gemma_param_shapes(GEMMA_TINY)
+    assert shapes[0] == ("table", (40, 32))
+    assert [n for n, _ in shapes[1:8]] == ["b0.g1", "b0.wqkv", "b0.wo", "b0.g2", "b0.wg",
+                                          "b0.wu", "b0.wd"]
+    assert dict(shapes)["b1.wqkv"] == (32, 6 * 16)
+    assert shapes[-1] == ("normf.g", (32,))
+
+
+def test_gemma_cached_forward_and_greedy_consistency():
+    P = ref.gemma_params(GEMMA_TINY, 3, 0.3)
+    ids = np.random.default_rng(36).integers(0, 40, (2, 7))
+    full = ref.gemma_forward(ids, P, GEMMA_TINY)
+    cache = {}
+    a = ref.gemma_forward(ids[:, :4], P, GEMMA_TINY, cache=cache)
+    b = ref.gemma_forward(ids[:, 4:], P, GEMMA_TINY, pos0=4, cache=cache)
+    assert ref.max_rel(np.concatenate([a, b], 1), full) < 1e-5
+    new, rows = ref.gemma_greedy(ids, P, GEMMA_TINY, 3)
+    assert np.array_equal(new, np.argmax(rows, -1).T)
+    seq = np.concatenate([ids, new[:, :2]], 1)
+    assert ref.max_rel(ref.gemma_forward(seq, P, GEMMA_TINY)[:, -1], rows[2]) == 0
+    # embedding scale: the first layer sees table[ids] * sqrt(d)
+    x0 = P["table"][ids] * np.sqrt(F32(32))
+    assert np.allclose(np.sqrt(np.mean(x0 ** 2)), np.sqrt(np.mean(P["table"] ** 2)) * np.sqrt(32), rtol=0.3)

@@ -25,7 +25,7 @@ struct AttnParams {
   const bf16_t* k;
   const bf16_t* vt;
   bf16_t* out;
-  int Hq, Hkv, Tq, Tk;
+  int Hq, Hkv, Tq, Tk, Lk;  // Lk: key/value capacity (row pitch of vt, rows of k)
   int64_t ld_out;
   int64_t offset;
   float scale_log2;  // log2(e) / divisor
@@ -54,8 +54,8 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest causal blocks first
   const int q0 = qb * 64 + wave * 16;
   const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
-  const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Tk) * D;
-  const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Tk;
+  const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
+  const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
 
   // Q fragments (B operand of S^T): lane holds Q[q0 + fr][32 s + 8 fg .. +7]
   bf16x8 qf[KS];
@@ -83,8 +83,10 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
       const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      const int kv = kv0 + c * 8;  // Tk % 8 == 0: a chunk is fully in or out
-      rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Tk + kv) : make_uint4(0, 0, 0, 0);
+      // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its keys past Tk
+      // get probability 0 (their values must be finite)
+      const int kv = kv0 + c * 8;
+      rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Lk + kv) : make_uint4(0, 0, 0, 0);
     }
   };
   auto store_chunk_lds = [&](int buf) {
@@ -209,7 +211,8 @@ using namespace tl;
 extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt,
                                 void* out, int64_t batch, int64_t n_heads_q, int64_t n_heads_kv,
                                 int64_t seq_q, int64_t seq_k, int64_t head_dim, int64_t ld_out,
-                                int64_t offset, float divisor, int32_t causal, int32_t dtype) {
+                                int64_t offset, float divisor, int32_t causal,
+                                int64_t kv_capacity, int32_t dtype) {
   int rc = enter(ctx);
   if (rc) return rc;
   TL_REQUIRE(q && k && vt && out, "null pointer");
@@ -224,13 +227,16 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
     return fail(TL_ERR_UNSUPPORTED, "fused attention is implemented for bf16 only");
   if (!(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
     return fail(TL_ERR_UNSUPPORTED, "fused attention supports head_dim 32, 64, 128, 256");
-  if (seq_k % 8 != 0 || ld_out % 4 != 0)
-    return fail(TL_ERR_UNSUPPORTED, "fused attention needs seq_k %% 8 == 0 and ld_out %% 4 == 0");
+  const int64_t cap = kv_capacity > 0 ? kv_capacity : seq_k;
+  TL_REQUIRE(seq_k <= cap && cap < (1 << 30), "seq_k exceeds kv_capacity");
+  if (cap % 8 != 0 || ld_out % 4 != 0)
+    return fail(TL_ERR_UNSUPPORTED, "fused attention needs kv_capacity %% 8 == 0 and ld_out %% 4 == 0");
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)vt) & 15u || ((uintptr_t)out & 7u))
     return fail(TL_ERR_UNSUPPORTED, "fused attention needs 16-byte aligned q, k, vt");
   AttnParams p;
   p.q = (const bf16_t*)q; p.k = (const bf16_t*)k; p.vt = (const bf16_t*)vt; p.out = (bf16_t*)out;
   p.Hq = (int)n_heads_q; p.Hkv = (int)n_heads_kv; p.Tq = (int)seq_q; p.Tk = (int)seq_k;
+  p.Lk = (int)cap;
   p.ld_out = ld_out; p.offset = offset; p.causal = causal ? 1 : 0;
   p.scale_log2 = 1.4426950408889634f / divisor;
   // algorithmic work: causal keeps sum over rows of min(Tk, t + offset + 1) keys

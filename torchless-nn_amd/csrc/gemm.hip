@@ -59,6 +59,8 @@ struct GemmParams {
   void* k;
   void* vt;
   int T, Hq, Hkv, Dh;
+  int L, pos0;  // key/value cache capacity and write position (QKV split)
+  int geglu;    // gated epilogue: C[m, n/2] = act(acc[m, n]) * acc[m, n+1]
   int tiles_m, tiles_n, group_m;
   FastDiv div_T, div_Dh;
 };
@@ -77,6 +79,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       if (e < cnt) v[e] = v[e] + Elem<TI>::load((const TI*)p.bias + n0 + e);
+  }
+  if (p.geglu) {  // columns (gate f, up f, gate f+1, up f+1), n0 even
+    TO* c = (TO*)p.C + zo * p.sc_o + zi * p.sc_i + m * p.ldc + n0 / 2;
+    Elem<TO>::store(c, apply_act(v[0], p.act) * v[1]);
+    if (cnt == 4) Elem<TO>::store(c + 1, apply_act(v[2], p.act) * v[3]);
+    return;
   }
   if (p.act != TL_ACT_NONE) {
 #pragma unroll
@@ -101,12 +109,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
       step = 1;
     } else if (ni < qw + kw) {
       const int nn = ni - qw, h = nn / p.Dh, d = nn - h * p.Dh;
-      dst = (TO*)p.k + ((int64_t)(b * p.Hkv + h) * p.T + t) * p.Dh + d;
+      dst = (TO*)p.k + ((int64_t)(b * p.Hkv + h) * p.L + t + p.pos0) * p.Dh + d;
       step = 1;
     } else {
       const int nn = ni - qw - kw, h = nn / p.Dh, d = nn - h * p.Dh;
-      dst = (TO*)p.vt + ((int64_t)(b * p.Hkv + h) * p.Dh + d) * p.T + t;
-      step = p.T;
+      dst = (TO*)p.vt + ((int64_t)(b * p.Hkv + h) * p.Dh + d) * p.L + t + p.pos0;
+      step = p.L;
     }
     if (step == 1 && sizeof(TO) == 2) {
       uint2 w;
@@ -172,7 +180,7 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
     for (int q = 0; q < 4; ++q) {
       if (e.divisor != 1.0f) v[q] = v[q] / e.divisor;
       v[q] = v[q] + bias[j][q];
-      if (e.act != TL_ACT_NONE) v[q] = apply_act(v[q], e.act);
+      if (e.act != TL_ACT_NONE && !e.geglu) v[q] = apply_act(v[q], e.act);
     }
   };
   if (e.qkv) {
@@ -187,8 +195,8 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
       const int nn = n - (part[j] == 0 ? 0 : (part[j] == 1 ? qw : qw + kw));
       const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
       cbase[j] = part[j] == 0 ? (TO*)e.q + ((int64_t)h * e.T) * e.Dh + d
-               : part[j] == 1 ? (TO*)e.k + ((int64_t)h * e.T) * e.Dh + d
-                              : (TO*)e.vt + ((int64_t)h * e.Dh + d) * e.T;
+               : part[j] == 1 ? (TO*)e.k + ((int64_t)h * e.L) * e.Dh + d
+                              : (TO*)e.vt + ((int64_t)h * e.Dh + d) * e.L;
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -196,8 +204,8 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
       if (m >= e.M) continue;
       const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
       const int64_t rq = ((int64_t)b * e.Hq * e.T + t) * e.Dh;
-      const int64_t rk = ((int64_t)b * e.Hkv * e.T + t) * e.Dh;
-      const int64_t rv = (int64_t)b * e.Hkv * e.Dh * e.T + t;
+      const int64_t rk = ((int64_t)b * e.Hkv * e.L + t + e.pos0) * e.Dh;
+      const int64_t rv = (int64_t)b * e.Hkv * e.Dh * e.L + t + e.pos0;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         if (cnt[j] == 0) continue;
@@ -217,13 +225,36 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
         } else {
           TO* dst = cbase[j] + rv;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + (int64_t)q * e.T, v[q]);
+          for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + (int64_t)q * e.L, v[q]);
         }
       }
     }
     return;
   }
   TO* cz = (TO*)e.C + zo * e.sc_o + zi * e.sc_i;
+  if (e.geglu) {  // columns (gate f, up f, gate f+1, up f+1) with f = n / 2
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t m = mb + 16 * i;
+      if (m >= e.M) continue;
+      TO* crow = cz + m * e.ldc + nb / 2;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        if (cnt[j] == 0) continue;
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        finish(v, j);
+        const float h0 = apply_act(v[0], e.act) * v[1], h1 = apply_act(v[2], e.act) * v[3];
+        TO* c = crow + 8 * j;
+        if (sizeof(TO) == 2 && cnt[j] == 4 && e.vec_store) {
+          *reinterpret_cast<uint32_t*>(c) = (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16);
+        } else {
+          Elem<TO>::store(c, h0);
+          if (cnt[j] == 4) Elem<TO>::store(c + 1, h1);
+        }
+      }
+    }
+    return;
+  }
   const TO* rz = e.res ? (const TO*)e.res + zo * e.sr_o + zi * e.sr_i : nullptr;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -759,7 +790,12 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->lda >= d->K, "lda < K");
   TL_REQUIRE(d->b_layout == TL_B_NK ? d->ldb >= d->K : d->ldb >= d->N, "ldb too small");
   const bool qkv = d->epilogue == TL_EPI_QKV_SPLIT;
-  TL_REQUIRE(d->epilogue == TL_EPI_STORE || qkv, "bad epilogue %d", d->epilogue);
+  const bool geglu = d->epilogue == TL_EPI_GEGLU;
+  TL_REQUIRE(d->epilogue == TL_EPI_STORE || qkv || geglu, "bad epilogue %d", d->epilogue);
+  if (geglu) {
+    TL_REQUIRE(d->N % 2 == 0 && !d->residual, "gated epilogue needs even N and no residual");
+    TL_REQUIRE(d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "gated epilogue needs GeLU or SiLU");
+  }
   if (qkv) {
     TL_REQUIRE(d->q && d->k && d->vt, "QKV split needs q, k and vt");
     TL_REQUIRE(batch == 1 && !d->residual, "QKV split is unbatched and has no residual");
@@ -769,9 +805,12 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
                "bad head configuration (head_dim must be a multiple of 4)");
     TL_REQUIRE(d->N == (d->n_heads_q + 2 * d->n_heads_kv) * d->head_dim, "N != (Hq + 2 Hkv) * Dh");
     TL_REQUIRE(d->seq_len < (1LL << 31) && d->N * d->seq_len < (1LL << 40), "QKV split too large");
+    const int64_t L = d->kv_len > 0 ? d->kv_len : d->seq_len;
+    TL_REQUIRE(d->kv_pos0 >= 0 && d->kv_pos0 + d->seq_len <= L && L < (1LL << 31),
+               "cache write [kv_pos0, kv_pos0 + seq_len) exceeds kv_len");
   } else {
     TL_REQUIRE(d->C, "null output");
-    TL_REQUIRE(d->ldc >= d->N, "ldc < N");
+    TL_REQUIRE(d->ldc >= (geglu ? d->N / 2 : d->N), "ldc too small");
   }
   if (d->residual) TL_REQUIRE(d->ldr >= d->N, "ldr < N");
 
@@ -785,9 +824,14 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.divisor = d->divisor; p.act = d->act; p.b_kn = d->b_layout == TL_B_KN;
   p.qkv = qkv; p.q = d->q; p.k = d->k; p.vt = d->vt;
   p.T = (int)d->seq_len; p.Hq = (int)d->n_heads_q; p.Hkv = (int)d->n_heads_kv; p.Dh = (int)d->head_dim;
+  p.L = (int)(d->kv_len > 0 ? d->kv_len : d->seq_len);
+  p.pos0 = (int)d->kv_pos0;
+  p.geglu = geglu;
   const size_t eo = dtype_size(d->dtype_out);
   p.vec_store = !qkv && d->ldc % 4 == 0 && ((uintptr_t)d->C % (4 * eo)) == 0 &&
                 d->sc_o % 4 == 0 && d->sc_i % 4 == 0;
+  if (geglu) p.vec_store = d->ldc % 2 == 0 && ((uintptr_t)d->C % (2 * eo)) == 0 &&
+                           d->sc_o % 2 == 0 && d->sc_i % 2 == 0;
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);

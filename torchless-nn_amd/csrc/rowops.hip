@@ -83,7 +83,7 @@ template <typename T, typename I, bool VEC>
 __global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table, const T* pos,
                                                     T* out, int64_t n_tok, int64_t seq_len,
                                                     int64_t pos0, int64_t vocab, int64_t dim,
-                                                    int64_t ld_out, int32_t* status) {
+                                                    int64_t ld_out, float scale, int32_t* status) {
   constexpr int VW = Elem<T>::kVec;
   const int lane = threadIdx.x & 63;
   const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -101,6 +101,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table
     for (int64_t c = (int64_t)lane * VW; c < dim; c += 64 * VW) {
       float a[VW], b[VW];
       load_chunk(tr + c, a);
+      if (scale != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) a[e] = a[e] * scale;
+      }
       if (pr) {
         load_chunk(pr + c, b);
 #pragma unroll
@@ -111,6 +115,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table
   } else {
     for (int64_t c = lane; c < dim; c += 64) {
       float a = Elem<T>::load(tr + c);
+      if (scale != 1.0f) a = a * scale;
       if (pr) a = a + Elem<T>::load(pr + c);
       Elem<T>::store(o + c, a);
     }
@@ -496,10 +501,9 @@ __global__ void rope_table_kernel(float* table, int64_t seq_len, int64_t head_di
 }
 
 template <typename T, bool VEC>
-__global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* __restrict__ y,
-                                                   const float* __restrict__ table,
+__global__ __launch_bounds__(256) void rope_kernel(const T* x, T* y, const float* __restrict__ table,
                                                    int64_t n_seq, int64_t seq_len,
-                                                   int64_t head_dim) {
+                                                   int64_t head_dim, int64_t seq_stride) {
   constexpr int VW = VEC ? Elem<T>::kVec : 1;
   const int64_t half = head_dim / 2;
   const int64_t per_row = half / VW;
@@ -509,9 +513,9 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* __restrict__ x, T* _
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = idx / per_row;
     const int64_t i = (idx % per_row) * VW;
-    const int64_t t = row % seq_len;
-    const T* xr = x + row * head_dim;
-    T* yr = y + row * head_dim;
+    const int64_t sq = row / seq_len, t = row - sq * seq_len;
+    const T* xr = x + sq * seq_stride + t * head_dim;
+    T* yr = y + sq * seq_stride + t * head_dim;
     const float* cs = table + t * half + i;
     const float* sn = table + tsz + t * half + i;
     float a[VW], b[VW], c[VW], s[VW], o1[VW], o2[VW];
@@ -645,7 +649,7 @@ namespace tl {
 template <typename T>
 static void launch_embed(tl_ctx* ctx, int ids_dtype, const void* ids, const void* table,
                          const void* pos, void* out, int64_t n_tok, int64_t seq_len,
-                         int64_t pos0, int64_t vocab, int64_t dim, int64_t ld_out) {
+                         int64_t pos0, int64_t vocab, int64_t dim, int64_t ld_out, float scale) {
   const bool vec = dim % Elem<T>::kVec == 0 && ld_out % Elem<T>::kVec == 0 &&
                    aligned16(table) && aligned16(out) && (!pos || aligned16(pos));
   const unsigned g = (unsigned)((n_tok + 3) / 4);
@@ -653,10 +657,10 @@ static void launch_embed(tl_ctx* ctx, int ids_dtype, const void* ids, const void
     typedef decltype(id_tag) I;
     if (vec)
       embed_kernel<T, I, true><<<g, 256, 0, ctx->stream>>>((const I*)ids, (const T*)table,
-          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, ctx->status);
+          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, scale, ctx->status);
     else
       embed_kernel<T, I, false><<<g, 256, 0, ctx->stream>>>((const I*)ids, (const T*)table,
-          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, ctx->status);
+          (const T*)pos, (T*)out, n_tok, seq_len, pos0, vocab, dim, ld_out, scale, ctx->status);
   };
   if (ids_dtype == TL_U8) go(uint8_t());
   else if (ids_dtype == TL_I32) go(int32_t());
@@ -735,19 +739,19 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
 
 template <typename T>
 static void launch_rope(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
-                        int64_t seq_len, int64_t head_dim) {
+                        int64_t seq_len, int64_t head_dim, int64_t seq_stride) {
   constexpr int VW = Elem<T>::kVec;
   const int64_t half = head_dim / 2;
   const bool vec = half % VW == 0 && aligned16(x) && aligned16(y) && aligned16(table) &&
-                   (seq_len * half) % 4 == 0;
+                   (seq_len * half) % 4 == 0 && seq_stride % VW == 0;
   const int64_t work = n_seq * seq_len * (vec ? half / VW : half);
   const unsigned g = grid_for(ctx, work, 256);
   if (vec)
     rope_kernel<T, true><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
-                                                      n_seq, seq_len, head_dim);
+                                                      n_seq, seq_len, head_dim, seq_stride);
   else
     rope_kernel<T, false><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
-                                                       n_seq, seq_len, head_dim);
+                                                       n_seq, seq_len, head_dim, seq_stride);
 }
 
 template <typename T>
@@ -874,7 +878,7 @@ int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
 
 int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* table,
                  const void* pos, void* out, int64_t n_tok, int64_t seq_len, int64_t pos0,
-                 int64_t vocab, int64_t dim, int64_t ld_out, int32_t dtype) {
+                 int64_t vocab, int64_t dim, int64_t ld_out, float scale, int32_t dtype) {
   int rc = enter(ctx);
   if (rc) return rc;
   TL_REQUIRE_FLOAT(dtype);
@@ -888,9 +892,9 @@ int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* ta
   LaunchScope ls(ctx, TL_KF_EMBED, 0,
                  (double)n_tok * (dtype_size(ids_dtype) + (pos ? 3 : 2) * dim * es));
   if (dtype == TL_F32)
-    launch_embed<float>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out);
+    launch_embed<float>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out, scale);
   else
-    launch_embed<bf16_t>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out);
+    launch_embed<bf16_t>(ctx, ids_dtype, ids, table, pos, out, n_tok, seq_len, pos0, vocab, dim, ld_out, scale);
   return ls.finish("embed_fwd");
 }
 
@@ -959,17 +963,18 @@ int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, d
 }
 
 int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
-                int64_t seq_len, int64_t head_dim, int32_t dtype) {
+                int64_t seq_len, int64_t head_dim, int64_t seq_stride, int32_t dtype) {
   int rc = enter(ctx);
   if (rc) return rc;
   TL_REQUIRE_FLOAT(dtype);
   TL_REQUIRE(n_seq >= 0 && seq_len > 0 && head_dim > 0 && head_dim % 2 == 0, "bad sizes");
+  TL_REQUIRE(seq_stride >= seq_len * head_dim, "seq_stride < seq_len * head_dim");
   if (n_seq == 0) return TL_OK;
   TL_REQUIRE(x && y && table, "null pointer");
   const double es = (double)dtype_size(dtype);
   LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * n_seq * seq_len * head_dim);
-  if (dtype == TL_F32) launch_rope<float>(ctx, x, y, table, n_seq, seq_len, head_dim);
-  else launch_rope<bf16_t>(ctx, x, y, table, n_seq, seq_len, head_dim);
+  if (dtype == TL_F32) launch_rope<float>(ctx, x, y, table, n_seq, seq_len, head_dim, seq_stride);
+  else launch_rope<bf16_t>(ctx, x, y, table, n_seq, seq_len, head_dim, seq_stride);
   return ls.finish("rope_fwd");
 }
 

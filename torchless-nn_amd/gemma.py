@@ -1,0 +1,100 @@
+"""Gemma-style decoder on the MI355X runtime: scaled tied embedding, pre-norm blocks with
+RMSNorm ((1 + gamma), eps 1e-6), multi-query rotary attention and GeGLU FFN, final RMSNorm,
+tied LM head; prefill into a KV cache, then greedy decoding that keeps every step on the
+device (argmax output feeds the next embedding gather without a host round trip).
+
+The reference generates by recomputing the whole window each step (demo.ipynb:1520-1537);
+the layers and the decode loop here are new components built on the same Layer protocol.
+"""
+import numpy as np
+
+import backend
+import tl_hip as xp
+from layers import GemmaBlock, KVCache, RMSNorm
+from transformer_adapters import GPTEmbeddingTable, GPTEmbedBack, ScaledEmbedFront
+
+__all__ = ["GEMMA_2B", "GemmaDecoder", "build_gemma", "seed_gemma"]
+
+# BASELINE config 5 model shape (vocab 256000, 18 layers, d 2048, 8 query heads sharing one
+# key/value head of width 256, FFN 16384); ctx is the positional range the cache may span.
+GEMMA_2B = dict(vocab=256000, ctx=8192, layers=18, d=2048, heads=8, kv_heads=1, head_dim=256,
+                ffn=16384, rope_base=10000.0)
+
+
+class GemmaDecoder:
+    """Layer list [ScaledEmbedFront, GemmaBlock x L, RMSNorm, GPTEmbedBack] over one tied
+    table. forward(ids, cache, pos0) -> logits [B, T, V] (row pitch a multiple of 8)."""
+
+    def __init__(self, cfg):
+        self.cfg = dict(cfg)
+        d = cfg["d"]
+        self.table = GPTEmbeddingTable(cfg["vocab"], d)
+        self.front = ScaledEmbedFront(self.table, np.sqrt(np.float32(d)))
+        self.blocks = [GemmaBlock(d, cfg["ctx"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"],
+                                  cfg["ffn"], cfg.get("rope_base", 10000.0))
+                       for _ in range(cfg["layers"])]
+        self.final_norm = RMSNorm(d, eps=1e-6, gamma_offset=1.0)
+        self.back = GPTEmbedBack(self.table)
+        self.layers = [self.front, *self.blocks, self.final_norm, self.back]
+        self.dtype = self.table.table.dtype
+
+    def new_cache(self, batch, capacity):
+        c = self.cfg
+        return KVCache(c["layers"], batch, c["kv_heads"], capacity, c["head_dim"], self.dtype)
+
+    def forward(self, ids, cache=None, pos0=0):
+        x = self.front.forward(ids)
+        for i, blk in enumerate(self.blocks):
+            x = blk.forward(x, cache, i, pos0)
+        x = self.final_norm.forward(x)
+        logits = self.back.forward(x)
+        if cache is not None:
+            cache.length = pos0 + x.shape[1]
+        return logits
+
+    @staticmethod
+    def last_rows(logits):
+        """View of logits[:, -1, :] as a [B, V] tensor (no copy)."""
+        B, T, V = logits.shape
+        es = logits.dtype.itemsize
+        return xp.DeviceTensor((B, V), logits.dtype, pitch=T * logits.pitch, buf=logits.buf,
+                               offset=logits.offset + (T - 1) * logits.pitch * es)
+
+    def generate_greedy(self, ids, n_new, cache=None, return_logits=False):
+        """Prefill `ids` [B, T] into a KV cache, then take `n_new` greedy steps, each feeding
+        the device argmax of the last logits row back as the next token. Returns the new
+        token ids [B, n_new] as a host int64 array (and, if asked, the per-step last-row
+        logits [n_new, B, V] as float32: step 0 from the prefill)."""
+        if not isinstance(ids, xp.DeviceTensor):
+            ids = xp.array(np.asarray(ids))
+        B, T = ids.shape
+        if cache is None:
+            cache = self.new_cache(B, T + n_new)
+        logits = self.forward(ids, cache, 0)
+        steps, kept = [], []
+        for t in range(n_new):
+            last = self.last_rows(logits)
+            if return_logits:
+                kept.append(last.get())
+            nxt = xp.argmax(last)  # [B] int64 on the device
+            steps.append(nxt)
+            if t + 1 < n_new:
+                logits = self.forward(nxt.reshape(B, 1), cache, T + t)
+        out = np.stack([s.get() for s in steps], axis=1) if steps else np.zeros((B, 0), np.int64)
+        return (out, np.stack(kept)) if return_logits else out
+
+
+def build_gemma(cfg, dtype=None):
+    if dtype is not None:
+        backend.set_float_type(dtype)
+    return GemmaDecoder(cfg)
+
+
+def seed_gemma(model, seed, scale=0.02):
+    """Overwrite all parameters, in layer order, with seeded N(0,1)*scale (the RMSNorm
+    gammas too: they scale by 1 + gamma)."""
+    rng = np.random.default_rng(seed)
+    for layer in model.layers:
+        for p in layer.parameters:
+            p.set(rng.standard_normal(p.shape, dtype=np.float32) * np.float32(scale))
+    return model

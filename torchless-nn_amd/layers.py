@@ -22,7 +22,8 @@ from utils import Layer
 from activations import act_code_of
 
 __all__ = ["Dense", "Dropout", "MultiHeadAttention", "TransformerFeedForward", "LayerNorm",
-           "RMSNorm", "TransformerBlock", "linear"]
+           "RMSNorm", "TransformerBlock", "linear", "KVCache", "MultiQueryAttention",
+           "GeGLUFeedForward", "GemmaBlock"]
 
 
 def _round_up(n, m):
@@ -303,3 +304,182 @@ class TransformerBlock(Layer):
         self.eval_mode = eval_mode
         self.attn_block.set_eval(eval_mode)
         self.ffn.set_eval(eval_mode)
+
+
+# ---------------------------------------------------------------------------------------
+# Gemma-style decoder pieces. The reference has no counterpart: its
+# attention is one fused [C, 3C] MHA with absolute positions (layers.py:241-307), its FFN
+# is ungated (layers.py:346-375) and generation recomputes the whole window
+# (demo.ipynb:1520-1537). Their interfaces follow the Layer protocol above.
+# ---------------------------------------------------------------------------------------
+class KVCache:
+    """Per-layer keys [B, Hkv, L, D] and transposed values [B, Hkv, D, L] in HBM, zero
+    filled (positions past the valid length must hold finite values), L a multiple of 8."""
+
+    def __init__(self, n_layers, batch, n_kv_heads, capacity, head_dim, dtype):
+        self.capacity = _round_up(capacity, 8)
+        self.batch, self.n_kv_heads, self.head_dim = batch, n_kv_heads, head_dim
+        self.k = [xp.zeros((batch, n_kv_heads, self.capacity, head_dim), dtype) for _ in range(n_layers)]
+        self.vt = [xp.zeros((batch, n_kv_heads, head_dim, self.capacity), dtype) for _ in range(n_layers)]
+        self.length = 0  # valid positions written so far
+
+
+class MultiQueryAttention(Layer):
+    """Multi-/grouped-query causal attention with rotary positions: num_heads query heads
+    share num_kv_heads key/value heads (Shazeer 2019, "Fast Transformer Decoding"; Ainslie
+    et al. 2023, GQA), rotate-half RoPE on queries and keys (Su et al. 2021), scores divided
+    by sqrt(head_dim), no biases. Weights qkv [C, (Hq + 2 Hkv) D] with columns [Q | K | V]
+    and out [Hq D, C]. `forward(x, cache, layer, pos0)` writes this call's keys and values
+    into `cache` at positions pos0.. and attends over positions 0 .. pos0 + T - 1."""
+    fused = True
+
+    def __init__(self, embedding_dim, context_length, num_heads, num_kv_heads, head_dim,
+                 rope_base=10000.0):
+        super(MultiQueryAttention, self).__init__()
+        if num_heads % num_kv_heads:
+            raise ValueError("num_heads must be a multiple of num_kv_heads")
+        self.embedding_dim, self.context_length = embedding_dim, context_length
+        self.num_heads, self.num_kv_heads, self.heads_dim = num_heads, num_kv_heads, head_dim
+        self.rope_base = float(rope_base)
+        C, N = embedding_dim, (num_heads + 2 * num_kv_heads) * head_dim
+        self.qkv_weights = backend.init_random_tensor((C, N), divisor=C ** 0.5)
+        self.out_weights = backend.init_random_tensor((num_heads * head_dim, C),
+                                                      divisor=(num_heads * head_dim) ** 0.5)
+        self.register_param(self.qkv_weights)
+        self.register_param(self.out_weights)
+        self.softmax = None
+
+    def forward(self, input, cache=None, layer=0, pos0=0):
+        return self._forward(input, None, cache, layer, pos0)
+
+    def _forward(self, input, residual, cache=None, layer=0, pos0=0):
+        self.input = input
+        B, T, C = input.shape
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.heads_dim
+        if pos0 + T > self.context_length:
+            raise ValueError(f"positions up to {pos0 + T} exceed the context length "
+                             f"{self.context_length}")
+        dt = input.dtype
+        q = xp.empty((B, Hq, T, D), dt)
+        if cache is not None:
+            if pos0 + T > cache.capacity:
+                raise ValueError("KV cache too small")
+            k, vt, L = cache.k[layer], cache.vt[layer], cache.capacity
+        else:
+            L = _round_up(T, 8)
+            k, vt = xp.zeros((B, Hkv, L, D), dt), xp.zeros((B, Hkv, D, L), dt)
+        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0))
+        table = xp.rope_table(T, D, self.rope_base, pos0)
+        xp.rope(q, table, out=q)
+        kslice = xp.DeviceTensor((B * Hkv, T, D), dt, buf=k.buf,
+                                 offset=k.offset + pos0 * D * dt.itemsize)
+        xp.rope(kslice, table, out=kslice, seq_len=T, n_seq=B * Hkv, seq_stride=L * D)
+        Tk = pos0 + T
+        divisor = float(np.float32(D ** 0.5))
+        heads = xp.empty((B, T, Hq * D), dt)
+        if self.fused and xp.attention_supported(dt, D, L):
+            xp.attention(q, k, vt, heads, n_heads_q=Hq, n_heads_kv=Hkv, divisor=divisor,
+                         causal=True, offset=pos0, seq_k=Tk)
+        else:
+            self._unfused(q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt, divisor, pos0)
+        out = linear(heads.reshape(B * T, Hq * D), self.out_weights,
+                     residual=(residual.reshape(B * T, C) if residual is not None else None))
+        self.output = out.reshape(B, T, C)
+        return self.output
+
+    def _unfused(self, q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt, divisor, pos0):
+        g = Hq // Hkv
+        ldS = _round_up(Tk, 8)
+        scores = xp.empty((B, Hq, T, Tk), dt, pitch=ldS)
+        es = dt.itemsize
+        for hk in range(Hkv):  # one batched product per kv head: z = (b, query head in group)
+            qv = xp.DeviceTensor((1,), dt, buf=q.buf, offset=q.offset + hk * g * T * D * es)
+            kv = xp.DeviceTensor((1,), dt, buf=k.buf, offset=k.offset + hk * L * D * es)
+            sv = xp.DeviceTensor((1,), dt, buf=scores.buf, offset=scores.offset + hk * g * T * ldS * es)
+            xp.gemm(qv, kv, M=T, N=Tk, K=D, lda=D, ldb=D, b_layout=xp.TL_B_NK, C=sv, ldc=ldS,
+                    batch=B * g, batch_inner=g, sa=(Hq * T * D, T * D), sb=(Hkv * L * D, 0),
+                    sc=(Hq * T * ldS, T * ldS), divisor=divisor, family="gemm_batched")
+        probs = xp.softmax(scores, causal=True, period=T, offset=pos0, out=scores)
+        self.softmax = probs
+        for hk in range(Hkv):
+            pv = xp.DeviceTensor((1,), dt, buf=probs.buf, offset=probs.offset + hk * g * T * ldS * es)
+            vv = xp.DeviceTensor((1,), dt, buf=vt.buf, offset=vt.offset + hk * D * L * es)
+            hv = xp.DeviceTensor((1,), dt, buf=heads.buf, offset=heads.offset + hk * g * D * es)
+            xp.gemm(pv, vv, M=T, N=D, K=Tk, lda=ldS, ldb=L, b_layout=xp.TL_B_NK, C=hv,
+                    ldc=Hq * D, batch=B * g, batch_inner=g, sa=(Hq * T * ldS, T * ldS),
+                    sb=(Hkv * D * L, 0), sc=(T * Hq * D, D), family="gemm_batched")
+
+
+class GeGLUFeedForward(Layer):
+    """act(x W_gate) * (x W_up) then W_down, no biases (Shazeer 2020, "GLU Variants Improve
+    Transformer"); act is the tanh-GeLU of reference activations.py:24-28 (GeGLU) or SiLU
+    (SwiGLU). The gate and up weights are packed into one [2F, C] operand with interleaved
+    rows (gate f, up f), so one GEMM's epilogue forms act(gate) * up."""
+
+    def __init__(self, num_channels, hidden, activation=None):
+        super(GeGLUFeedForward, self).__init__()
+        from activations import GeLU
+        activation = activation or GeLU
+        self.act_code = act_code_of(activation)
+        if self.act_code not in (xp.TL_ACT_GELU, xp.TL_ACT_SILU):
+            raise ValueError("gated FFN supports GeLU or SiLU")
+        C, F = num_channels, hidden
+        self.hidden = F
+        self.gate_weights = backend.init_random_tensor((C, F), divisor=C ** 0.5)
+        self.up_weights = backend.init_random_tensor((C, F), divisor=C ** 0.5)
+        self.down_weights = backend.init_random_tensor((F, C), divisor=F ** 0.5)
+        for w in (self.gate_weights, self.up_weights, self.down_weights):
+            self.register_param(w)
+        self._pack = None
+
+    def _packed(self):
+        g, u = self.gate_weights, self.up_weights
+        key = (g._version, u._version)
+        if self._pack is None or self._pack[0] != key:
+            C, F = g.shape
+            packed = xp.empty((2 * F, C), g.dtype)
+            xp.transpose2d(g, out=packed, out_offset=0, ldy=2 * C)
+            xp.transpose2d(u, out=packed, out_offset=C, ldy=2 * C)
+            self._pack = (key, packed)
+        return self._pack[1]
+
+    def forward(self, input):
+        return self._forward(input, None)
+
+    def _forward(self, input, residual):
+        self.input = input
+        shape = input.shape
+        C, F = shape[-1], self.hidden
+        x2 = input.reshape(-1, C)
+        M = x2.shape[0]
+        h = xp.empty((M, F), input.dtype)
+        xp.gemm(x2, self._packed(), M=M, N=2 * F, K=C, lda=x2.pitch, ldb=C, b_layout=xp.TL_B_NK,
+                C=h, ldc=F, act=self.act_code, geglu=True)
+        self.hidden_output = h
+        y = linear(h, self.down_weights,
+                   residual=(residual.reshape(-1, C) if residual is not None else None))
+        self.output = y.reshape(*shape)
+        return self.output
+
+
+class GemmaBlock(Layer):
+    """Pre-norm decoder block with RMSNorm ((1 + gamma) scale, eps 1e-6), multi-query
+    rotary attention and a GeGLU FFN: y = x + Attn(N1 x); z = y + FFN(N2 y). Residual adds
+    run in the GEMM epilogues, as in TransformerBlock."""
+
+    def __init__(self, embed_dim, context_length, num_heads, num_kv_heads, head_dim, ffn_hidden,
+                 rope_base=10000.0, eps=1e-6):
+        super(GemmaBlock, self).__init__()
+        self.pre_attn_norm = RMSNorm(embed_dim, eps=eps, gamma_offset=1.0)
+        self.attn_block = MultiQueryAttention(embed_dim, context_length, num_heads, num_kv_heads,
+                                              head_dim, rope_base)
+        self.pre_ffn_norm = RMSNorm(embed_dim, eps=eps, gamma_offset=1.0)
+        self.ffn = GeGLUFeedForward(embed_dim, ffn_hidden)
+        self.parameters = [*self.pre_attn_norm.parameters, *self.attn_block.parameters,
+                           *self.pre_ffn_norm.parameters, *self.ffn.parameters]
+
+    def forward(self, input, cache=None, layer=0, pos0=0):
+        self.input = input
+        y = self.attn_block._forward(self.pre_attn_norm.forward(input), input, cache, layer, pos0)
+        self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), y)
+        return self.output

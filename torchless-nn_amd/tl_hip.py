@@ -22,7 +22,7 @@ LIB_PATH = os.environ.get("TL_LIBRARY", os.path.join(_HERE, "libtl.so"))
 TL_OK, TL_ERR_INVALID, TL_ERR_HIP, TL_ERR_OOM, TL_ERR_NO_DEVICE, TL_ERR_BAD_INPUT, TL_ERR_UNSUPPORTED = range(7)
 TL_ACT_NONE, TL_ACT_GELU, TL_ACT_SILU = 0, 1, 2
 TL_B_NK, TL_B_KN = 0, 1
-TL_EPI_STORE, TL_EPI_QKV_SPLIT = 0, 1
+TL_EPI_STORE, TL_EPI_QKV_SPLIT, TL_EPI_GEGLU = 0, 1, 2
 GEMM_TILES = {"auto": 0, "256x256": 1, "256x128": 2, "128x128": 3, "128x64": 4, "64x64": 5,
               "256x256w4": 6, "256x128w8": 7, "dma128x128": 8, "dma256x128w8": 9,
               "dma128x64s3": 10, "dma128x128s3": 11, "persist256x128w8": 12,
@@ -127,6 +127,7 @@ class _GemmDesc(ctypes.Structure):
         ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("vt", ctypes.c_void_p),
         ("seq_len", ctypes.c_int64), ("n_heads_q", ctypes.c_int64),
         ("n_heads_kv", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+        ("kv_len", ctypes.c_int64), ("kv_pos0", ctypes.c_int64),
         ("family", ctypes.c_int32), ("tile", ctypes.c_int32),
     ]
 
@@ -162,17 +163,17 @@ SIGNATURES = {
     "tl_cast": [_P, _P, _P, _I64, _I32, _I32],
     "tl_transpose2d": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
-    "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32],
+    "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_layernorm_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_rmsnorm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _F32, _I32],
     "tl_softmax_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32, _I64, _I64, _I32],
     "tl_rope_table": [_P, _P, _I64, _I64, _F64, _I64],
-    "tl_rope_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I32],
+    "tl_rope_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_act_fwd": [_P, _P, _P, _I64, _I32, _I32],
     "tl_argmax": [_P, _P, _I64, _I64, _I64, _I32, _P],
     "tl_gemm": [_P, ctypes.POINTER(_GemmDesc)],
     "tl_attention_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
-                         _F32, _I32, _I32],
+                         _F32, _I32, _I64, _I32],
 }
 _RESTYPES = {"tl_last_error": ctypes.c_char_p}
 
@@ -308,6 +309,12 @@ class DeviceTensor:
             raise ValueError("pitch smaller than the last dimension")
         if buf is None:
             buf = DeviceBuffer(max(1, self.nrows * self.pitch * self.dtype.itemsize))
+        elif self.size:
+            # a view must lie inside its buffer: kernels take raw pointers and cannot check
+            end = int(offset) + ((self.nrows - 1) * self.pitch + cols) * self.dtype.itemsize
+            if int(offset) < 0 or end > buf.nbytes:
+                raise ValueError(f"view of {end - int(offset)} bytes at offset {int(offset)} "
+                                 f"exceeds its {buf.nbytes}-byte buffer")
         self.buf, self.offset, self._version = buf, int(offset), 0
         self._aux = None  # device-side derived data (e.g. a packed weight), by _version
 
@@ -507,7 +514,7 @@ def _c():
 def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=None, ldc=0,
          out_dtype=None, batch=1, batch_inner=1, sa=(0, 0), sb=(0, 0), sc=(0, 0), bias=None,
          residual=None, ldr=0, sr=(0, 0), act=TL_ACT_NONE, divisor=1.0, qkv=None,
-         family="gemm_mfma", tile="auto"):
+         family="gemm_mfma", tile="auto", geglu=False):
     d = _GemmDesc()
     d.M, d.N, d.K = M, N, K
     d.A, d.lda, d.B, d.ldb, d.b_layout = A.ptr, lda, B.ptr, ldb, b_layout
@@ -526,10 +533,14 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
     d.family = KFAMILY[family]
     d.tile = GEMM_TILES[tile]
     if qkv is not None:
-        q, k, vt, T, Hq, Hkv, Dh = qkv
+        q, k, vt, T, Hq, Hkv, Dh = qkv[:7]
+        kv_len, kv_pos0 = (qkv[7], qkv[8]) if len(qkv) > 7 else (0, 0)
         d.epilogue = TL_EPI_QKV_SPLIT
         d.q, d.k, d.vt = q.ptr, k.ptr, vt.ptr
         d.seq_len, d.n_heads_q, d.n_heads_kv, d.head_dim = T, Hq, Hkv, Dh
+        d.kv_len, d.kv_pos0 = kv_len, kv_pos0
+    elif geglu:
+        d.epilogue = TL_EPI_GEGLU
     else:
         d.epilogue = TL_EPI_STORE
     lib_, h = _c()
@@ -568,14 +579,26 @@ def rope_table(seq_len, head_dim, base=10000.0, pos0=0) -> DeviceTensor:
     return t
 
 
-def rope(x: DeviceTensor, table: DeviceTensor, out=None):
-    """Rotate-half RoPE over the last two dims [.., T, D] of a contiguous tensor."""
+def rope(x: DeviceTensor, table: DeviceTensor, out=None, seq_len=None, n_seq=None,
+         seq_stride=None):
+    """Rotate-half RoPE over the last two dims [.., T, D] of a contiguous tensor, or over
+    `n_seq` sequences of `seq_len` rows placed `seq_stride` elements apart (a cache slice;
+    then x/out are the first row of the slice and the op may run in place)."""
     if not x.contiguous:
         raise ValueError("rope needs a contiguous tensor")
-    T, D = x.shape[-2], x.shape[-1]
+    D = x.shape[-1]
+    T = seq_len if seq_len is not None else x.shape[-2]
+    n = n_seq if n_seq is not None else x.size // (T * D)
+    stride = seq_stride if seq_stride is not None else T * D
     out = out if out is not None else DeviceTensor(x.shape, x.dtype)
+    if n > 0:
+        span = ((n - 1) * stride + T * D) * x.dtype.itemsize
+        for t in (x, out):
+            if t.offset + span > t.buf.nbytes:
+                raise ValueError(f"rope over {n} sequences {stride} elements apart runs past "
+                                 f"the end of its buffer")
     lib_, h = _c()
-    check(lib_.tl_rope_fwd(h, x.ptr, out.ptr, table.ptr, x.size // (T * D), T, D, x.dtype.code))
+    check(lib_.tl_rope_fwd(h, x.ptr, out.ptr, table.ptr, n, T, D, stride, x.dtype.code))
     return out
 
 
@@ -588,41 +611,50 @@ def activation(x: DeviceTensor, act: int, out=None):
     return out
 
 
-def embed(ids: DeviceTensor, table: DeviceTensor, pos, seq_len, pos0=0, out_shape=None):
+def embed(ids: DeviceTensor, table: DeviceTensor, pos, seq_len, pos0=0, out_shape=None,
+          scale=1.0):
     V, C = table.shape
     out = DeviceTensor(out_shape or (ids.size, C), table.dtype)
     lib_, h = _c()
     check(lib_.tl_embed_fwd(h, ids.ptr, ids.dtype.code, table.ptr,
                             pos.ptr if pos is not None else None, out.ptr, ids.size, seq_len,
-                            pos0, V, C, out.pitch, table.dtype.code))
+                            pos0, V, C, out.pitch, float(scale), table.dtype.code))
     return out
 
 
 def attention(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTensor, *,
-              n_heads_q, n_heads_kv, divisor, causal=True, offset=0):
-    """Fused attention: q [B, Hq, Tq, D], k [B, Hkv, Tk, D], vt [B, Hkv, D, Tk] -> out
-    [B, Tq, Hq*D] (row pitch out.pitch). Raises TLError(TL_ERR_UNSUPPORTED) for shapes
-    the kernel does not take."""
+              n_heads_q, n_heads_kv, divisor, causal=True, offset=0, seq_k=None):
+    """Fused attention: q [B, Hq, Tq, D], k [B, Hkv, Lk, D], vt [B, Hkv, D, Lk] (the first
+    `seq_k` keys valid, all Lk by default) -> out [B, Tq, Hq*D] (row pitch out.pitch).
+    Raises TLError(TL_ERR_UNSUPPORTED) for shapes the kernel does not take."""
     B, Hq, Tq, D = q.shape
-    Tk = k.shape[2]
+    Lk = k.shape[2]
+    Tk = Lk if seq_k is None else seq_k
     lib_, h = _c()
     check(lib_.tl_attention_fwd(h, q.ptr, k.ptr, vt.ptr, out.ptr, B, n_heads_q, n_heads_kv, Tq,
                                 Tk, D, out.pitch, int(offset), float(divisor), int(bool(causal)),
-                                q.dtype.code))
+                                Lk, q.dtype.code))
     return out
 
 
-def attention_supported(dtype, head_dim, seq_k) -> bool:
+def attention_supported(dtype, head_dim, kv_capacity) -> bool:
     """Whether tl_attention_fwd takes this configuration (bf16, D in {32, 64, 128, 256},
-    key length a multiple of 8)."""
-    return as_dtype(dtype) is bfloat16 and head_dim in (32, 64, 128, 256) and seq_k % 8 == 0
+    key capacity a multiple of 8)."""
+    return (as_dtype(dtype) is bfloat16 and head_dim in (32, 64, 128, 256)
+            and kv_capacity % 8 == 0)
 
 
-def transpose2d(x: DeviceTensor) -> DeviceTensor:
+def transpose2d(x: DeviceTensor, out=None, out_offset=0, ldy=None) -> DeviceTensor:
+    """y[c, r] = x[r, c]. With `out`, writes into out's buffer at element `out_offset` with
+    row pitch `ldy` (e.g. every other row of an interleaved pack)."""
     r, c_ = x.shape
-    out = DeviceTensor((c_, r), x.dtype)
+    if out is None:
+        out = DeviceTensor((c_, r), x.dtype)
+        ptr, ld = out.ptr, out.pitch
+    else:
+        ptr, ld = out.ptr + out_offset * x.dtype.itemsize, ldy
     lib_, h = _c()
-    check(lib_.tl_transpose2d(h, x.ptr, out.ptr, r, c_, x.pitch, out.pitch, x.dtype.code))
+    check(lib_.tl_transpose2d(h, x.ptr, ptr, r, c_, x.pitch, ld, x.dtype.code))
     return out
 
 

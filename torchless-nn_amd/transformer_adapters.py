@@ -7,7 +7,8 @@ import tl_hip as xp
 from utils import Layer
 from layers import linear
 
-__all__ = ["GPTEmbeddingTable", "GPTEmbedFront", "GPTEmbedBack", "VitMLPHead"]
+__all__ = ["GPTEmbeddingTable", "GPTEmbedFront", "GPTEmbedBack", "VitMLPHead",
+           "ScaledEmbedFront"]
 
 
 def _round_up(n, m):
@@ -107,4 +108,25 @@ class VitMLPHead(Layer):
         cls = xp.DeviceTensor((B, C), input.dtype, pitch=L * C, buf=input.buf,
                               offset=input.offset)
         self.output = linear(cls, self.weights, self.bias)
+        return self.output
+
+
+class ScaledEmbedFront(Layer):
+    """table[ids] * scale with no positional table (rotary positions are applied inside
+    attention). Gemma-style decoders scale by sqrt(d_model). No reference counterpart; the
+    gather is GPTEmbedFront's (reference transformer_adapters.py:150)."""
+
+    def __init__(self, embedding_table, scale):
+        super(ScaledEmbedFront, self).__init__()
+        self.embedding_table = embedding_table
+        self.scale = float(np.float32(scale))
+        self.parameters.append(self.embedding_table.table)
+
+    def forward(self, input):
+        if not isinstance(input, xp.DeviceTensor):
+            input = xp.array(np.asarray(input))
+        self.input = input
+        B, T = input.shape
+        self.output = xp.embed(input, self.embedding_table.table, None, T,
+                               out_shape=(B, T, self.embedding_table.embed_size), scale=self.scale)
         return self.output
