@@ -151,6 +151,73 @@ def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None):
     return table
 
 
+def gemma_bench(xp, prefill_reps=3, decode_steps=128):
+    """Gemma-style bf16 decoder (2.5B weights, device-seeded N(0,0.02)):
+    prefill B=4 x T=2048 into the KV cache, then `decode_steps` greedy steps at M=4 whose
+    ids are fed back on the device. Decode is weight-streaming: every step reads all
+    GEMM weights once (the packed [N, K] copies) plus the live KV cache."""
+    import gemma
+    cfg = gemma.GEMMA_2B
+    B, T = 4, 2048
+    log("building Gemma-style config-5 model (bf16, device-seeded)")
+    model = gemma.build_gemma(cfg, "bf16")
+    gemma.seed_gemma(model, 0, 0.02, device=True)
+    ids = xp.array(np.random.default_rng(2).integers(0, cfg["vocab"], (B, T)).astype(np.int32))
+    cache = model.new_cache(B, T + decode_steps)
+    model.forward(ids, cache, 0)  # warm-up; packs every weight once
+    xp.synchronize()
+    e0, e1 = xp.Event(), xp.Event()
+    e0.record()
+    for _ in range(prefill_reps):
+        logits = model.forward(ids, cache, 0)
+    e1.record()
+    prefill_ms = e0.elapsed_ms(e1) / prefill_reps
+    C, F, V, L = cfg["d"], cfg["ffn"], cfg["vocab"], cfg["layers"]
+    Hq, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    M = B * T
+    dense_w = L * (C * (Hq + 2 * Hkv) * D + Hq * D * C + C * 2 * F + F * C)
+    attn = L * B * Hq * 2 * 2 * D * (T * (T + 1) / 2)  # causal QK^T and PV
+    prefill_flops = 2 * M * (dense_w + C * V) + attn
+
+    def step(nxt, pos):
+        lg = model.forward(nxt.reshape(B, 1), cache, pos)
+        return xp.argmax(model.last_rows(lg))
+
+    nxt = xp.argmax(model.last_rows(logits))
+    for w in range(3):  # warm-up decode steps (positions rewritten by the timed loop)
+        step(nxt, T + w)
+    xp.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for t in range(decode_steps):
+        nxt = step(nxt, T + t)
+    e1.record()
+    xp.synchronize()
+    wall = (time.perf_counter() - t0) / decode_steps * 1e3
+    decode_ms = e0.elapsed_ms(e1) / decode_steps
+    w_bytes = 2.0 * (dense_w + C * V)
+    kv_bytes = 2.0 * L * B * Hkv * D * 2 * (T + decode_steps / 2)
+    out = {
+        "workload": "Gemma-style decoder (BASELINE config 5): vocab 256000, 18 layers, d 2048, "
+                    "8 q heads / 1 kv head of 256, GeGLU FFN 16384; bf16, weights N(0,0.02) "
+                    "device-seeded; prefill B=4 T=2048, then greedy decode with KV cache",
+        "prefill_ms": round(prefill_ms, 3),
+        "prefill_tokens_per_s": round(M / (prefill_ms * 1e-3), 1),
+        "prefill_tflops": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 1),
+        "prefill_flops": prefill_flops,
+        "decode_steps": decode_steps,
+        "decode_ms_per_step": round(decode_ms, 4),
+        "decode_wall_ms_per_step": round(wall, 4),
+        "decode_tokens_per_s": round(B / (decode_ms * 1e-3), 1),
+        "decode_bytes_per_step": w_bytes + kv_bytes,
+        "decode_hbm_gbs": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9, 1),
+        "decode_hbm_frac": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+    }
+    log(f"gemma config 5: {json.dumps(out)}")
+    del model, cache, logits
+    return out
+
+
 def cpu_baseline(sample_seqs=5, sample_T=SEQ):
     """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
     of the workload: `sample_seqs` sequences of T tokens of the same model."""
@@ -181,6 +248,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-row-kernels", action="store_true")
+    ap.add_argument("--no-gemma", action="store_true", help="skip the config-5 decoder section")
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
@@ -261,6 +329,7 @@ def main():
                 "traffic": None}
 
     rows = {} if args.no_row_kernels else row_kernel_bench(xp)
+    gem = None if args.no_gemma else gemma_bench(xp)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -280,6 +349,7 @@ def main():
         "gemm_flops_per_step": {"dense": dense, "lm_head": head, "attention_full": attn},
         "kernel_breakdown": breakdown,
         "row_kernels": rows,
+        "gemma_decoder": gem,
     }
     print(json.dumps(line), flush=True)
 

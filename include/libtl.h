@@ -169,6 +169,11 @@ int tl_kprof_query(tl_ctx* ctx, int family, int64_t* launches, double* total_ms,
  * Replaces init_zeros_tensor (reference backend.py:33-34). */
 int tl_fill(tl_ctx* ctx, void* y, int64_t n, int32_t dtype, double value);
 int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dtype_x, int32_t dtype_y);
+/* y[e] = mean + std * N(0,1), drawn on the device: Philox4x32-10 keyed by `seed` with
+ * counter (e / 4, stream), Box-Muller on its output word pairs. Replaces
+ * init_random_tensor's draw (reference backend.py:27-31, a device draw under CuPy). */
+int tl_random_normal(tl_ctx* ctx, void* y, int64_t n, uint64_t seed, uint64_t stream,
+                     float mean, float std_dev, int32_t dtype);
 /* y[c*ldy + r] = x[r*ldx + c]: weight pre-packing into the K-contiguous GEMM layout. */
 int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t ldy, int32_t dtype);

@@ -32,6 +32,9 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
   gpt_forward      brute-force float64 composition of the above at a tiny shape (golden
                    fixture)
   bf16 rounding    hand-computed bit patterns (ties to even, NaN, inf)
+  philox4x32_10    the published known-answer vectors of Random123 (zero, all-ones and
+                   pi-digit counters/keys)
+  random_normal    moments of a large draw; Box-Muller radius/angle identities
 The reference itself was not imported or run: its files are pure Python over CuPy/NumPy
 with no golden vectors, and every function above is pinned by the checks listed.
 """
@@ -377,3 +380,41 @@ def gemma_greedy(ids, params, cfg, n_new, bf16=False):
         rows.append(last)
         seq = np.concatenate([seq, nxt[:, None]], axis=1)
     return np.stack(new, axis=1), np.stack(rows)
+
+
+# ---- device random numbers (Philox4x32-10 + Box-Muller) --------------------------------
+def philox4x32_10(ctr, key):
+    """Philox4x32-10 (Salmon et al., SC 2011). ctr uint32 [..., 4], key uint32 [2] ->
+    uint32 [..., 4]. Each round: (lo0, hi0) = M0 * c0, (lo1, hi1) = M1 * c2,
+    c = (hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0); then the key is bumped by the Weyl
+    constants."""
+    mask = np.uint64(0xFFFFFFFF)
+    ctr = np.asarray(ctr, dtype=np.uint64)
+    c = [ctr[..., i] for i in range(4)]
+    k0, k1 = np.uint64(int(key[0])), np.uint64(int(key[1]))
+    m0, m1 = np.uint64(0xD2511F53), np.uint64(0xCD9E8D57)
+    for _ in range(10):
+        p0, p1 = m0 * c[0], m1 * c[2]
+        c = [((p1 >> np.uint64(32)) ^ c[1] ^ k0) & mask, p1 & mask,
+             ((p0 >> np.uint64(32)) ^ c[3] ^ k1) & mask, p0 & mask]
+        k0 = (k0 + np.uint64(0x9E3779B9)) & mask
+        k1 = (k1 + np.uint64(0xBB67AE85)) & mask
+    return np.stack(c, axis=-1).astype(np.uint32)
+
+
+def random_normal(n, seed, stream=0, mean=0.0, std=1.0):
+    """Element e: Philox counter (e // 4 as two words, stream as two words), key = seed;
+    Box-Muller on output words (0, 1) and (2, 3) with 24-bit uniforms
+    u1 = (w >> 8 + 1) 2^-24, u2 = (w >> 8) 2^-24. Evaluated in float64, returned float32."""
+    g = np.arange((n + 3) // 4, dtype=np.uint64)
+    ctr = np.stack([g & np.uint64(0xFFFFFFFF), g >> np.uint64(32),
+                    np.full_like(g, stream & 0xFFFFFFFF), np.full_like(g, stream >> 32)], -1)
+    w = philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32)).astype(np.float64)
+    out = np.empty((g.size, 4))
+    for a, b in ((0, 1), (2, 3)):
+        u1 = (np.floor(w[:, a] / 256) + 1) * 2.0 ** -24
+        u2 = np.floor(w[:, b] / 256) * 2.0 ** -24
+        r = np.sqrt(-2 * np.log(u1))
+        out[:, a] = r * np.cos(2 * np.pi * u2)
+        out[:, b] = r * np.sin(2 * np.pi * u2)
+    return (mean + std * out.reshape(-1)[:n]).astype(F32)

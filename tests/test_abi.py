@@ -27,6 +27,48 @@ def test_header_declares_the_binding_table():
     assert header_functions() == sorted(tl_hip.SIGNATURES)
 
 
+def _ctype_of(decl):
+    """C parameter declaration -> the ctypes type the binding must use."""
+    import ctypes as C
+    decl = re.sub(r"\bconst\b", "", decl).strip()
+    if "*" in decl:
+        base = decl.split("*")[0].strip()
+        stars = decl.count("*")
+        scalar = {"int": C.c_int, "int64_t": C.c_int64, "size_t": C.c_size_t,
+                  "float": C.c_float, "double": C.c_double}
+        if stars == 1 and base in scalar:
+            return ("ptr", scalar[base])
+        return ("ptr", None)
+    base = decl.rsplit(" ", 1)[0].strip()
+    return {"int": C.c_int, "int32_t": C.c_int32, "int64_t": C.c_int64, "uint32_t": C.c_uint32,
+            "uint64_t": C.c_uint64, "size_t": C.c_size_t, "float": C.c_float,
+            "double": C.c_double}[base]
+
+
+def test_binding_argument_types_match_the_header():
+    """Every prototype's parameter types, position by position, against SIGNATURES."""
+    import ctypes as C
+    import tl_hip
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    protos = re.findall(r"\b(?:int|const char\*)\s+(tl_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text)
+    assert sorted(n for n, _ in protos) == sorted(tl_hip.SIGNATURES)
+    for name, params in protos:
+        params = params.strip()
+        decls = [] if params in ("", "void") else [p.strip() for p in params.split(",")]
+        got = tl_hip.SIGNATURES[name]
+        assert len(decls) == len(got), name
+        for i, (d, t) in enumerate(zip(decls, got)):
+            want = _ctype_of(d)
+            if isinstance(want, tuple):
+                if want[1] is None:
+                    assert t is C.c_void_p or issubclass(t, C._Pointer), (name, i, d)
+                else:
+                    assert t is C.c_void_p or t == C.POINTER(want[1]), (name, i, d)
+            else:
+                assert C.sizeof(t) == C.sizeof(want) and (t in (C.c_float, C.c_double)) == \
+                    (want in (C.c_float, C.c_double)), (name, i, d, t, want)
+
+
 @needs_lib
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(LIB)

@@ -279,3 +279,42 @@ def test_gemma_decode_bf16_matches_prefill(tl):
         assert ref.max_rel(rows[t], full) <= 2e-2
     want = ref.gemma_forward(ids[:1], ref.gemma_params(cfg, 15, 0.05, bf16=True), cfg, bf16=True)
     assert ref.max_rel(rows[0][:1], want[:, -1]) <= 2e-2
+
+
+def _device_params(model, cfg):
+    """Download the device-seeded parameters under the oracle's names."""
+    names = [n for n, _ in ref.gemma_param_shapes(cfg)]
+    params = [p for layer in model.layers for p in layer.parameters]
+    assert len(names) == len(params)
+    return {n: p.get() for n, p in zip(names, params)}
+
+
+def test_gemma_full_width_one_layer_bf16(tl):
+    """Config 5 widths (d 2048, 8 query heads of 256 sharing one kv head, FFN 16384, vocab
+    256000) with one layer, device-seeded N(0, 0.02) weights, against the oracle."""
+    g = tl["gemma"]
+    cfg = dict(g.GEMMA_2B, layers=1)
+    model = g.build_gemma(cfg, "bf16")
+    g.seed_gemma(model, 21, 0.02, device=True)
+    ids = np.random.default_rng(22).integers(0, cfg["vocab"], (1, 64))
+    got = model.forward(ids).get()
+    want = ref.gemma_forward(ids, _device_params(model, cfg), cfg, bf16=True)
+    assert ref.max_rel(got, want) <= 2e-2
+    assert np.array_equal(tl["xp"].argmax(model.back.output).get(), np.argmax(got, -1))
+
+
+def test_gemma_config5_full_shape_decode_bf16(tl):
+    """BASELINE config 5 at full size: 18 layers, 2.5B device-seeded bf16 weights, prefill
+    B=4, T=2048 into the KV cache, then greedy steps. Every cached step's logits equal the
+    last row of a fresh prefill over the same tokens, and the ids are the device argmax of
+    those rows. (The whole model is beyond the CPU oracle; its layers are pinned above.)"""
+    g = tl["gemma"]
+    model = g.build_gemma(g.GEMMA_2B, "bf16")
+    g.seed_gemma(model, 23, 0.02, device=True)
+    ids = np.random.default_rng(24).integers(0, 256000, (4, 2048))
+    new, rows = model.generate_greedy(ids, 4, return_logits=True)
+    assert new.shape == (4, 4) and np.array_equal(new, np.argmax(rows, -1).T)
+    assert np.all(np.isfinite(rows))
+    seq = np.concatenate([ids, new], axis=1)
+    fresh = model.last_rows(model.forward(seq[:, :2051])).get()
+    assert ref.max_rel(rows[3], fresh) <= 2e-2

@@ -413,3 +413,26 @@ def test_attention_fused_rejects_unsupported(xp):
     with pytest.raises(xp.TLError):
         xp.attention(q32, q32, xp.empty((1, 1, 64, 16), "fp32"), xp.empty((1, 16, 64), "fp32"),
                      n_heads_q=1, n_heads_kv=1, divisor=8.0)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("n", [1, 7, 4096, 1000003])
+def test_random_normal_matches_philox_oracle(xp, dt, n):
+    seed, stream = 0x1234_5678_9ABC, 11
+    got = xp.random_normal((n,), seed, stream, mean=0.5, std=2.0, dtype=dt).get()
+    want = ref.random_normal(n, seed, stream, 0.5, 2.0).astype(np.float64)
+    if dt == "fp32":
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+    else:
+        # fp32 evaluation then one bf16 rounding: within one bf16 ulp of the oracle
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-5)
+
+
+def test_random_normal_prefix_and_streams(xp):
+    a = xp.random_normal((1000,), 3, 0).get()
+    b = xp.random_normal((10, 10), 3, 0).get().reshape(-1)
+    assert np.array_equal(a[:100], b)
+    c = xp.random_normal((1000,), 3, 1).get()
+    assert not np.allclose(a, c)
+    big = xp.random_normal((1 << 24,), 9, 2).get().astype(np.float64)
+    assert abs(big.mean()) < 2e-3 and abs(big.std() - 1) < 2e-3

@@ -343,3 +343,32 @@ def test_gemma_cached_forward_and_greedy_consistency():
     # embedding scale: the first layer sees table[ids] * sqrt(d)
     x0 = P["table"][ids] * np.sqrt(F32(32))
     assert np.allclose(np.sqrt(np.mean(x0 ** 2)), np.sqrt(np.mean(P["table"] ** 2)) * np.sqrt(32), rtol=0.3)
+
+
+# ---- Philox / normal draws ----------------------------------------------------------------
+def test_philox_known_answer_vectors():
+    """Random123's known-answer vectors for philox4x32-10."""
+    cases = [
+        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+        ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+         [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1]),
+    ]
+    for ctr, key, want in cases:
+        got = ref.philox4x32_10(np.array(ctr, np.uint32), key)
+        assert [int(v) for v in got] == want
+
+
+def test_random_normal_moments_and_structure():
+    z = ref.random_normal(1_000_003, seed=1234, stream=7).astype(np.float64)
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1) < 5e-3
+    assert abs(np.mean(z ** 3)) < 2e-2 and abs(np.mean(z ** 4) - 3) < 3e-2
+    # pairs share a radius: z0^2 + z1^2 = -2 ln u1 from word 0 of the same counter
+    w = ref.philox4x32_10(np.array([[0, 0, 7, 0]], np.uint32), (1234, 0))[0]
+    u1 = ((int(w[0]) >> 8) + 1) * 2.0 ** -24
+    assert math.isclose(z[0] ** 2 + z[1] ** 2, -2 * math.log(u1), rel_tol=1e-5)
+    # seed and stream select different draws; mean/std are affine
+    assert not np.allclose(ref.random_normal(16, 1, 0), ref.random_normal(16, 2, 0))
+    assert not np.allclose(ref.random_normal(16, 1, 0), ref.random_normal(16, 1, 1))
+    np.testing.assert_allclose(ref.random_normal(10, 5, 3, 1.0, 0.02),
+                               1.0 + 0.02 * ref.random_normal(10, 5, 3), rtol=1e-6)

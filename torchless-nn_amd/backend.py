@@ -34,14 +34,13 @@ def set_float_type(dtype):
 
 
 def init_random_tensor(size, divisor=None):
-    """N(0,1) of `size` in FLOAT_TYPE, optionally divided by `divisor` (in fp32, on the
-    host before upload; the reference divides on the device right after drawing)."""
-    import numpy as np
-    host = rng._g.standard_normal(tuple(size) if not isinstance(size, int) else (size,),
-                                  dtype=np.float32)
-    if divisor is not None:
-        host = host / np.float32(divisor)
-    return xp.array(host, dtype=FLOAT_TYPE)
+    """N(0,1) / divisor of `size` in FLOAT_TYPE, drawn on the device as the reference's
+    CuPy runtime does (backend.py:27-31): a Philox draw whose key comes from the seeded
+    host generator `rng`, so TL_SEED makes initialisation reproducible."""
+    key = int(rng._g.integers(0, 2 ** 63))
+    std = 1.0 / float(divisor) if divisor is not None else 1.0
+    return xp.random_normal(tuple(size) if not isinstance(size, int) else (size,), key, 0,
+                            std=std, dtype=FLOAT_TYPE)
 
 
 def init_zeros_tensor(size):

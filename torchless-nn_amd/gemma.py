@@ -90,11 +90,17 @@ def build_gemma(cfg, dtype=None):
     return GemmaDecoder(cfg)
 
 
-def seed_gemma(model, seed, scale=0.02):
+def seed_gemma(model, seed, scale=0.02, device=False):
     """Overwrite all parameters, in layer order, with seeded N(0,1)*scale (the RMSNorm
-    gammas too: they scale by 1 + gamma)."""
+    gammas too: they scale by 1 + gamma). device=False draws on the host from
+    numpy default_rng(seed) (what the parity tests mirror); device=True draws on the GPU
+    with Philox keyed by seed, stream = the parameter's index (seconds for 2.5B weights)."""
+    params = [p for layer in model.layers for p in layer.parameters]
+    if device:
+        for i, p in enumerate(params):
+            xp.random_normal(p.shape, seed, stream=i, std=scale, out=p)
+        return model
     rng = np.random.default_rng(seed)
-    for layer in model.layers:
-        for p in layer.parameters:
-            p.set(rng.standard_normal(p.shape, dtype=np.float32) * np.float32(scale))
+    for p in params:
+        p.set(rng.standard_normal(p.shape, dtype=np.float32) * np.float32(scale))
     return model

@@ -161,6 +161,7 @@ SIGNATURES = {
                        ctypes.POINTER(_F64), ctypes.POINTER(_F64)],
     "tl_fill": [_P, _P, _I64, _I32, _F64],
     "tl_cast": [_P, _P, _P, _I64, _I32, _I32],
+    "tl_random_normal": [_P, _P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F32, _F32, _I32],
     "tl_transpose2d": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
     "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32],
@@ -481,6 +482,21 @@ def argmax(t: DeviceTensor, axis=-1) -> DeviceTensor:
     out = DeviceTensor(t.shape[:-1] if t.ndim > 1 else (1,), int64)
     c = ctx()
     check(c.lib.tl_argmax(c.handle, t.ptr, t.nrows, t.ncols, t.pitch, t.dtype.code, out.ptr))
+    return out
+
+
+def random_normal(shape, seed, stream=0, mean=0.0, std=1.0, dtype=float32, out=None) -> DeviceTensor:
+    """mean + std * N(0, 1) drawn on the device (Philox4x32-10 keyed by `seed`, counter
+    stream `stream`, Box-Muller). Same (seed, stream) -> same values for any dtype/shape
+    prefix. `out` (contiguous) is filled in place."""
+    out = out if out is not None else DeviceTensor(shape, dtype)
+    if not out.contiguous:
+        raise ValueError("random_normal needs a contiguous tensor")
+    c = ctx()
+    check(c.lib.tl_random_normal(c.handle, out.ptr, out.size, int(seed) & (2 ** 64 - 1),
+                                 int(stream) & (2 ** 64 - 1), float(mean), float(std),
+                                 out.dtype.code))
+    out._version += 1
     return out
 
 
