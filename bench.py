@@ -195,6 +195,19 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
     xp.synchronize()
     wall = (time.perf_counter() - t0) / decode_steps * 1e3
     decode_ms = e0.elapsed_ms(e1) / decode_steps
+    # per-family kernel time of the decode steps (HIP events around every launch)
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    n_prof = 16
+    for t in range(n_prof):
+        nxt = step(nxt, T + t)
+    xp.synchronize()
+    fam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
+    decode_breakdown = {f: {"ms_per_step": round(r["ms"] / n_prof, 4),
+                            "launches_per_step": r["launches"] // n_prof,
+                            "gbs": round(r["bytes"] / (r["ms"] * 1e-3) / 1e9, 1)}
+                        for f, r in fam.items() if r["launches"]}
     w_bytes = 2.0 * (dense_w + C * V)
     kv_bytes = 2.0 * L * B * Hkv * D * 2 * (T + decode_steps / 2)
     out = {
@@ -212,9 +225,62 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
         "decode_bytes_per_step": w_bytes + kv_bytes,
         "decode_hbm_gbs": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9, 1),
         "decode_hbm_frac": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "decode_kernel_breakdown": decode_breakdown,
     }
     log(f"gemma config 5: {json.dumps(out)}")
     del model, cache, logits
+    return out
+
+
+def decode_sweep(xp, reps=50):
+    """Times each GEMM of a config-5 decode step (M = 4) and one layer's decode attention,
+    in GB/s of algorithmic bytes (weights + activations; K and V for attention)."""
+    rng = np.random.default_rng(0)
+    B, C, F, V, D, Hq = 4, 2048, 16384, 256000, 256, 8
+    Tk, L = 2176, 2176
+
+    def dev(shape, scale=0.02):
+        return xp.random_normal(shape, int(rng.integers(1 << 30)), 0, std=scale, dtype="bf16")
+
+    x, h = dev((B, C), 1.0), dev((B, F), 1.0)
+    res = dev((B, C), 1.0)
+    w = {"qkv": dev((10 * D, C)), "out": dev((C, C)), "geglu": dev((2 * F, C)),
+         "down": dev((C, F)), "head": dev((V, C))}
+    q, k, vt = (xp.empty((B, Hq, 1, D), "bf16"), dev((B, 1, L, D), 1.0), dev((B, 1, D, L), 1.0))
+    outc, outf = xp.empty((B, C), "bf16"), xp.empty((B, F), "bf16")
+    logits = xp.empty((B, V), "bf16", pitch=V)
+    heads = xp.empty((B, Hq * D), "bf16")
+    gam, xn = dev((C,)), xp.empty((B, C), "bf16")
+    cases = {
+        "qkv": (lambda: xp.gemm(x, w["qkv"], M=B, N=10 * D, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                qkv=(q, k, vt, 1, Hq, 1, D, L, 2100)), 2 * 10 * D * C),
+        "out": (lambda: xp.gemm(x, w["out"], M=B, N=C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                C=outc, ldc=C, residual=res, ldr=C), 2 * C * C),
+        "geglu": (lambda: xp.gemm(x, w["geglu"], M=B, N=2 * F, K=C, lda=C, ldb=C,
+                                  b_layout=xp.TL_B_NK, C=outf, ldc=F, act=xp.TL_ACT_GELU,
+                                  geglu=True), 2 * 2 * F * C),
+        "down": (lambda: xp.gemm(h, w["down"], M=B, N=C, K=F, lda=F, ldb=F, b_layout=xp.TL_B_NK,
+                                 C=outc, ldc=C, residual=res, ldr=C), 2 * C * F),
+        "head": (lambda: xp.gemm(x, w["head"], M=B, N=V, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
+                                 C=logits, ldc=V), 2 * V * C),
+        "rmsnorm_4x2048": (lambda: xp.rmsnorm(x, gam, np.float32(1e-6), 1.0, out=xn), 2 * 2 * B * C),
+        "attention": (lambda: xp.attention(q, k, vt, heads, n_heads_q=Hq, n_heads_kv=1,
+                                           divisor=16.0, causal=True, offset=Tk - 1, seq_k=Tk),
+                      2 * 2 * B * Tk * D),
+    }
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(3):
+            fn()
+        e0, e1 = xp.Event(), xp.Event()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        us = e0.elapsed_ms(e1) / reps * 1e3
+        out[name] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    log(f"decode sweep (skinny cfg {os.environ.get('TL_SKINNY_CFG', '0')}, attention cfg "
+        f"{os.environ.get('TL_ATTN_DECODE_CFG', '0')}): {json.dumps(out)}")
     return out
 
 
@@ -252,6 +318,8 @@ def main():
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
+    ap.add_argument("--sweep-decode", action="store_true",
+                    help="only time the config-5 decode-step GEMMs and attention")
     ap.add_argument("--sweep-tiles", default="", help="comma list of tiles for --sweep-gemm")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
@@ -273,6 +341,9 @@ def main():
         xp.synchronize()
         del src, dst
         log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
+    if args.sweep_decode:
+        print(json.dumps({"decode_sweep": decode_sweep(xp)}), flush=True)
+        return
     if args.sweep_gemm:
         print(json.dumps({"gemm_sweep": gemm_sweep(
             xp, only_shapes=[x for x in args.sweep_shapes.split(",") if x],

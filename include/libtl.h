@@ -80,7 +80,10 @@ enum tl_gemm_tile {
   TL_TILE_DMA_128x128_S3 = 11, /* 3 stages */
   /* persistent direct-to-LDS variants (one workgroup per resident slot; batch 1) */
   TL_TILE_PERSIST_256x128_W8 = 12,
-  TL_TILE_PERSIST_128x128 = 13
+  TL_TILE_PERSIST_128x128 = 13,
+  /* weight streaming for M <= 16 (decode steps): 16 rows of B per workgroup, K split over
+   * its 8 waves; chosen by TL_TILE_AUTO whenever M <= 16 */
+  TL_TILE_SKINNY = 14
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

@@ -351,6 +351,70 @@ def test_gemm_every_tile_shape(xp, tile, mnk):
     assert ref.max_rel(vt.get(), y[..., (Hq + Hkv) * D:].reshape(2, T, Hkv, D).transpose(0, 2, 3, 1)) <= 2e-2
 
 
+@pytest.mark.parametrize("mnk", [(1, 1, 8), (4, 15, 40), (4, 2560, 2048), (16, 2048, 16384),
+                                 (7, 50257, 64), (3, 300, 776)])
+@pytest.mark.parametrize("out_dt", ["bf16", "fp32"])
+def test_gemm_skinny_decode_rows(xp, mnk, out_dt):
+    """The weight-streaming kernel (M <= 16, chosen automatically) on ragged N and a K that
+    splits unevenly over its waves, with bias, GeLU and residual."""
+    M, N, K = mnk
+    rng = np.random.default_rng(M * 31 + N + K)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+    wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    res = rng.standard_normal((M, N)).astype(F32)
+    res = ref.round_bf16(res) if out_dt == "bf16" else res
+    ldc = (N + 7) // 8 * 8
+    out = xp.empty((M, N), out_dt, pitch=ldc)
+    dres = xp.empty((M, N), out_dt, pitch=ldc)
+    dres.set(res)
+    for tile in ("auto", "skinny"):
+        xp.gemm(up(xp, a, "bf16"), up(xp, wt, "bf16"), M=M, N=N, K=K, lda=K, ldb=K,
+                b_layout=xp.TL_B_NK, C=out, ldc=ldc, out_dtype=out_dt,
+                bias=up(xp, bias, "bf16"), act=xp.TL_ACT_GELU, residual=dres, ldr=ldc,
+                tile=tile)
+        want = gemm_ref(a, wt.T, bias, "gelu", res)
+        tol = 2e-2 if out_dt == "bf16" else 1e-5
+        assert ref.max_rel(out.get(), want) <= tol, (mnk, out_dt, tile)
+
+
+@pytest.mark.parametrize("C", [512, 2048])
+def test_gemm_skinny_qkv_cache_and_gated(xp, C):
+    """Decode-step epilogues through the skinny kernel: QKV scatter into a cache at a
+    position offset (T = 1, B = 4) and the gated GeGLU pairs; C = 2048 splits K over
+    workgroups (the last one to finish runs the epilogue)."""
+    rng = np.random.default_rng(77 + C)
+    B, Hq, Hkv, D, L, pos = 4, 8, 1, 256, 40, 17
+    N = (Hq + 2 * Hkv) * D
+    x = ref.round_bf16(rng.standard_normal((B, C)).astype(F32))
+    w = ref.round_bf16(rng.standard_normal((N, C)).astype(F32) / np.sqrt(C))
+    q = xp.empty((B, Hq, 1, D), "bf16")
+    k, vt = xp.zeros((B, Hkv, L, D), "bf16"), xp.zeros((B, Hkv, D, L), "bf16")
+    xp.gemm(up(xp, x, "bf16"), up(xp, w, "bf16"), M=B, N=N, K=C, lda=C, ldb=C,
+            b_layout=xp.TL_B_NK, qkv=(q, k, vt, 1, Hq, Hkv, D, L, pos))
+    y = gemm_ref(x, w.T)
+    assert ref.max_rel(q.get()[:, :, 0].reshape(B, Hq * D), y[:, :Hq * D]) <= 2e-2
+    assert ref.max_rel(k.get()[:, 0, pos], y[:, Hq * D:(Hq + 1) * D]) <= 2e-2
+    assert ref.max_rel(vt.get()[:, 0, :, pos], y[:, (Hq + 1) * D:]) <= 2e-2
+    assert not np.any(k.get()[:, :, :pos]) and not np.any(vt.get()[:, :, :, pos + 1:])
+    F = 3000
+    wg = ref.round_bf16(rng.standard_normal((2 * F, C)).astype(F32) / np.sqrt(C))
+    h = xp.empty((B, F), "bf16")
+    xp.gemm(up(xp, x, "bf16"), up(xp, wg, "bf16"), M=B, N=2 * F, K=C, lda=C, ldb=C,
+            b_layout=xp.TL_B_NK, C=h, ldc=F, act=xp.TL_ACT_GELU, geglu=True)
+    t = gemm_ref(x, wg.T)
+    want = ref.gelu(t[:, 0::2].astype(F32)) * t[:, 1::2]
+    assert ref.max_rel(h.get(), want) <= 2e-2
+
+
+def test_gemm_skinny_rejects_tall(xp):
+    a = xp.zeros((17, 64), "bf16")
+    w = xp.zeros((32, 64), "bf16")
+    with pytest.raises(xp.TLError):
+        xp.gemm(a, w, M=17, N=32, K=64, lda=64, ldb=64, b_layout=xp.TL_B_NK,
+                C=xp.empty((17, 32), "bf16"), ldc=32, tile="skinny")
+
+
 # ---- fused attention ---------------------------------------------------------------------
 def attention_ref(q, k, vt, Hq, Hkv, divisor, causal, offset):
     """float64 scores / divisor, -inf above the (offset) diagonal, softmax, times V; out
@@ -404,6 +468,31 @@ def test_attention_fused_grouped_heads_and_offset(xp, heads):
     assert ref.max_rel(out.get(), want) <= 2e-2
 
 
+@pytest.mark.parametrize("case", [
+    # B, Hq, Hkv, Tq, Tk, Lk, D, causal, offset
+    (4, 8, 1, 1, 2049, 2056, 256, True, 2048),
+    (2, 4, 2, 2, 300, 304, 64, True, 298),
+    (1, 16, 16, 1, 77, 80, 32, False, 0),
+    (3, 8, 1, 2, 1000, 1024, 128, True, 998),
+    (1, 8, 1, 1, 1, 8, 64, True, 0),
+    (2, 2, 1, 8, 600, 640, 256, True, 592),
+])
+def test_attention_decode_split_kv(xp, case):
+    """Few query rows per kv head (decode): split-KV kernel + combine, keys read from a cache
+    of capacity Lk whose first Tk positions are valid (the rest hold other finite values)."""
+    B, Hq, Hkv, Tq, Tk, Lk, D, causal, offset = case
+    rng = np.random.default_rng(Tk + D)
+    q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, Hkv, Lk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=divisor, causal=causal, offset=offset, seq_k=Tk)
+    want = attention_ref(q, k[:, :, :Tk], vt[:, :, :, :Tk], Hq, Hkv, divisor, causal, offset)
+    assert ref.max_rel(out.get(), want) <= 2e-2, case
+
+
 def test_attention_fused_rejects_unsupported(xp):
     q = xp.empty((1, 1, 12, 64), "bf16").fill(0)
     with pytest.raises(xp.TLError):
@@ -436,3 +525,44 @@ def test_random_normal_prefix_and_streams(xp):
     assert not np.allclose(a, c)
     big = xp.random_normal((1 << 24,), 9, 2).get().astype(np.float64)
     assert abs(big.mean()) < 2e-3 and abs(big.std() - 1) < 2e-3
+
+
+def test_argmax_split_rows_ties_and_nan(xp):
+    """Few long rows take the column-split path: ties resolve to the first index across
+    slices, and the first NaN wins, as np.argmax."""
+    R, V = 4, 256000
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((R, V)).astype(F32)
+    x[0, 100] = x[0, 200000] = 50.0           # tie across slices -> 100
+    x[1, 255999] = 60.0                        # max in the last column
+    x[2, 7] = 70.0
+    x[2, 130000] = np.nan                      # NaN beats the max
+    x[3, 9000] = np.nan
+    x[3, 250000] = np.nan                      # first NaN
+    for dt in ("fp32", "bf16"):
+        d = xp.empty((R, V), dt, pitch=V + 8)
+        d.set(x)
+        got = xp.argmax(d).get()
+        host = ref.round_bf16(x) if dt == "bf16" else x
+        assert got.tolist() == np.argmax(host, -1).tolist() == [100, 255999, 130000, 9000]
+
+
+def test_gemm_skinny_split_sequence(xp):
+    """Back-to-back skinny GEMMs whose K splits differ (1, 2, 4, 8 workgroups per row block)
+    share the split scratch: every result is checked."""
+    rng = np.random.default_rng(90)
+    shapes = [(4, 2048, 16384), (4, 256, 2048), (16, 2560, 2048), (2, 4096, 4096), (4, 64, 8192)]
+    ops = []
+    for M, N, K in shapes:
+        a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+        wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+        ops.append((M, N, K, up(xp, a, "bf16"), up(xp, wt, "bf16"), gemm_ref(a, wt.T)))
+    for it in range(3):
+        outs = []
+        for M, N, K, da, dw, want in ops:
+            out = xp.empty((M, N), "bf16")
+            xp.gemm(da, dw, M=M, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK, C=out, ldc=N)
+            outs.append((out, want))
+        for out, want in outs:
+            assert ref.max_rel(out.get(), want) <= 2e-2, it
+

@@ -204,6 +204,223 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Decode (split-KV) attention for a few query rows per kv head: the query rows that share a
+// kv head (Hq / Hkv heads x Tq positions, at most 16) form one MFMA column block, so every
+// key and value is read once per kv head rather than once per query head; the key range is
+// split over many workgroups so the cache streams from HBM in parallel (flash-decoding,
+// Dao et al. 2023). Each wave takes 64 keys and keeps its scores, probabilities and P.V in
+// registers with the same layouts as attention_fwd_kernel (K fragments and V^T fragments are
+// read straight from global memory: each is used by one MFMA of one wave). The 4 waves of a
+// workgroup merge their (max, sum, O) in LDS and write one partial per workgroup;
+// attention_combine_kernel rescales the partials by their maxima and writes O / l.
+// ---------------------------------------------------------------------------------------
+struct DecodeWs {
+  float* o;   // [B*Hkv][nblk][16][D] unnormalised partial outputs
+  float* ml;  // [B*Hkv][nblk][16][2] (max in log2 units, sum)
+  int nblk;
+};
+
+template <int D, int NW, int J>
+__global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p, DecodeWs w) {
+  static_assert(J == 2 || J == 4, "16-key tiles per wave: 2 or 4");
+  constexpr int KS = D / 32, DT = D / 16, KPW = 16 * J;
+  __shared__ float sm[NW][16], sl[NW][16];
+  __shared__ f32x4 so[NW][DT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int bh = blockIdx.y;
+  const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
+  const int g = p.Hq / p.Hkv;
+  const int R = g * p.Tq;
+  const bool rowok = col < R;
+  const int jh = rowok ? col / p.Tq : 0, t = rowok ? col - jh * p.Tq : 0;
+  const int64_t qpos = (int64_t)t + p.offset;
+  const bf16x8 zero = {};
+
+  bf16x8 qf[KS];
+  {
+    const bf16_t* qrow = p.q + ((int64_t)(b * p.Hq + hk * g + jh) * p.Tq + t) * D + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = rowok ? *reinterpret_cast<const bf16x8*>(qrow + 32 * ks) : zero;
+  }
+  const bf16_t* kh = p.k + (int64_t)bh * p.Lk * D;
+  const bf16_t* vh = p.vt + (int64_t)bh * D * p.Lk;
+  const int kc0 = (blockIdx.x * NW + wave) * KPW;
+
+  // S^T = K Q^T for J tiles of 16 keys: lane holds keys kc0 + 16 j + 4 grp + i of row col
+  f32x4 s[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int key = kc0 + 16 * j + col;
+    const bool kin = key < p.Tk;
+    const bf16_t* krow = kh + (int64_t)(kin ? key : 0) * D + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bf16x8 kf = kin ? *reinterpret_cast<const bf16x8*>(krow + 32 * ks) : zero;
+      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kc0 + 16 * j + 4 * grp + i;
+      const bool ok = rowok && key < p.Tk && (!p.causal || (int64_t)key <= qpos);
+      const float x = ok ? s[j][i] * p.scale_log2 : -INFINITY;
+      s[j][i] = x;
+      mx = fmaxf(mx, x);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[j][i] - mx);
+      s[j][i] = e;
+      sum += e;
+    }
+  sum += __shfl_xor(sum, 16, 64);
+  sum += __shfl_xor(sum, 32, 64);
+
+  // O^T = V^T P^T: B operand = this lane's 8 probabilities (keys 32 hp + 4 grp + 0..3 and
+  // 32 hp + 16 + 4 grp + 0..3), A operand = V^T rows read with the same key order
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int hp = 0; hp < J / 2; ++hp) {
+    bf16x8 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pf[i] = (__bf16)s[2 * hp][i];
+      pf[4 + i] = (__bf16)s[2 * hp + 1][i];
+    }
+    const int ka = kc0 + 32 * hp + 4 * grp, kb = ka + 16;
+    const bool ina = ka < p.Tk, inb = kb < p.Tk;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
+      const uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
+      const uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
+    }
+  }
+
+  // merge the 4 waves: rows col, head-dim 16 dt + 4 grp + i
+  if (grp == 0) {
+    sm[wave][col] = mx;
+    sl[wave][col] = sum;
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) so[wave][dt][lane] = o[dt];
+  __syncthreads();
+  const int64_t slot = (int64_t)bh * w.nblk + blockIdx.x;
+  for (int e = threadIdx.x; e < DT * 64; e += 64 * NW) {
+    const int dt = e >> 6, ln = e & 63, r = ln & 15;
+    if (r >= R) continue;
+    float m = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) m = fmaxf(m, sm[v][r]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float f = sm[v][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sm[v][r] - m);
+      acc += so[v][dt][ln] * f;
+    }
+    *reinterpret_cast<f32x4*>(w.o + (slot * 16 + r) * D + dt * 16 + 4 * (ln >> 4)) = acc;
+  }
+  if (threadIdx.x < 16) {
+    const int r = threadIdx.x;
+    float m = -INFINITY, l = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) m = fmaxf(m, sm[v][r]);
+#pragma unroll
+    for (int v = 0; v < NW; ++v)
+      l += sm[v][r] == -INFINITY ? 0.f : sl[v][r] * __builtin_amdgcn_exp2f(sm[v][r] - m);
+    w.ml[(slot * 16 + r) * 2] = m;
+    w.ml[(slot * 16 + r) * 2 + 1] = l;
+  }
+}
+
+// One workgroup per (query row, batch x kv head). The partials' maxima and sums are read
+// in parallel into LDS and turned into weights exp2(m_k - max); thread d then sums the
+// partials of head-dim d with independent (unrolled) loads.
+template <int D>
+__global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(AttnParams p, DecodeWs w) {
+  constexpr int NT = D < 64 ? 64 : D;  // whole waves, so the shuffles see only live lanes
+  constexpr int NWV = NT / 64;
+  __shared__ float wk[1024];
+  __shared__ float red[NWV];
+  __shared__ float stats[2];
+  const int r = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+  const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
+  const int g = p.Hq / p.Hkv;
+  const int jh = r / p.Tq, t = r - jh * p.Tq;
+  const int64_t base = (int64_t)bh * w.nblk;
+  float m = -INFINITY;
+  for (int k = d; k < w.nblk; k += NT) {
+    const float mk = w.ml[((base + k) * 16 + r) * 2];
+    wk[k] = mk;
+    m = fmaxf(m, mk);
+  }
+  m = wave_max(m);
+  if ((d & 63) == 0) red[d >> 6] = m;
+  __syncthreads();
+  if (d == 0) {
+    float mm = red[0];
+    for (int i = 1; i < NWV; ++i) mm = fmaxf(mm, red[i]);
+    stats[0] = mm;
+  }
+  __syncthreads();
+  m = stats[0];
+  float l = 0.f;
+  for (int k = d; k < w.nblk; k += NT) {
+    const float f = wk[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wk[k] - m);
+    wk[k] = f;
+    l += w.ml[((base + k) * 16 + r) * 2 + 1] * f;
+  }
+  l = wave_sum(l);
+  if ((d & 63) == 0) red[d >> 6] = l;
+  __syncthreads();
+  if (d == 0) {
+    float ll = 0.f;
+    for (int i = 0; i < NWV; ++i) ll += red[i];
+    stats[1] = ll;
+  }
+  __syncthreads();
+  if (d >= D) return;
+  const float* src = w.o + (base * 16 + r) * D + d;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int k = 0;
+  for (; k + 4 <= w.nblk; k += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += src[(int64_t)(k + u) * 16 * D] * wk[k + u];
+  }
+  for (; k < w.nblk; ++k) acc[0] += src[(int64_t)k * 16 * D] * wk[k];
+  const float o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  const int h = hk * g + jh;
+  p.out[((int64_t)b * p.Tq + t) * p.ld_out + (int64_t)h * D + d] = f2bf(o / stats[1]);
+}
+
+template <int D>
+static void launch_decode(int nw, int jt, dim3 g1, dim3 g2, hipStream_t st, const AttnParams& p,
+                          const DecodeWs& w) {
+  if (nw == 4 && jt == 4) attention_decode_kernel<D, 4, 4><<<g1, 256, 0, st>>>(p, w);
+  else if (nw == 2 && jt == 2) attention_decode_kernel<D, 2, 2><<<g1, 128, 0, st>>>(p, w);
+  else if (nw == 1 && jt == 2) attention_decode_kernel<D, 1, 2><<<g1, 64, 0, st>>>(p, w);
+  else if (nw == 4 && jt == 2) attention_decode_kernel<D, 4, 2><<<g1, 256, 0, st>>>(p, w);
+  else if (nw == 2 && jt == 4) attention_decode_kernel<D, 2, 4><<<g1, 128, 0, st>>>(p, w);
+  else attention_decode_kernel<D, 1, 4><<<g1, 64, 0, st>>>(p, w);
+  attention_combine_kernel<D><<<g2, D < 64 ? 64 : D, 0, st>>>(p, w);
+}
+
 }  // namespace tl
 
 using namespace tl;
@@ -247,6 +464,34 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
   const double flops = bh * kept * 4.0 * head_dim;
   const double bytes = 2.0 * (bh * seq_q * head_dim * 2 + (double)batch * n_heads_kv * seq_k * head_dim * 2);
   LaunchScope ls(ctx, TL_KF_ATTENTION, flops, bytes);
+  const int64_t rows_per_kv = (n_heads_q / n_heads_kv) * seq_q;
+  if (rows_per_kv <= 16) {  // decode: split the keys over workgroups of 4 x 64 keys
+    DecodeWs w;
+    // (waves per workgroup, 16-key tiles per wave)
+    static const int kDecodeCfg[][2] = {{4, 2}, {4, 4}, {1, 4}, {2, 2}, {1, 2}, {4, 2}, {2, 4}};
+    const int cfg = ctx->attn_decode_cfg >= 1 && ctx->attn_decode_cfg <= 6 ? ctx->attn_decode_cfg : 0;
+    const int nw = kDecodeCfg[cfg][0], jt = kDecodeCfg[cfg][1];
+    w.nblk = (int)((seq_k + 16 * nw * jt - 1) / (16 * nw * jt));
+    TL_REQUIRE(w.nblk <= 1024, "decode attention takes up to %d keys with this split",
+               1024 * 16 * nw * jt);
+    const int64_t slots = batch * n_heads_kv * w.nblk;
+    TL_REQUIRE(batch * n_heads_kv <= 65535, "batch * kv heads exceeds 65535");
+    void* ws;
+    const size_t obytes = (size_t)slots * 16 * head_dim * sizeof(float);
+    rc = workspace(ctx, obytes + (size_t)slots * 16 * 2 * sizeof(float), &ws);
+    if (rc) return rc;
+    w.o = (float*)ws;
+    w.ml = (float*)((char*)ws + obytes);
+    const dim3 g1((unsigned)w.nblk, (unsigned)(batch * n_heads_kv));
+    const dim3 g2((unsigned)rows_per_kv, (unsigned)(batch * n_heads_kv));
+    switch (head_dim) {
+      case 32: launch_decode<32>(nw, jt, g1, g2, ctx->stream, p, w); break;
+      case 64: launch_decode<64>(nw, jt, g1, g2, ctx->stream, p, w); break;
+      case 128: launch_decode<128>(nw, jt, g1, g2, ctx->stream, p, w); break;
+      default: launch_decode<256>(nw, jt, g1, g2, ctx->stream, p, w); break;
+    }
+    return ls.finish("attention_decode");
+  }
   dim3 grid((unsigned)((seq_q + 63) / 64), (unsigned)(batch * n_heads_q));
   switch (head_dim) {
     case 32: attention_fwd_kernel<32><<<grid, 256, 0, ctx->stream>>>(p); break;

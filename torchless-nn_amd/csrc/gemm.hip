@@ -666,6 +666,87 @@ void gemm_dma_persistent_kernel(GemmParams p) {
   }
 }
 
+// gemm_skinny_kernel: M <= 16 (a decode step's few rows), where the product is a stream of
+// the weights. A workgroup owns 16 rows of Bt (n0 .. n0 + 15) and its NW waves split K. Per
+// 32-wide K step a wave loads one 16 x 32 fragment of Bt (lane: row lane % 16, 8 columns at
+// 8 * (lane / 16), so the 4 lanes of a row read 64 contiguous bytes) and the matching A
+// fragment (row m = lane % 16 of A, zeros for m >= M), and issues one MFMA with Bt as the
+// first operand: lane holds out[m = lane % 16][n0 + 4 (lane / 16) + 0..3]. U steps are in
+// flight per wave. The NW partial sums meet in LDS and the first wave runs the same
+// epilogue as the fp32 kernel (bias, activation, residual, QKV scatter, gated pairs).
+// When there are too few 16-row blocks to fill the GPU, K is also split over gridDim.y
+// workgroups: each writes its partial block (64 lanes x 4 floats) to `part`, and
+// gemm_skinny_reduce_kernel, the next launch on the stream, sums them and runs the epilogue.
+template <typename TO, int NW, int U>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p, float* part) {
+  __shared__ f32x4 red[NW][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t z = blockIdx.z;
+  const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t wrow = min(n0 + r, p.N - 1);
+  const bf16_t* W = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i + wrow * p.ldb + 8 * g;
+  const bool xrow = r < p.M;
+  const bf16_t* X = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i +
+                    (xrow ? r : 0) * p.lda + 8 * g;
+  const int S = gridDim.y, ky = blockIdx.y;
+  const int64_t nsteps = (p.K + 31) / 32;
+  const int64_t spg = (nsteps + S - 1) / S;
+  const int64_t g0 = ky * spg, g1 = min(nsteps, g0 + spg);
+  const int64_t per = g1 > g0 ? (g1 - g0 + NW - 1) / NW : 0;
+  const int64_t s0 = g0 + wave * per, s1 = min(g1, s0 + per);
+  const bf16x8 zero = {};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t s = s0; s < s1; s += U) {
+    bf16x8 w[U], x[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t k = (s + u) * 32;
+      const bool in = s + u < s1 && k + 8 * g < p.K;
+      w[u] = in ? *reinterpret_cast<const bf16x8*>(W + k) : zero;
+      x[u] = in && xrow ? *reinterpret_cast<const bf16x8*>(X + k) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], x[u], acc, 0, 0, 0);
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (S == 1) {
+    if (wave == 0 && xrow) {
+      f32x4 t = red[0][lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) t += red[w][lane];
+      float v[4] = {t[0], t[1], t[2], t[3]};
+      epilogue4<bf16_t, TO>(p, zo, zi, r, n0 + 4 * g, v);
+    }
+    return;
+  }
+  if (wave == 0) {
+    const int64_t tile = (int64_t)blockIdx.z * gridDim.x + blockIdx.x;
+    f32x4 t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w][lane];
+    *reinterpret_cast<f32x4*>(part + ((tile * S + ky) * 64 + lane) * 4) = t;
+  }
+}
+
+// One wave per 16-row block: sums the `split` partials of the skinny kernel, then the epilogue.
+template <typename TO>
+__global__ __launch_bounds__(64) void gemm_skinny_reduce_kernel(GemmParams p, const float* part,
+                                                                int split) {
+  const int lane = threadIdx.x, r = lane & 15, g = lane >> 4;
+  if (r >= p.M) return;
+  const int64_t z = blockIdx.z;
+  const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
+  const int64_t tile = z * gridDim.x + blockIdx.x;
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < split; ++k)
+    t += *reinterpret_cast<const f32x4*>(part + ((tile * split + k) * 64 + lane) * 4);
+  float v[4] = {t[0], t[1], t[2], t[3]};
+  epilogue4<bf16_t, TO>(p, zo, zi, r, (int64_t)blockIdx.x * 16 + 4 * g, v);
+}
+
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
   constexpr int BM = 64, BN = 64, BK = 16;
@@ -748,6 +829,27 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
   return TL_TILE_64x64;
 }
 
+// (waves per workgroup, K steps in flight per wave) of the skinny kernel
+// Measured on an MI355X at the config-5 decode shapes (M = 4): (4 waves, 16 steps) streams
+// the wide GEMMs fastest (GeGLU 134 MB in 23.9 us, LM head 1.05 GB in 197 us); the others
+// are kept for TL_SKINNY_CFG sweeps.
+static const int kSkinnyCfg[][2] = {{4, 16}, {4, 8}, {8, 16}, {8, 8}, {16, 4}, {8, 4}, {16, 8}};
+
+template <typename TO>
+static void launch_skinny(int cfg, dim3 grid, hipStream_t st, const GemmParams& p, float* part) {
+  switch (cfg) {
+    case 1: gemm_skinny_kernel<TO, 4, 8><<<grid, 256, 0, st>>>(p, part); break;
+    case 2: gemm_skinny_kernel<TO, 8, 16><<<grid, 512, 0, st>>>(p, part); break;
+    case 3: gemm_skinny_kernel<TO, 8, 8><<<grid, 512, 0, st>>>(p, part); break;
+    case 4: gemm_skinny_kernel<TO, 16, 4><<<grid, 1024, 0, st>>>(p, part); break;
+    case 5: gemm_skinny_kernel<TO, 8, 4><<<grid, 512, 0, st>>>(p, part); break;
+    case 6: gemm_skinny_kernel<TO, 16, 8><<<grid, 1024, 0, st>>>(p, part); break;
+    default: gemm_skinny_kernel<TO, 4, 16><<<grid, 256, 0, st>>>(p, part); break;
+  }
+  if (grid.y > 1)
+    gemm_skinny_reduce_kernel<TO><<<dim3(grid.x, 1, grid.z), 64, 0, st>>>(p, part, (int)grid.y);
+}
+
 template <typename TO>
 static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
   switch (tile) {
@@ -783,7 +885,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_PERSIST_128x128, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_SKINNY, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -848,6 +950,33 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   const int family = mfma ? d->family : TL_KF_GEMM_SIMT;
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
   const bool f32out = d->dtype_out == TL_F32;
+  const bool skinny = mfma && (d->tile == TL_TILE_SKINNY || (d->tile == TL_TILE_AUTO && d->M <= 16));
+  if (skinny) {
+    TL_REQUIRE(d->M <= 16, "the skinny GEMM takes M <= 16");
+    const int cfg = ctx->skinny_cfg >= 1 && ctx->skinny_cfg <= 6 ? ctx->skinny_cfg : 0;
+    const int64_t tiles = (d->N + 15) / 16 * batch;
+    const int64_t nsteps = (d->K + 31) / 32;
+    const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    // Long K only (the split costs a second launch): split until there are 2 workgroups
+    // per CU while every part keeps >= 4096 of K (down projection K = 16384: 4 parts,
+    // 23.6 -> 18.0 us; K = 2048 shapes lose more to the extra launch than they gain).
+    int64_t split = 1;
+    while (split < std::min(16, ctx->skinny_max_split) && tiles * split < 2 * cus &&
+           nsteps / (split * 2) >= 128)
+      split *= 2;
+    dim3 grid((unsigned)((d->N + 15) / 16), (unsigned)split, (unsigned)batch);
+    float* part = nullptr;
+    if (split > 1) {
+      void* ws;
+      rc = workspace(ctx, (size_t)tiles * split * 64 * 4 * sizeof(float), &ws);
+      if (rc) return rc;
+      part = (float*)ws;
+    }
+    LaunchScope ls(ctx, family, flops, bytes);
+    if (f32out) launch_skinny<float>(cfg, grid, ctx->stream, p, part);
+    else launch_skinny<bf16_t>(cfg, grid, ctx->stream, p, part);
+    return ls.finish("gemm_skinny");
+  }
   if (mfma) {
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps

@@ -10,6 +10,8 @@
 #include <cstring>
 #include <type_traits>
 
+#include <algorithm>
+
 #include "tl_internal.hpp"
 
 namespace tl {
@@ -588,10 +590,15 @@ __device__ __forceinline__ bool argmax_better(float va, int64_t ia, float vb, in
   return ia < ib;
 }
 
+// One block per (row, column slice of split_len): with one slice the block writes the row's
+// index; with several it writes its slice's (value, index) to pv/pi[row * slices + slice]
+// and argmax_finish_kernel reduces them.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, int64_t rows,
                                                      int64_t cols, int64_t ldx,
-                                                     int64_t* __restrict__ out) {
+                                                     int64_t* __restrict__ out, int64_t split_len,
+                                                     float* __restrict__ pv,
+                                                     int64_t* __restrict__ pi) {
   constexpr int VW = VEC ? Elem<T>::kVec : 1;
   __shared__ float rv[4];
   __shared__ int64_t ri[4];
@@ -599,17 +606,19 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, in
   const T* xr = x + row * ldx;
   float best = -INFINITY;
   int64_t bi = INT64_MAX;
-  for (int64_t c0 = (int64_t)threadIdx.x * VW; c0 < cols; c0 += 256 * VW) {
+  const int64_t cbeg = (int64_t)blockIdx.y * split_len;
+  const int64_t cend = min(cols, cbeg + split_len);
+  for (int64_t c0 = cbeg + (int64_t)threadIdx.x * VW; c0 < cend; c0 += 256 * VW) {
     float v[VW];
     if (VEC && c0 + VW <= cols) {
       load_chunk(xr + c0, v);
     } else {
 #pragma unroll
-      for (int e = 0; e < VW; ++e) v[e] = (c0 + e < cols) ? Elem<T>::load(xr + c0 + e) : -INFINITY;
+      for (int e = 0; e < VW; ++e) v[e] = (c0 + e < cend) ? Elem<T>::load(xr + c0 + e) : -INFINITY;
     }
 #pragma unroll
     for (int e = 0; e < VW; ++e)
-      if (c0 + e < cols && argmax_better(v[e], c0 + e, best, bi)) {
+      if (c0 + e < cend && argmax_better(v[e], c0 + e, best, bi)) {
         best = v[e];
         bi = c0 + e;
       }
@@ -635,8 +644,37 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* __restrict__ x, in
         best = rv[i];
         bi = ri[i];
       }
-    out[row] = bi;
+    if (gridDim.y == 1) {
+      out[row] = bi;
+    } else {
+      pv[row * gridDim.y + blockIdx.y] = best;
+      pi[row * gridDim.y + blockIdx.y] = bi;
+    }
   }
+}
+
+// One wave per row over its `slices` (<= 64) partial results, in slice order.
+__global__ __launch_bounds__(64) void argmax_finish_kernel(const float* __restrict__ pv,
+                                                           const int64_t* __restrict__ pi,
+                                                           int slices, int64_t* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  float best = -INFINITY;
+  int64_t bi = INT64_MAX;
+  if (lane < slices) {
+    best = pv[row * slices + lane];
+    bi = pi[row * slices + lane];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int64_t oi = __shfl_xor(bi, o, 64);
+    if (argmax_better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) out[row] = bi;
 }
 
 }  // namespace tl
@@ -762,14 +800,39 @@ static void launch_act(tl_ctx* ctx, const void* x, void* y, int64_t n, int act) 
   else act_kernel<T, false><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, n, act);
 }
 
+// Rows are split into column slices when there are too few rows to fill the GPU (a decode
+// step's handful of vocabulary rows): slices of >= 8192 columns, at most 64 per row.
 template <typename T>
-static void launch_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
-                          void* out) {
+static int launch_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                         void* out) {
   const bool vec = ldx % Elem<T>::kVec == 0 && aligned16(x);
+  const int64_t target = 4LL * (ctx->num_cus > 0 ? ctx->num_cus : 256);
+  int64_t slices = 1;
+  if (rows < target && cols >= 2 * 8192) {
+    slices = std::min<int64_t>(std::min<int64_t>((target + rows - 1) / rows, cols / 8192), 64);
+    if (rows * slices > 65535LL * 64) slices = 1;
+  }
+  int64_t split_len = (cols + slices - 1) / slices;
+  split_len = (split_len + 7) / 8 * 8;
+  slices = (cols + split_len - 1) / split_len;
+  float* pv = nullptr;
+  int64_t* pi = nullptr;
+  if (slices > 1) {
+    void* ws;
+    const size_t nv = (size_t)rows * slices;
+    int rc = workspace(ctx, nv * (sizeof(float) + sizeof(int64_t)) + 256, &ws);
+    if (rc) return rc;
+    pi = (int64_t*)ws;
+    pv = (float*)((char*)ws + ((nv * sizeof(int64_t) + 255) & ~(size_t)255));
+  }
+  const dim3 grid((unsigned)rows, (unsigned)slices);
   if (vec)
-    argmax_kernel<T, true><<<(unsigned)rows, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out);
+    argmax_kernel<T, true><<<grid, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out, split_len, pv, pi);
   else
-    argmax_kernel<T, false><<<(unsigned)rows, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out);
+    argmax_kernel<T, false><<<grid, 256, 0, ctx->stream>>>((const T*)x, rows, cols, ldx, (int64_t*)out, split_len, pv, pi);
+  if (slices > 1)
+    argmax_finish_kernel<<<(unsigned)rows, 64, 0, ctx->stream>>>(pv, pi, (int)slices, (int64_t*)out);
+  return TL_OK;
 }
 
 template <bool RMS>
@@ -1004,8 +1067,9 @@ int tl_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ld
   TL_REQUIRE(ldx >= cols, "leading dimension smaller than cols");
   TL_REQUIRE(rows < (int64_t)0x7fffffff, "too many rows");
   LaunchScope ls(ctx, TL_KF_ARGMAX, 0, (double)dtype_size(dtype) * rows * cols + 8.0 * rows);
-  if (dtype == TL_F32) launch_argmax<float>(ctx, x, rows, cols, ldx, out_ids);
-  else launch_argmax<bf16_t>(ctx, x, rows, cols, ldx, out_ids);
+  rc = dtype == TL_F32 ? launch_argmax<float>(ctx, x, rows, cols, ldx, out_ids)
+                      : launch_argmax<bf16_t>(ctx, x, rows, cols, ldx, out_ids);
+  if (rc) return rc;
   return ls.finish("argmax");
 }
 

@@ -20,6 +20,21 @@ int fail(int code, const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
+int workspace(tl_ctx* ctx, size_t bytes, void** ptr) {
+  if (bytes > ctx->ws_bytes) {
+    // the old buffer may still be read by queued kernels: wait for them before freeing
+    TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    const size_t size = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    TL_CHECK_HIP(hipMalloc(&ctx->ws, size));
+    ctx->ws_bytes = size;
+  }
+  *ptr = ctx->ws;
+  return TL_OK;
+}
+
 int enter(tl_ctx* ctx) {
   clear_error();
   if (!ctx) return fail(TL_ERR_INVALID, "null tl_ctx");
@@ -146,6 +161,9 @@ int tl_init(int device, tl_ctx** out) {
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
   if (const char* g = std::getenv("TL_GEMM_GROUP_M")) ctx->gemm_group_m = std::atoi(g);
+  if (const char* g = std::getenv("TL_SKINNY_CFG")) ctx->skinny_cfg = std::atoi(g);
+  if (const char* g = std::getenv("TL_SKINNY_MAX_SPLIT")) ctx->skinny_max_split = std::atoi(g);
+  if (const char* g = std::getenv("TL_ATTN_DECODE_CFG")) ctx->attn_decode_cfg = std::atoi(g);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
@@ -174,6 +192,7 @@ int tl_destroy(tl_ctx* ctx) {
   for (auto& kv : ctx->free_blocks) (void)hipFree(kv.second);
   for (auto& kv : ctx->live) (void)hipFree(kv.first);
   (void)hipFree(ctx->status);
+  if (ctx->ws) (void)hipFree(ctx->ws);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return TL_OK;

@@ -50,6 +50,15 @@ struct tl_ctx {
   tl::KprofTotals kprof_totals[TL_KF_COUNT];
   int num_cus = 0;
   int gemm_group_m = 0;  // tile-rows per group in the GEMM tile order (TL_GEMM_GROUP_M)
+  // tuning overrides (0 = built-in choice): skinny GEMM variant (TL_SKINNY_CFG) and
+  // decode attention split (TL_ATTN_DECODE_CFG)
+  int skinny_cfg = 0;
+  int skinny_max_split = 16;  // TL_SKINNY_MAX_SPLIT
+  int attn_decode_cfg = 0;
+  // grow-only scratch for kernels that combine partial results (split argmax, split-KV
+  // attention); used in stream order, so one buffer serves every call on this context
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
 };
 
 namespace tl {
@@ -68,6 +77,8 @@ inline size_t dtype_size(int dt) {
 
 // Checks the context, binds its device and clears the thread's error message.
 int enter(tl_ctx* ctx);
+// Returns the context's scratch buffer, grown to at least `bytes` (256-byte aligned).
+int workspace(tl_ctx* ctx, size_t bytes, void** ptr);
 
 // Brackets one kernel launch with profiler events when its family is enabled.
 struct LaunchScope {

@@ -46,8 +46,7 @@ class GemmaDecoder:
         x = self.front.forward(ids)
         for i, blk in enumerate(self.blocks):
             x = blk.forward(x, cache, i, pos0)
-        x = self.final_norm.forward(x)
-        logits = self.back.forward(x)
+        logits = self.back.forward(self.final_norm.forward(x))
         if cache is not None:
             cache.length = pos0 + x.shape[1]
         return logits

@@ -312,6 +312,22 @@ class TransformerBlock(Layer):
 # is ungated (layers.py:346-375) and generation recomputes the whole window
 # (demo.ipynb:1520-1537). Their interfaces follow the Layer protocol above.
 # ---------------------------------------------------------------------------------------
+_ROPE_TABLES = {}
+
+
+def _rope_table(T, D, base, pos0):
+    """cos/sin table for positions pos0 .. pos0 + T - 1, shared by every layer of a step
+    (a handful of recent tables are kept; each is T * D * 4 bytes)."""
+    key = (T, D, base, pos0)
+    t = _ROPE_TABLES.pop(key, None)
+    if t is None:
+        t = xp.rope_table(T, D, base, pos0)
+        while len(_ROPE_TABLES) >= 8:
+            _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))
+    _ROPE_TABLES[key] = t
+    return t
+
+
 class KVCache:
     """Per-layer keys [B, Hkv, L, D] and transposed values [B, Hkv, D, L] in HBM, zero
     filled (positions past the valid length must hold finite values), L a multiple of 8."""
@@ -369,7 +385,7 @@ class MultiQueryAttention(Layer):
             L = _round_up(T, 8)
             k, vt = xp.zeros((B, Hkv, L, D), dt), xp.zeros((B, Hkv, D, L), dt)
         linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0))
-        table = xp.rope_table(T, D, self.rope_base, pos0)
+        table = _rope_table(T, D, self.rope_base, pos0)
         xp.rope(q, table, out=q)
         kslice = xp.DeviceTensor((B * Hkv, T, D), dt, buf=k.buf,
                                  offset=k.offset + pos0 * D * dt.itemsize)
