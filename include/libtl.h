@@ -180,6 +180,13 @@ int tl_random_normal(tl_ctx* ctx, void* y, int64_t n, uint64_t seed, uint64_t st
 /* y[c*ldy + r] = x[r*ldx + c]: weight pre-packing into the K-contiguous GEMM layout. */
 int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t ldy, int32_t dtype);
+/* ViT patch extraction, reference transformer_adapters.py:39-47 (VitProjector.forward's
+ * reshape / transpose(0,2,4,3,5,1) / reshape): x [B, C, H, W] -> y [B, (H/ph)(W/pw),
+ * ph*pw*C], token i*(W/pw) + j, features ordered (row in patch, column in patch, channel).
+ * H and W must be multiples of the patch size. x and y may differ in dtype. */
+int tl_patchify(tl_ctx* ctx, const void* x, void* y, int64_t batch, int64_t channels,
+                int64_t height, int64_t width, int64_t patch_h, int64_t patch_w,
+                int32_t dtype_x, int32_t dtype_y);
 /* y = a + b (elementwise, same shape). Replaces the residual adds at reference
  * layers.py:465-466 when they are not fused into a GEMM epilogue. */
 int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype);

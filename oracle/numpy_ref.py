@@ -25,6 +25,9 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
                    two-call run equals one call over the whole sequence
   gemma_forward    incremental (cached) logits equal recomputed ones; composition of the
                    pinned pieces above; gemma_greedy ids are argmax of its own rows
+  patchify         brute-force index loops (token i*(W/p1)+j, feature (a*p1+c2)*C+ch)
+  vit_projector    brute-force loops over the same formula at a tiny shape
+  vit_forward      composition of pinned pieces; images are independent (batch split)
   mha              brute-force per-head loops in float64 (golden fixture); permutation
                    weights pin the head split/merge order
   embed_front      brute-force gather + add
@@ -418,3 +421,78 @@ def random_normal(n, seed, stream=0, mean=0.0, std=1.0):
         out[:, a] = r * np.cos(2 * np.pi * u2)
         out[:, b] = r * np.sin(2 * np.pi * u2)
     return (mean + std * out.reshape(-1)[:n]).astype(F32)
+
+
+# ---- ViT (reference transformer_adapters.py:6-95, demo.ipynb cell 8) ----------------
+def patchify(x, patch):
+    """transformer_adapters.py:39-47: [B, C, H, W] -> reshape [B, C, H/p0, p0, W/p1, p1],
+    transpose (0, 2, 4, 3, 5, 1), reshape [B, L, p0 p1 C]."""
+    x = np.asarray(x)
+    B, C, H, W = x.shape
+    p0, p1 = patch
+    r = x.reshape(B, C, H // p0, p0, W // p1, p1).transpose(0, 2, 4, 3, 5, 1)
+    return r.reshape(B, (H // p0) * (W // p1), p0 * p1 * C)
+
+
+def vit_projector(x, proj, cls_reg, pos, patch):
+    """transformer_adapters.py:49-55: tokens @ projection (no bias), class/register tokens
+    tiled over the batch and prepended, plus the positional table."""
+    tokens = patchify(np.asarray(x, dtype=F32), patch)
+    emb = tokens @ proj
+    B = emb.shape[0]
+    cls = np.broadcast_to(cls_reg, (B,) + cls_reg.shape)
+    return np.concatenate([cls, emb], axis=1) + pos
+
+
+def vit_param_shapes(cfg):
+    """Parameter shapes in layer order: VitProjector [projection, cls_reg_tokens, positions]
+    (transformer_adapters.py:29-31), the encoder blocks, the final LayerNorm, the head
+    (VitMLPHead [W, b], then Dense [W, b] when the head has a hidden layer)."""
+    C, H, W = cfg["image"]
+    p0, p1 = cfg["patch"]
+    d, R = cfg["d"], 1 + cfg.get("registers", 0)
+    L = (H // p0) * (W // p1)
+    shapes = [("proj", (p0 * p1 * C, d)), ("cls", (R, d)), ("pos", (R + L, d))]
+    for l in range(cfg["layers"]):
+        shapes += [(f"b{l}.g1", (d,)), (f"b{l}.be1", (d,)), (f"b{l}.wqkv", (d, 3 * d)),
+                   (f"b{l}.bqkv", (3 * d,)), (f"b{l}.wo", (d, d)), (f"b{l}.bo", (d,)),
+                   (f"b{l}.g2", (d,)), (f"b{l}.be2", (d,)), (f"b{l}.w1", (d, 4 * d)),
+                   (f"b{l}.bb1", (4 * d,)), (f"b{l}.w2", (4 * d, d)), (f"b{l}.bb2", (d,))]
+    shapes += [("lnf.g", (d,)), ("lnf.be", (d,))]
+    hidden = cfg.get("head_hidden")
+    if hidden:
+        shapes += [("head.w", (d, hidden)), ("head.b", (hidden,)),
+                   ("dense.w", (hidden, cfg["classes"])), ("dense.b", (cfg["classes"],))]
+    else:
+        shapes += [("head.w", (d, cfg["classes"])), ("head.b", (cfg["classes"],))]
+    return shapes
+
+
+def vit_params(cfg, seed, scale=0.02, bf16=False):
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in vit_param_shapes(cfg):
+        a = rng.standard_normal(shape, dtype=F32) * F32(scale)
+        if name.endswith(".g1") or name.endswith(".g2") or name == "lnf.g":
+            a = a + F32(1.0)
+        out[name] = round_bf16(a) if bf16 else a
+    return out
+
+
+def vit_forward(x, params, cfg, bf16=False):
+    """demo.ipynb cell 8 composition: projector -> encoder blocks (no mask) -> LayerNorm ->
+    class-token head (-> SiLU -> Dense when the head has a hidden layer) -> SoftMax."""
+    rnd = round_bf16 if bf16 else None
+    r = rnd or (lambda a: a)
+    x = r(np.asarray(x, dtype=F32))
+    h = r(vit_projector(x, params["proj"], params["cls"], params["pos"], cfg["patch"]))
+    for l in range(cfg["layers"]):
+        p = [params[f"b{l}.{k}"] for k in ("g1", "be1", "wqkv", "bqkv", "wo", "bo", "g2", "be2",
+                                          "w1", "bb1", "w2", "bb2")]
+        h = block(h, p, cfg["heads"], cfg.get("act", "gelu"), False, None, rnd)
+    h = r(layernorm(h, params["lnf.g"], params["lnf.be"]))
+    y = r(vit_head(h, params["head.w"], params["head.b"]))
+    if cfg.get("head_hidden"):
+        y = r(silu(y))
+        y = r(dense(y, params["dense.w"], params["dense.b"]))
+    return r(softmax(y))

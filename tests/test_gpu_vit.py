@@ -1,0 +1,144 @@
+"""ViT front end and classifier on the MI355X against the NumPy oracle: the patch gather,
+VitProjector (projection, class/register rows, positions), encoder attention at a token
+count that is not a multiple of 8, a tiny notebook-style ViT end to end (fp32, 1e-5), and
+BASELINE config 4 at full size (bf16, 2e-2 on sampled images, class ids bit-exact against
+np.argmax of the downloaded probabilities)."""
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+@pytest.fixture(scope="module")
+def tl():
+    import tl_hip
+    tl_hip.ctx()
+    import backend
+    import layers
+    import transformer_adapters
+    import vit
+    return dict(xp=tl_hip, backend=backend, layers=layers, ta=transformer_adapters, vit=vit)
+
+
+@pytest.mark.parametrize("dts", [("fp32", "fp32"), ("fp32", "bf16"), ("bf16", "bf16"), ("bf16", "fp32")])
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 4, 4), (3, 3, 32, 32, 2, 2), (1, 1, 6, 4, 3, 2),
+                                   (5, 4, 8, 12, 4, 3)])
+def test_patchify_matches_reference_order(tl, dts, shape):
+    xp = tl["xp"]
+    B, C, H, W, p0, p1 = shape
+    x = np.random.default_rng(B * H + p1).standard_normal((B, C, H, W)).astype(F32)
+    if dts[0] == "bf16":
+        x = ref.round_bf16(x)
+    got = xp.patchify(xp.array(x, dtype=dts[0]), (p0, p1), dtype=dts[1]).get()
+    want = ref.patchify(x, (p0, p1))
+    if dts[1] == "bf16":
+        want = ref.round_bf16(want)
+    assert np.array_equal(got, want)
+
+
+def test_patchify_rejects_partial_patches(tl):
+    xp = tl["xp"]
+    with pytest.raises(ValueError):
+        xp.patchify(xp.zeros((1, 3, 10, 8)), (4, 4))
+    lib, h = xp.lib(), xp.ctx().handle
+    x, y = xp.zeros((1, 3, 10, 8)), xp.zeros((1, 240))
+    assert lib.tl_patchify(h, x.ptr, y.ptr, 1, 3, 10, 8, 4, 4, 0, 0) == 1  # TL_ERR_INVALID
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("registers", [0, 4])
+def test_vit_projector_layer(tl, dt, registers):
+    tl["backend"].set_float_type(dt)
+    layer = tl["ta"].VitProjector((3, 32, 32), (4, 4), 384, num_registers=registers)
+    rng = np.random.default_rng(registers + 1)
+    P = []
+    for p in layer.parameters:
+        a = rng.standard_normal(p.shape).astype(F32) * F32(0.5)
+        a = ref.round_bf16(a) if dt == "bf16" else a
+        p.set(a)
+        P.append(a)
+    x = rng.standard_normal((6, 3, 32, 32)).astype(F32)
+    if dt == "bf16":
+        x = ref.round_bf16(x)
+    y = layer.forward(tl["xp"].array(x, dtype=dt)).get()
+    want = ref.vit_projector(x, *P, (4, 4))
+    assert y.shape == (6, 1 + registers + 64, 384)
+    assert ref.max_rel(y, want) <= (1e-5 if dt == "fp32" else 2e-2)
+    # host arrays are accepted like the reference's xp arrays
+    y2 = layer.forward(x).get()
+    assert ref.max_rel(y2, want) <= (1e-5 if dt == "fp32" else 2e-2)
+
+
+def test_vit_projector_rejects_wrong_image_shape(tl):
+    tl["backend"].set_float_type("fp32")
+    layer = tl["ta"].VitProjector((3, 32, 32), (4, 4), 64)
+    with pytest.raises(ValueError):
+        layer.forward(np.zeros((2, 3, 28, 28), F32))
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_encoder_attention_at_65_tokens(tl, dt):
+    """Config 4's token count (64 patches + CLS) is not a multiple of 8: the fused kernel
+    runs with padded key capacity; the padding is never read as values."""
+    B, T, C, H = 4, 65, 384, 6
+    tl["backend"].set_float_type(dt)
+    mha = tl["layers"].MultiHeadAttention(C, 0, H, decoder=False)
+    rng = np.random.default_rng(65)
+    P = [rng.standard_normal(p.shape).astype(F32) * F32(0.1) for p in mha.parameters]
+    P = [ref.round_bf16(p) if dt == "bf16" else p for p in P]
+    for p, a in zip(mha.parameters, P):
+        p.set(a)
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    if dt == "bf16":
+        x = ref.round_bf16(x)
+    y = mha.forward(tl["xp"].array(x, dtype=dt)).get()
+    want = ref.mha(x, *P, H, False, None, rnd=ref.round_bf16 if dt == "bf16" else None)
+    assert ref.max_rel(y, want) <= (1e-5 if dt == "fp32" else 2e-2)
+    if dt == "bf16":
+        assert mha.softmax is None  # the fused kernel ran
+
+
+def test_tiny_notebook_vit_fp32(tl):
+    """The notebook composition (registers, SiLU hidden head, Dropout in eval) at a small
+    size, end to end against the oracle."""
+    cfg = dict(image=(3, 16, 16), patch=(2, 2), d=32, heads=4, layers=2, act="silu",
+               registers=4, classes=10, head_hidden=16, dropout=0.1)
+    net = tl["vit"].build_vit(cfg, "fp32")
+    tl["vit"].seed_vit(net, 3, 0.2)
+    x = np.random.default_rng(4).standard_normal((5, 3, 16, 16)).astype(F32)
+    probs = net.predict(x)
+    want = ref.vit_forward(x, ref.vit_params(cfg, 3, 0.2), cfg)
+    got = probs.get()
+    assert ref.max_rel(got, want) <= 1e-5
+    assert np.array_equal(tl["xp"].argmax(probs).get(), np.argmax(got, -1))
+
+
+def _cifar_like(rng, n):
+    """Pixels uniform in [0, 1], normalised per channel as (x - 0.5) / sqrt(1/12)."""
+    x = rng.random((n, 3, 32, 32), dtype=F32)
+    return ((x - F32(0.5)) / F32(np.sqrt(1.0 / 12.0))).astype(F32)
+
+
+def test_vit_config4_full_shape_bf16(tl):
+    """BASELINE config 4 at its full size (B=512, 65 tokens, d 384, 6 heads, 8 layers,
+    10 classes, bf16): rows are probability vectors, images are independent of the rest of
+    the batch, and sampled images match the oracle."""
+    cfg = tl["vit"].VIT_S4
+    net = tl["vit"].build_vit(cfg, "bf16")
+    tl["vit"].seed_vit(net, 5, 0.02)
+    x = ref.round_bf16(_cifar_like(np.random.default_rng(6), 512))
+    xp = tl["xp"]
+    probs_dev = net.predict(xp.array(x, dtype="bf16"))
+    probs = probs_dev.get()
+    assert probs.shape == (512, 10)
+    assert np.array_equal(xp.argmax(probs_dev).get(), np.argmax(probs, -1))
+    np.testing.assert_allclose(probs.astype(np.float64).sum(-1), 1.0, rtol=2e-2)
+    P = ref.vit_params(cfg, 5, 0.02, bf16=True)
+    idx = [0, 1, 255, 511]
+    want = ref.vit_forward(x[idx], P, cfg, bf16=True)
+    assert ref.max_rel(probs[idx], want) <= 2e-2
+    sub = net.predict(xp.array(x[idx], dtype="bf16")).get()
+    assert ref.max_rel(sub, probs[idx]) <= 1e-2  # other tile shapes at 4 images

@@ -372,3 +372,53 @@ def test_random_normal_moments_and_structure():
     assert not np.allclose(ref.random_normal(16, 1, 0), ref.random_normal(16, 1, 1))
     np.testing.assert_allclose(ref.random_normal(10, 5, 3, 1.0, 0.02),
                                1.0 + 0.02 * ref.random_normal(10, 5, 3), rtol=1e-6)
+
+
+# ---- ViT ------------------------------------------------------------------------------------
+def test_patchify_brute_force():
+    rng = np.random.default_rng(40)
+    B, C, H, W, p0, p1 = 2, 3, 6, 4, 3, 2
+    x = rng.standard_normal((B, C, H, W)).astype(F32)
+    got = ref.patchify(x, (p0, p1))
+    ph, pw = H // p0, W // p1
+    assert got.shape == (B, ph * pw, p0 * p1 * C)
+    for b in range(B):
+        for i in range(ph):
+            for j in range(pw):
+                for a in range(p0):
+                    for c2 in range(p1):
+                        for ch in range(C):
+                            assert got[b, i * pw + j, (a * p1 + c2) * C + ch] == x[b, ch, i * p0 + a, j * p1 + c2]
+
+
+def test_vit_projector_brute_force():
+    rng = np.random.default_rng(41)
+    B, C, H, W, p, E, R = 2, 2, 4, 4, 2, 5, 3
+    x = rng.standard_normal((B, C, H, W)).astype(F32)
+    proj = rng.standard_normal((p * p * C, E)).astype(F32)
+    cls = rng.standard_normal((R, E)).astype(F32)
+    L = (H // p) * (W // p)
+    pos = rng.standard_normal((R + L, E)).astype(F32)
+    got = ref.vit_projector(x, proj, cls, pos, (p, p))
+    want = np.zeros((B, R + L, E))
+    for b in range(B):
+        for r in range(R):
+            want[b, r] = cls[r] + pos[r]
+        for l in range(L):
+            i, j = divmod(l, W // p)
+            tok = [x[b, ch, i * p + a, j * p + c2] for a in range(p) for c2 in range(p) for ch in range(C)]
+            want[b, R + l] = np.array(tok, np.float64) @ proj + pos[R + l]
+    assert ref.max_rel(got, want) < 1e-5
+
+
+def test_vit_forward_images_are_independent():
+    cfg = dict(image=(3, 8, 8), patch=(4, 4), d=16, heads=2, layers=2, act="gelu", registers=1,
+               classes=5, head_hidden=8)
+    P = ref.vit_params(cfg, 0, 0.3)
+    x = np.random.default_rng(42).standard_normal((3, 3, 8, 8)).astype(F32)
+    full = ref.vit_forward(x, P, cfg)
+    assert full.shape == (3, 5)
+    np.testing.assert_allclose(full.sum(-1), 1.0, rtol=1e-5)
+    assert ref.max_rel(ref.vit_forward(x[1:2], P, cfg), full[1:2]) < 1e-5
+    names = [n for n, _ in ref.vit_param_shapes(cfg)]
+    assert names[:3] == ["proj", "cls", "pos"] and names[-4:] == ["head.w", "head.b", "dense.w", "dense.b"]

@@ -1,9 +1,9 @@
 // Fused causal attention: scores, mask, online softmax, P.V and the head merge in one
 // kernel (replaces the reference's materialised [B, H, T, T] path, layers.py:293-304).
 //
-// Layout: q [B, Hq, Tq, D], k [B, Hkv, Tk, D], vt [B, Hkv, D, Tk] (bf16, as the QKV GEMM's
-// split epilogue writes them); out [B, Tq, Hq*D] with row pitch ld_out. Query head h reads
-// kv head h / (Hq / Hkv).
+// Layout: q [B, Hq, Tq, D], k [B, Hkv, Lk, D], vt [B, Hkv, D, Lk] (bf16, as the QKV GEMM's
+// split epilogue writes them; the first Tk of the Lk positions are valid, Lk % 8 == 0);
+// out [B, Tq, Hq*D] with row pitch ld_out. Query head h reads kv head h / (Hq / Hkv).
 //
 // One workgroup = 4 wavefronts = 64 query rows of one (batch, head); each wave owns 16
 // rows. Key/value chunks of 64 positions are double-buffered in LDS and shared by the 4
@@ -19,6 +19,22 @@
 #include "tl_internal.hpp"
 
 namespace tl {
+
+// Keep the first n (1..7) bf16 values of an 8-value chunk (or 1..3 of a 4-value run) and
+// zero the rest: value rows past the last valid key.
+__device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (2 * i >= n) w[i] = 0;
+    else if (2 * i + 1 >= n) w[i] &= 0xffffu;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+__device__ __forceinline__ uint2 keep_first4(uint2 v, int n) {
+  const uint4 t = keep_first(make_uint4(v.x, v.y, 0, 0), n);
+  return make_uint2(t.x, t.y);
+}
 
 struct AttnParams {
   const bf16_t* q;
@@ -83,10 +99,11 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
       const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its keys past Tk
-      // get probability 0 (their values must be finite)
+      // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its positions
+      // past Tk (capacity padding, never written) are zeroed, since 0 * NaN would not be 0
       const int kv = kv0 + c * 8;
       rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Lk + kv) : make_uint4(0, 0, 0, 0);
+      if (kv < p.Tk && kv + 8 > p.Tk) rv[i] = keep_first(rv[i], p.Tk - kv);
     }
   };
   auto store_chunk_lds = [&](int buf) {
@@ -306,8 +323,10 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
-      const uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
-      const uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
+      uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
+      uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
+      if (ina && ka + 4 > p.Tk) va = keep_first4(va, p.Tk - ka);
+      if (inb && kb + 4 > p.Tk) vb = keep_first4(vb, p.Tk - kb);
       const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
     }

@@ -79,6 +79,31 @@ __global__ __launch_bounds__(256) void transpose_kernel(const U* x, U* y, int64_
 }
 
 // ------------------------------------------------------------------------------------
+// ViT patch extraction (reference transformer_adapters.py:39-47): image [B, C, H, W] ->
+// tokens [B, (H/p0)(W/p1), p0 p1 C] with token index i (W/p1) + j and feature order
+// (row in patch a, column in patch c2, channel ch). One thread per output element, so the
+// writes are coalesced; the reads gather from the small image.
+// ------------------------------------------------------------------------------------
+template <typename TX, typename TY>
+__global__ __launch_bounds__(256) void patchify_kernel(const TX* __restrict__ x, TY* __restrict__ y,
+                                                       int64_t n, int C, int H, int W, int p0,
+                                                       int p1) {
+  const int pw = W / p1, L = (H / p0) * pw, tok = p0 * p1 * C;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int t = (int)(idx % tok);
+    const int64_t rest = idx / tok;
+    const int l = (int)(rest % L);
+    const int64_t b = rest / L;
+    const int ch = t % C, t2 = t / C;
+    const int c2 = t2 % p1, a = t2 / p1;
+    const int i = l / pw, j = l - i * pw;
+    const float v = Elem<TX>::load(x + ((b * C + ch) * H + i * p0 + a) * W + j * p1 + c2);
+    Elem<TY>::store(y + idx, v);
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // embedding gather + positional add (reference transformer_adapters.py:150-151)
 // ------------------------------------------------------------------------------------
 template <typename T, typename I, bool VEC>
@@ -901,6 +926,34 @@ int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dx, int32_t 
   else
     cast_kernel<bf16_t, bf16_t><<<g, 256, 0, ctx->stream>>>((const bf16_t*)x, (bf16_t*)y, n);
   return ls.finish("cast");
+}
+
+int tl_patchify(tl_ctx* ctx, const void* x, void* y, int64_t batch, int64_t channels,
+                int64_t height, int64_t width, int64_t patch_h, int64_t patch_w,
+                int32_t dtype_x, int32_t dtype_y) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(dtype_is_float(dtype_x) && dtype_is_float(dtype_y), "patchify supports fp32 and bf16");
+  TL_REQUIRE(batch >= 0 && channels > 0 && patch_h > 0 && patch_w > 0, "bad sizes");
+  TL_REQUIRE(height >= patch_h && width >= patch_w && height % patch_h == 0 && width % patch_w == 0,
+             "image %lldx%lld is not a whole number of %lldx%lld patches", (long long)height,
+             (long long)width, (long long)patch_h, (long long)patch_w);
+  TL_REQUIRE(channels * height * width < (1LL << 31), "image too large");
+  const int64_t n = batch * channels * height * width;
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(x && y && x != y, "null or aliased pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, (double)n * (dtype_size(dtype_x) + dtype_size(dtype_y)));
+  const unsigned g = grid_for(ctx, n, 256);
+  const int C = (int)channels, H = (int)height, W = (int)width, p0 = (int)patch_h, p1 = (int)patch_w;
+  if (dtype_x == TL_F32 && dtype_y == TL_F32)
+    patchify_kernel<float, float><<<g, 256, 0, ctx->stream>>>((const float*)x, (float*)y, n, C, H, W, p0, p1);
+  else if (dtype_x == TL_F32)
+    patchify_kernel<float, bf16_t><<<g, 256, 0, ctx->stream>>>((const float*)x, (bf16_t*)y, n, C, H, W, p0, p1);
+  else if (dtype_y == TL_F32)
+    patchify_kernel<bf16_t, float><<<g, 256, 0, ctx->stream>>>((const bf16_t*)x, (float*)y, n, C, H, W, p0, p1);
+  else
+    patchify_kernel<bf16_t, bf16_t><<<g, 256, 0, ctx->stream>>>((const bf16_t*)x, (bf16_t*)y, n, C, H, W, p0, p1);
+  return ls.finish("patchify");
 }
 
 int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype) {

@@ -148,19 +148,23 @@ class MultiHeadAttention(Layer):
                              f"{self.context_length} of the causal mask")
         dt = input.dtype
         x2 = input.reshape(B * T, C)
+        # the fused kernel takes keys/values with a capacity that is a multiple of 8; the
+        # padding positions are never written and never read as values
+        fused = self.fused and xp.attention_supported(dt, D, _round_up(T, 8))
+        L = _round_up(T, 8) if fused else T
         q = xp.empty((B, H, T, D), dt)
-        k = xp.empty((B, H, T, D), dt)
-        vt = xp.empty((B, H, D, T), dt)
-        linear(x2, self.qkv_weights, self.qkv_bias, qkv=(q, k, vt, T, H, H, D))
+        k = xp.empty((B, H, L, D), dt)
+        vt = xp.empty((B, H, D, L), dt)
+        linear(x2, self.qkv_weights, self.qkv_bias, qkv=(q, k, vt, T, H, H, D, L, 0))
         self.query, self.key_t, self.value = q, k, vt
 
         divisor = float(np.float32(D ** 0.5))  # reference layers.py:293 divides by sqrt(D)
-        if self.fused and xp.attention_supported(dt, D, T):
+        if fused:
             heads = xp.empty((B, T, C), dt)
             if self.attn_dropout.dropout_rate > 0.0 and not self.attn_dropout.eval_mode:
                 self.attn_dropout.forward(heads)  # raises: no dropout sampling at inference
             xp.attention(q, k, vt, heads, n_heads_q=H, n_heads_kv=H, divisor=divisor,
-                         causal=self.is_decoder, offset=0)
+                         causal=self.is_decoder, offset=0, seq_k=T)
             self.softmax = None
         else:
             heads = self._unfused(q, k, vt, B, T, C, H, D, dt, divisor)
@@ -329,8 +333,8 @@ def _rope_table(T, D, base, pos0):
 
 
 class KVCache:
-    """Per-layer keys [B, Hkv, L, D] and transposed values [B, Hkv, D, L] in HBM, zero
-    filled (positions past the valid length must hold finite values), L a multiple of 8."""
+    """Per-layer keys [B, Hkv, L, D] and transposed values [B, Hkv, D, L] in HBM, L a
+    multiple of 8; positions at or past the valid length are never read as values."""
 
     def __init__(self, n_layers, batch, n_kv_heads, capacity, head_dim, dtype):
         self.capacity = _round_up(capacity, 8)
@@ -383,7 +387,7 @@ class MultiQueryAttention(Layer):
             k, vt, L = cache.k[layer], cache.vt[layer], cache.capacity
         else:
             L = _round_up(T, 8)
-            k, vt = xp.zeros((B, Hkv, L, D), dt), xp.zeros((B, Hkv, D, L), dt)
+            k, vt = xp.empty((B, Hkv, L, D), dt), xp.empty((B, Hkv, D, L), dt)
         linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0))
         table = _rope_table(T, D, self.rope_base, pos0)
         xp.rope(q, table, out=q)

@@ -164,6 +164,7 @@ SIGNATURES = {
     "tl_random_normal": [_P, _P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F32, _F32, _I32],
     "tl_transpose2d": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
+    "tl_patchify": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32],
     "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_layernorm_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_rmsnorm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _F32, _I32],
@@ -628,13 +629,33 @@ def activation(x: DeviceTensor, act: int, out=None):
 
 
 def embed(ids: DeviceTensor, table: DeviceTensor, pos, seq_len, pos0=0, out_shape=None,
-          scale=1.0):
+          scale=1.0, out=None, ld_out=None):
+    """out[t] = table[ids[t]] * scale (+ pos[pos0 + t % seq_len]). With `out`, row t is
+    written at out + t * ld_out elements (e.g. one row per image of a token sequence)."""
     V, C = table.shape
-    out = DeviceTensor(out_shape or (ids.size, C), table.dtype)
+    if out is None:
+        out = DeviceTensor(out_shape or (ids.size, C), table.dtype)
+        ld_out = out.pitch
+    elif ids.size and out.offset + ((ids.size - 1) * ld_out + C) * out.dtype.itemsize > out.buf.nbytes:
+        raise ValueError("embedding rows run past the end of the output buffer")
     lib_, h = _c()
     check(lib_.tl_embed_fwd(h, ids.ptr, ids.dtype.code, table.ptr,
                             pos.ptr if pos is not None else None, out.ptr, ids.size, seq_len,
-                            pos0, V, C, out.pitch, float(scale), table.dtype.code))
+                            pos0, V, C, ld_out, float(scale), table.dtype.code))
+    return out
+
+
+def patchify(x: DeviceTensor, patch, dtype=None) -> DeviceTensor:
+    """[B, C, H, W] -> [B, (H/p0)(W/p1), p0 p1 C] (reference transformer_adapters.py:39-47)."""
+    if not x.contiguous or x.ndim != 4:
+        raise ValueError("patchify needs a contiguous [B, C, H, W] tensor")
+    B, C, H, W = x.shape
+    p0, p1 = patch
+    if H % p0 or W % p1:
+        raise ValueError(f"image {H}x{W} is not a whole number of {p0}x{p1} patches")
+    out = DeviceTensor((B, (H // p0) * (W // p1), p0 * p1 * C), dtype or x.dtype)
+    lib_, h = _c()
+    check(lib_.tl_patchify(h, x.ptr, out.ptr, B, C, H, W, p0, p1, x.dtype.code, out.dtype.code))
     return out
 
 

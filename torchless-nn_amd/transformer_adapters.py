@@ -5,14 +5,84 @@ import numpy as np
 import backend
 import tl_hip as xp
 from utils import Layer
-from layers import linear
+from layers import _packed_nk, linear
 
-__all__ = ["GPTEmbeddingTable", "GPTEmbedFront", "GPTEmbedBack", "VitMLPHead",
+__all__ = ["VitProjector", "GPTEmbeddingTable", "GPTEmbedFront", "GPTEmbedBack", "VitMLPHead",
            "ScaledEmbedFront"]
 
 
 def _round_up(n, m):
     return (n + m - 1) // m * m
+
+
+class VitProjector(Layer):
+    """Image -> token sequence (reference transformer_adapters.py:6-55): patches of
+    patch_size, flattened in (row, column, channel) order, projected by `projection`
+    (no bias), preceded by 1 + num_registers learned tokens, plus positional embeddings.
+
+    Three launches: the patch gather (tl_patchify), one batched GEMM that writes each
+    image's patch rows after its class/register rows with the positional rows added in the
+    epilogue (a residual shared by the whole batch, stride 0), and one gather per
+    class/register row that writes that row of every image (row pitch = tokens x dim)."""
+
+    def __init__(self, input_size: tuple, patch_size: tuple, embedding_dim, num_registers=0):
+        super(VitProjector, self).__init__()
+        self.batch_size = 0
+        self.channels, self.height, self.width = input_size
+        self.patch_size = tuple(patch_size)
+        self.patches_height = self.height // self.patch_size[0]
+        self.patches_width = self.width // self.patch_size[1]
+        self.sequence_length = self.patches_height * self.patches_width
+        self.token_dim = self.patch_size[0] * self.patch_size[1] * self.channels
+        self.embedding_dim = embedding_dim
+        self.cls_reg_size = 1 + num_registers
+        self.tokens = None
+        self.embeddings = None
+        E = embedding_dim
+        self.projection = backend.init_random_tensor((self.token_dim, E), divisor=self.token_dim ** 0.5)
+        self.cls_reg_tokens = backend.init_random_tensor((self.cls_reg_size, E), divisor=E ** 0.5)
+        self.positional_embeddings = backend.init_zeros_tensor((self.cls_reg_size + self.sequence_length, E))
+        self.projection_grads = self.register_param(self.projection)
+        self.cls_reg_token_grads = self.register_param(self.cls_reg_tokens)
+        self.positional_embeddings_grads = self.register_param(self.positional_embeddings)
+        self._zero_ids = None
+
+    def forward(self, input):
+        if not isinstance(input, xp.DeviceTensor):
+            input = xp.array(np.asarray(input, dtype=np.float32), dtype=self.projection.dtype)
+        self.input = input
+        if input.ndim != 4 or tuple(input.shape[1:]) != (self.channels, self.height, self.width):
+            raise ValueError(f"expected images [B, {self.channels}, {self.height}, {self.width}], "
+                             f"got {input.shape}")
+        B = self.batch_size = input.shape[0]
+        dt = self.projection.dtype
+        L, R, E, K = self.sequence_length, self.cls_reg_size, self.embedding_dim, self.token_dim
+        self.tokens = xp.patchify(input, self.patch_size, dtype=dt)  # [B, L, K]
+        out = xp.empty((B, R + L, E), dt)
+        es = dt.itemsize
+        pos = self.positional_embeddings
+        # rows R.. of every image: tokens @ projection + positions[R:]
+        if dt is xp.bfloat16:
+            W, ldb, layout = _packed_nk(self.projection), K, xp.TL_B_NK
+        else:
+            W, ldb, layout = self.projection, E, xp.TL_B_KN
+        body = xp.DeviceTensor((1,), dt, buf=out.buf, offset=out.offset + R * E * es)
+        pos_body = xp.DeviceTensor((L, E), dt, buf=pos.buf, offset=pos.offset + R * E * es)
+        xp.gemm(self.tokens, W, M=L, N=E, K=K, lda=K, ldb=ldb, b_layout=layout, C=body, ldc=E,
+                batch=B, sa=(L * K, 0), sc=((R + L) * E, 0), residual=pos_body, ldr=E,
+                sr=(0, 0), family="gemm_batched")
+        # rows 0..R-1: the class/register token plus its position, for every image
+        if self._zero_ids is None or self._zero_ids.size != B:
+            self._zero_ids = xp.zeros((B,), xp.int32)
+        for r in range(R):
+            tok = xp.DeviceTensor((1, E), dt, buf=self.cls_reg_tokens.buf,
+                                  offset=self.cls_reg_tokens.offset + r * E * es)
+            prow = xp.DeviceTensor((1, E), dt, buf=pos.buf, offset=pos.offset + r * E * es)
+            row = xp.DeviceTensor((1,), dt, buf=out.buf, offset=out.offset + r * E * es)
+            xp.embed(self._zero_ids, tok, prow, 1, out=row, ld_out=(R + L) * E)
+        self.embeddings = out
+        self.output = out
+        return self.output
 
 
 class GPTEmbeddingTable:
