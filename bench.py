@@ -232,6 +232,56 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
     return out
 
 
+def vit_bench(xp, steps=10, warmup=3):
+    """ViT-S/4 bf16 classifier forward over 512 CIFAR-shaped images
+    (65 tokens each) already in HBM; per-step kernel breakdown from HIP events."""
+    import vit
+    cfg = vit.VIT_S4
+    B = 512
+    log("building ViT-S/4 config-4 model (bf16)")
+    net = vit.build_vit(cfg, "bf16")
+    vit.seed_vit(net, 0, 0.02)
+    rng = np.random.default_rng(3)
+    pix = rng.random((B, 3, 32, 32), dtype=np.float32)
+    x = xp.array((pix - np.float32(0.5)) / np.float32(np.sqrt(1.0 / 12.0)), dtype="bf16")
+    for _ in range(warmup):
+        net.predict(x)
+    xp.synchronize()
+    e0, e1 = xp.Event(), xp.Event()
+    e0.record()
+    for _ in range(steps):
+        net.predict(x)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    for _ in range(steps):
+        net.predict(x)
+    xp.synchronize()
+    fam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
+    d, L, T = cfg["d"], cfg["layers"], 65
+    M = B * T
+    dense = L * 2 * M * d * 12 * d + 2 * B * 64 * 48 * d + 2 * B * d * cfg["classes"]
+    attn = L * B * cfg["heads"] * 2 * 2 * T * T * (d // cfg["heads"])
+    out = {
+        "workload": "ViT-S/4 classifier forward (BASELINE config 4): 512 images 3x32x32, patch 4 "
+                    "(64 tokens + CLS), 8 encoder layers, d 384, 6 heads, MLP 1536 GeLU, 10 "
+                    "classes; bf16, weights N(0,0.02) seeded, pixels uniform normalised",
+        "ms_per_step": round(ms, 4),
+        "images_per_s": round(B / (ms * 1e-3), 1),
+        "tokens_per_s": round(M / (ms * 1e-3), 1),
+        "tflops": round((dense + attn) / (ms * 1e-3) / 1e12, 1),
+        "flops": dense + attn,
+        "kernel_breakdown": {f: {"ms_per_step": round(r["ms"] / steps, 4),
+                                 "launches_per_step": r["launches"] // steps}
+                             for f, r in fam.items() if r["launches"]},
+    }
+    log(f"vit config 4: {json.dumps(out)}")
+    del net, x
+    return out
+
+
 def decode_sweep(xp, reps=50):
     """Times each GEMM of a config-5 decode step (M = 4) and one layer's decode attention,
     in GB/s of algorithmic bytes (weights + activations; K and V for attention)."""
@@ -315,6 +365,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-row-kernels", action="store_true")
     ap.add_argument("--no-gemma", action="store_true", help="skip the config-5 decoder section")
+    ap.add_argument("--no-vit", action="store_true", help="skip the config-4 ViT section")
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
@@ -401,6 +452,7 @@ def main():
 
     rows = {} if args.no_row_kernels else row_kernel_bench(xp)
     gem = None if args.no_gemma else gemma_bench(xp)
+    vit_line = None if args.no_vit else vit_bench(xp)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if cpu:
         log(f"cpu baseline: {cpu}")
@@ -421,6 +473,7 @@ def main():
         "kernel_breakdown": breakdown,
         "row_kernels": rows,
         "gemma_decoder": gem,
+        "vit_classifier": vit_line,
     }
     print(json.dumps(line), flush=True)
 
