@@ -96,12 +96,38 @@ def row_kernel_bench(xp, reps=20):
     return out
 
 
-def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None):
-    """Times every MFMA tile shape on the five dense GEMMs of one forward (with their real
-    epilogues) and prints TFLOP/s per (shape, tile); used to tune the tile heuristic."""
+def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None, model="gpt"):
+    """Times every MFMA tile shape on the dense GEMMs of one forward (with their real
+    epilogues) and prints TFLOP/s per (shape, tile); used to tune the tile heuristic.
+    model="gpt": config 3 (M = 8192, d 768, 12 heads, LM head); "vit": config 4 (M = 512 x
+    65 tokens, d 384, 6 heads, no LM head)."""
     rng = np.random.default_rng(0)
-    M, C, V = BATCH * SEQ, CFG["d"], CFG["vocab"]
-    H, D = CFG["heads"], CFG["d"] // CFG["heads"]
+    if model == "square":  # one long-K GEMM: per-tile start-up amortised over 128 K steps
+        a = xp.random_normal((8192, 8192), 1, 0, std=1.0, dtype="bf16")
+        bt = xp.random_normal((8192, 8192), 2, 0, std=0.02, dtype="bf16")
+        c = xp.empty((8192, 8192), "bf16")
+        table = {"square8192": {}}
+        for t in ["auto"] + [t for t in xp.GEMM_TILES if t not in ("auto", "skinny")]:
+            if only_tiles and t not in only_tiles:
+                continue
+            fn = lambda: xp.gemm(a, bt, M=8192, N=8192, K=8192, lda=8192, ldb=8192,
+                                 b_layout=xp.TL_B_NK, C=c, ldc=8192, tile=t)
+            fn()
+            e0, e1 = xp.Event(), xp.Event()
+            e0.record()
+            for _ in range(3):
+                fn()
+            e1.record()
+            ms = e0.elapsed_ms(e1) / 3
+            table["square8192"][t] = {"us": round(ms * 1e3, 1), "tflops": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12, 1)}
+        log("gemm sweep square8192: " + ", ".join(f"{t} {v['tflops']}" for t, v in table["square8192"].items()))
+        return table
+    if model == "vit":
+        BATCH_, SEQ_, C, V, H = 512, 65, 384, 10, 6
+    else:
+        BATCH_, SEQ_, C, V, H = BATCH, SEQ, CFG["d"], CFG["vocab"], CFG["heads"]
+    M, D = BATCH_ * SEQ_, C // H
+    Lk = (SEQ_ + 7) // 8 * 8
 
     def dev(shape, scale=0.02):
         return xp.array(rng.standard_normal(shape).astype(np.float32) * np.float32(scale), dtype="bf16")
@@ -111,13 +137,13 @@ def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None):
     w = {"qkv": dev((3 * C, C)), "out": dev((C, C)), "ffn1": dev((4 * C, C)), "ffn2": dev((C, 4 * C)),
          "head": dev((V, C))}
     b = {k: dev((w[k].shape[0],)) for k in w}
-    q, k, vt = (xp.empty((BATCH, H, SEQ, D), "bf16"), xp.empty((BATCH, H, SEQ, D), "bf16"),
-                xp.empty((BATCH, H, D, SEQ), "bf16"))
+    q, k, vt = (xp.empty((BATCH_, H, SEQ_, D), "bf16"), xp.empty((BATCH_, H, Lk, D), "bf16"),
+                xp.empty((BATCH_, H, D, Lk), "bf16"))
     out_c, out_4c = xp.empty((M, C), "bf16"), xp.empty((M, 4 * C), "bf16")
     logits = xp.empty((M, V), "bf16", pitch=(V + 7) // 8 * 8)
     shapes = {
         "qkv": lambda t: xp.gemm(x, w["qkv"], M=M, N=3 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                 bias=b["qkv"], qkv=(q, k, vt, SEQ, H, H, D), tile=t),
+                                 bias=b["qkv"], qkv=(q, k, vt, SEQ_, H, H, D, Lk, 0), tile=t),
         "out_proj": lambda t: xp.gemm(x, w["out"], M=M, N=C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
                                       C=out_c, ldc=C, bias=b["out"], residual=res, ldr=C, tile=t),
         "ffn1": lambda t: xp.gemm(x, w["ffn1"], M=M, N=4 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
@@ -132,10 +158,10 @@ def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None):
              "ffn2": 2 * M * C * 4 * C, "lm_head": 2 * M * V * C}
     table = {}
     for name, fn in shapes.items():
-        if only_shapes and name not in only_shapes:
+        if only_shapes and name not in only_shapes or (model == "vit" and name == "lm_head"):
             continue
         table[name] = {}
-        for t in ["auto"] + [t for t in xp.GEMM_TILES if t != "auto"]:
+        for t in ["auto"] + [t for t in xp.GEMM_TILES if t not in ("auto", "skinny")]:
             if only_tiles and t not in only_tiles:
                 continue
             for _ in range(2):
@@ -372,6 +398,8 @@ def main():
     ap.add_argument("--sweep-decode", action="store_true",
                     help="only time the config-5 decode-step GEMMs and attention")
     ap.add_argument("--sweep-tiles", default="", help="comma list of tiles for --sweep-gemm")
+    ap.add_argument("--sweep-model", default="gpt", choices=["gpt", "vit", "square"],
+                    help="GEMM shapes for --sweep-gemm: config 3 (gpt) or config 4 (vit)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
                          "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -398,7 +426,8 @@ def main():
     if args.sweep_gemm:
         print(json.dumps({"gemm_sweep": gemm_sweep(
             xp, only_shapes=[x for x in args.sweep_shapes.split(",") if x],
-            only_tiles=[x for x in args.sweep_tiles.split(",") if x])}), flush=True)
+            only_tiles=[x for x in args.sweep_tiles.split(",") if x], model=args.sweep_model)}),
+              flush=True)
         return
     log("building GPT-2-small-shape model (bf16) and seeding weights")
     net, _ = gpt.build_gpt(CFG, dtype="bf16")

@@ -83,7 +83,9 @@ enum tl_gemm_tile {
   TL_TILE_PERSIST_128x128 = 13,
   /* weight streaming for M <= 16 (decode steps): 16 rows of B per workgroup, K split over
    * its 8 waves; chosen by TL_TILE_AUTO whenever M <= 16 */
-  TL_TILE_SKINNY = 14
+  TL_TILE_SKINNY = 14,
+  TL_TILE_DMA_256x256_W8 = 15, /* direct global->LDS, 8 waves of 128x64, 2 stages */
+  TL_TILE_DMA_128x96 = 16      /* direct global->LDS, 4 waves of 64x48, 2 stages */
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

@@ -319,7 +319,8 @@ def test_gemm_qkv_split(xp, dt, heads):
 
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64", "256x256w4",
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
-                                  "dma128x128s3", "persist256x128w8", "persist128x128"])
+                                  "dma128x128s3", "persist256x128w8", "persist128x128",
+                                  "dma256x256w8", "dma128x96"])
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (64, 64, 64), (513, 129, 776), (700, 300, 640)])
 def test_gemm_every_tile_shape(xp, tile, mnk):
     """Forces each MFMA tile shape on ragged M/N and a K tail, with a full epilogue."""

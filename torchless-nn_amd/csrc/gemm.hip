@@ -54,6 +54,7 @@ struct GemmParams {
   int act;
   int b_kn;
   int vec_store;
+  int vec_res;  // residual rows allow one 4-element vector load per lane fragment
   int qkv;
   void* q;
   void* k;
@@ -268,9 +269,23 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
       float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
       finish(v, j);
       if (rrow) {
+        if (cnt[j] == 4 && e.vec_res) {
+          float r[4];
+          if (sizeof(TO) == 2) {
+            const uint2 u = *reinterpret_cast<const uint2*>(rrow + 16 * j);
+            r[0] = __uint_as_float(u.x << 16); r[1] = __uint_as_float(u.x & 0xffff0000u);
+            r[2] = __uint_as_float(u.y << 16); r[3] = __uint_as_float(u.y & 0xffff0000u);
+          } else {
+            const float4 u = *reinterpret_cast<const float4*>(rrow + 16 * j);
+            r[0] = u.x; r[1] = u.y; r[2] = u.z; r[3] = u.w;
+          }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q < cnt[j]) v[q] = v[q] + Elem<TO>::load(rrow + 16 * j + q);
+          for (int q = 0; q < 4; ++q) v[q] = v[q] + r[q];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (q < cnt[j]) v[q] = v[q] + Elem<TO>::load(rrow + 16 * j + q);
+        }
       }
       TO* c = crow + 16 * j;
       if (cnt[j] == 4 && e.vec_store) {
@@ -431,6 +446,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 // so it adds no wait of its own before reading the other stages (it cannot tell the stage
 // arrays apart and would drain every load in flight); the kernel orders them with
 // dma_stage_sync. M0 (the LDS base of the 64 lanes' 16-byte slots) is saved and restored.
+// Scheduling pattern for one K step of fragment reads and MFMAs: NR reads of the first
+// half, then the second half's NR reads each followed by a share of the first half's NM
+// MFMAs, then the second half's NM MFMAs. The fragment registers of both halves stay live,
+// so no MFMA waits for an LDS read issued right before it.
+template <int NR, int NM, int R = 0>
+__device__ __forceinline__ void interleave_reads_mfma() {
+  if constexpr (R < NR) {
+    constexpr int q = NM / NR, rem = NM % NR;
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                       // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, q + (R < rem ? 1 : 0), 0);  // MFMA
+    interleave_reads_mfma<NR, NM, R + 1>();
+  }
+}
+template <int NR, int NM>
+__device__ __forceinline__ void schedule_kstep() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+  interleave_reads_mfma<NR, NM>();
+  __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+}
+
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
 }
@@ -502,33 +537,26 @@ void gemm_dma_kernel(GemmParams p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, fc = lane >> 4;
   const int a_frag = (wm * WM + fr) * BK, b_frag = BM * BK + (wn * WN + fr) * BK;
-  // Both 32-wide K halves' fragments are read before the first MFMA when the wave tile is
-  // small enough (their LDS latency then overlaps the first half's MFMAs); larger wave
-  // tiles read and consume one half at a time to bound register use.
+  // Both 32-wide K halves' fragments are read into their own registers; the second half's
+  // reads are spread over the first half's MFMAs (schedule_kstep).
   auto compute = [&](const bf16_t* S) {
-    constexpr bool kBoth = TM * TN <= 16;
     bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
-      if (s == 0 || !kBoth) {
+    for (int h = 0; h < 2; ++h) {
+      const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
 #pragma unroll
-        for (int h = s; h < (kBoth ? 2 : s + 1); ++h) {
-          const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
+      for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
 #pragma unroll
-          for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
+      for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
+    }
 #pragma unroll
-          for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
-        }
-      }
-      (void)sw;
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s][j], af[s][i], acc[i][j], 0, 0, 0);
-      if (!kBoth) __builtin_amdgcn_sched_barrier(0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[h][j], af[h][i], acc[i][j], 0, 0, 0);
+    schedule_kstep<TM + TN, TM * TN>();
   };
   const int nk = (int)(p.K / BK);
 #pragma unroll
@@ -808,23 +836,32 @@ static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 2
                                    {128, 128, 256}, {128, 64, 256},  {64, 64, 256},
                                    {256, 256, 256}, {256, 128, 512}, {128, 128, 256},
                                    {256, 128, 512}, {128, 64, 256},  {128, 128, 256},
-                                   {256, 128, 512}, {128, 128, 256}};
+                                   {256, 128, 512}, {128, 128, 256}, {16, 16, 256},
+                                   {256, 256, 512}, {128, 96, 256}};
 // resident workgroups per CU of the persistent variants (LDS: 144 KB and 64 KB)
 static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_256x128_W8 ? 1 : 2; }
 
-// Tile choice, from sweeps of the five GPT-2-small GEMMs (M = 8192) on an MI355X
-// (TFLOP/s): the LM head (N = 50257) runs best as 8-wave 256x128 direct-to-LDS tiles with
-// 3 stages (707 vs 642 for 128x128); QKV, FFN1 and FFN2 as 2-stage direct-to-LDS 128x128
-// (393 / 402 / 594); the short-K N = 768 out-projection as 128x64 register-prefetch tiles
-// (283), whose 3 tiles per CU balance better than 1.5. The direct-to-LDS kernels need
-// K % 64 == 0; 64x64 covers grids too small to fill the GPU.
+// Tile choice, from MI355X sweeps of the GPT-2-small (M = 8192) and ViT-S/4 (M = 33280)
+// GEMMs and an 8192^3 square: the direct-to-LDS kernels (K % 64 == 0) run best with 256x256
+// tiles when there are enough of them, else with 128-row tiles sized to the last round of
+// resident workgroups; register-prefetch tiles cover other K; 64x64 covers grids too
+// small to fill the GPU.
 static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
-  const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
-  const int64_t t64 = ((M + 127) / 128) * ((N + 63) / 64) * batch;
-  const bool dma = K % 64 == 0;
-  if (dma && t128 >= 16LL * cus) return TL_TILE_DMA_256x128_W8;
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
+  const int64_t t128 = tiles(128, 128), t64 = tiles(128, 64);
+  if (K % 64 == 0) {
+    // many 256x256 tiles (LM head, large square): 8 waves of 128x64 read the least LDS and
+    // L2 per flop (787 TF on the LM head vs 627; 1335 TF at 8192^3)
+    if (tiles(256, 256) >= 4LL * cus) return TL_TILE_DMA_256x256_W8;
+    // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
+    // workgroups wastes the least area (N = 768 or 2304: 128x96; 3072: 128x128)
+    const int64_t slots = 2LL * cus;
+    const int64_t a128 = (t128 + slots - 1) / slots * 128 * 128;
+    const int64_t t96 = tiles(128, 96);
+    const int64_t a96 = (t96 + slots - 1) / slots * 128 * 96;
+    if (t96 >= cus) return a96 < a128 ? TL_TILE_DMA_128x96 : TL_TILE_DMA_128x128;
+  }
   if (t128 >= 16LL * cus) return TL_TILE_128x128;
-  if (dma && t128 >= cus && !(t128 < 2LL * cus && K <= 1024)) return TL_TILE_DMA_128x128;
   if (t64 >= (int64_t)cus) return TL_TILE_128x64;
   return TL_TILE_64x64;
 }
@@ -865,6 +902,8 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
     case TL_TILE_DMA_128x128_S3: gemm_dma_kernel<TO, 128, 128, 2, 2, 1, 3><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_PERSIST_256x128_W8: gemm_dma_persistent_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_PERSIST_128x128: gemm_dma_persistent_kernel<TO, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_DMA_256x256_W8: gemm_dma_kernel<TO, 256, 256, 2, 4, 2, 2><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_DMA_128x96: gemm_dma_kernel<TO, 128, 96, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
   }
 }
@@ -885,7 +924,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_SKINNY, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_128x96, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -934,6 +973,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
                 d->sc_o % 4 == 0 && d->sc_i % 4 == 0;
   if (geglu) p.vec_store = d->ldc % 2 == 0 && ((uintptr_t)d->C % (2 * eo)) == 0 &&
                            d->sc_o % 2 == 0 && d->sc_i % 2 == 0;
+  p.vec_res = d->residual && d->ldr % 4 == 0 && ((uintptr_t)d->residual % (4 * eo)) == 0 &&
+              d->sr_o % 4 == 0 && d->sr_i % 4 == 0;
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
@@ -980,14 +1021,14 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (mfma) {
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
-    const bool persistent = tile >= TL_TILE_PERSIST_256x128_W8;
+    const bool persistent = tile == TL_TILE_PERSIST_256x128_W8 || tile == TL_TILE_PERSIST_128x128;
     if (persistent && batch != 1) tile = tile == TL_TILE_PERSIST_128x128 ? TL_TILE_DMA_128x128 : TL_TILE_DMA_256x128_W8;
     const TileShape& s = kTiles[tile];
     p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
     p.tiles_n = (int)((d->N + s.bn - 1) / s.bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
-    if (tile >= TL_TILE_PERSIST_256x128_W8) {
+    if (persistent) {
       const int64_t slots = (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256) * persistent_per_cu(tile);
       const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n;
       grid.x = (unsigned)(std::min(slots, (ntiles + 7) / 8 * 8) / 8 * 8);
