@@ -472,12 +472,16 @@ def main():
     log(f"breakdown: {json.dumps(breakdown)}")
     g = fam["gemm_mfma"]
     achieved = g["flops"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] else 0.0
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemm_traffic_gpt2_small_bf16_prefill.json")
+    if os.path.exists(tpath):  # rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated (see the file)
+        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
     roofline = {"bound": "mfma", "kernel": "gemm_mfma_kernel (QKV, out-proj, FFN1, FFN2, LM head)",
                 "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "avg_launch_us": round(g["ms"] / max(1, g["launches"]) * 1e3, 2),
                 "flops_per_launch": round(g["flops"] / max(1, g["launches"])),
-                "traffic": None}
+                "traffic": traffic, "traffic_unit": "bytes per launch (HBM, measured)"}
 
     rows = {} if args.no_row_kernels else row_kernel_bench(xp)
     gem = None if args.no_gemma else gemma_bench(xp)
