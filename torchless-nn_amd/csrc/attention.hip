@@ -67,156 +67,200 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
   const int nqb = (p.Tq + 63) / 64;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest causal blocks first
-  const int q0 = qb * 64 + wave * 16;
-  const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
-  const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
-  const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
+  // Under a causal mask query blocks are processed in pairs (nqb-1-x, x): the pair's chunk
+  // counts sum to nqb + 1 for every x, so all workgroups carry the same work. Without a
+  // mask every block costs the same and each workgroup takes one.
+  const int x = (int)blockIdx.x;
+  for (int pass = 0; pass < (p.causal ? 2 : 1); ++pass) {
+    const int qb = pass == 0 ? nqb - 1 - x : x;
+    if (pass == 1 && qb >= nqb - 1 - x) break;
+    const int q0 = qb * 64 + wave * 16;
+    const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
+    const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
+    const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
 
-  // Q fragments (B operand of S^T): lane holds Q[q0 + fr][32 s + 8 fg .. +7]
-  bf16x8 qf[KS];
-  {
-    const int qi = min(q0 + fr, p.Tq - 1);
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qf[s] = *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * D + 32 * s + 8 * fg);
-  }
+    // Q fragments (B operand of S^T): lane holds Q[q0 + fr][32 s + 8 fg .. +7]
+    bf16x8 qf[KS];
+    {
+      const int qi = min(q0 + fr, p.Tq - 1);
+  #pragma unroll
+      for (int s = 0; s < KS; ++s)
+        qf[s] = *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * D + 32 * s + 8 * fg);
+    }
 
-  // kv range this block needs
-  const int q_last = min(qb * 64 + 63, p.Tq - 1);
-  int kv_end = p.Tk;
-  if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q_last + p.offset + 1);
-  const int nchunks = (kv_end + BKV - 1) / BKV;
+    // kv range this block needs
+    const int q_last = min(qb * 64 + 63, p.Tq - 1);
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q_last + p.offset + 1);
+    const int nchunks = (kv_end + BKV - 1) / BKV;
 
-  uint4 rk[K_LOADS], rv[V_LOADS];
-  auto load_chunk_regs = [&](int kv0) {
-#pragma unroll
+    uint4 rk[K_LOADS], rv[V_LOADS];
+    // Per-thread 32-bit offsets from a per-chunk uniform base (SGPR-based addressing).
+    uint32_t k_off[K_LOADS], v_off[V_LOADS];
+  #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
-      const int kv = kv0 + r;
-      rk[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(kh + (int64_t)kv * D + c * 8) : make_uint4(0, 0, 0, 0);
+      const int idx = i * 256 + tid;
+      k_off[i] = (uint32_t)((idx / KCH) * D + (idx % KCH) * 8);
     }
-#pragma unroll
+  #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its positions
-      // past Tk (capacity padding, never written) are zeroed, since 0 * NaN would not be 0
-      const int kv = kv0 + c * 8;
-      rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Lk + kv) : make_uint4(0, 0, 0, 0);
-      if (kv < p.Tk && kv + 8 > p.Tk) rv[i] = keep_first(rv[i], p.Tk - kv);
+      const int idx = i * 256 + tid;
+      v_off[i] = (uint32_t)((idx >> 3) * p.Lk + (idx & 7) * 8);
     }
-  };
-  auto store_chunk_lds = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
-      *reinterpret_cast<uint4*>(&Ks[buf][r * D + ((c ^ (r & KSW)) << 3)]) = rk[i];
-    }
-#pragma unroll
-    for (int i = 0; i < V_LOADS; ++i) {
-      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      *reinterpret_cast<uint4*>(&Vs[buf][r * BKV + ((c ^ (r & 7)) << 3)]) = rv[i];
-    }
-  };
-
-  f32x4 o[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  const int qpos = q0 + fr;  // this lane's query row (position qpos + offset)
-
-  load_chunk_regs(0);
-  store_chunk_lds(0);
-  __syncthreads();
-  for (int ch = 0; ch < nchunks; ++ch) {
-    const int cur = ch & 1;
-    const int kv0 = ch * BKV;
-    if (ch + 1 < nchunks) load_chunk_regs(kv0 + BKV);
-
-    // S^T for 4 key tiles of 16
-    f32x4 s[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int r = j * 16 + fr;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int c = ks * 4 + fg;
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[cur][r * D + ((c ^ (r & KSW)) << 3)]);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
+    auto load_chunk_regs = [&](int kv0) {
+      const bf16_t* kc = kh + (int64_t)kv0 * D;
+      const bf16_t* vc = vh + kv0;
+      if (kv0 + BKV <= p.Tk) {  // whole chunk valid (uniform)
+  #pragma unroll
+        for (int i = 0; i < K_LOADS; ++i) rk[i] = *reinterpret_cast<const uint4*>(kc + k_off[i]);
+  #pragma unroll
+        for (int i = 0; i < V_LOADS; ++i) rv[i] = *reinterpret_cast<const uint4*>(vc + v_off[i]);
+        return;
       }
-    }
-    // scale, mask, running max
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int kv = kv0 + j * 16 + 4 * fg + v;
-        const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
-        const float x = ok ? s[j][v] * p.scale_log2 : -INFINITY;
-        s[j][v] = x;
-        mx = fmaxf(mx, x);
+  #pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int kv = kv0 + (i * 256 + tid) / KCH;
+        rk[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(kc + k_off[i]) : make_uint4(0, 0, 0, 0);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    float rs = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float e = __builtin_amdgcn_exp2f(s[j][v] - m_new);
-        s[j][v] = e;
-        rs += e;
+  #pragma unroll
+      for (int i = 0; i < V_LOADS; ++i) {
+        // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its positions
+        // past Tk (capacity padding, never written) are zeroed, since 0 * NaN would not be 0
+        const int kv = kv0 + ((i * 256 + tid) & 7) * 8;
+        rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vc + v_off[i]) : make_uint4(0, 0, 0, 0);
+        if (kv < p.Tk && kv + 8 > p.Tk) rv[i] = keep_first(rv[i], p.Tk - kv);
       }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) o[t][v] *= alpha;
+    };
+    auto store_chunk_lds = [&](int buf) {
+  #pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
+        *reinterpret_cast<uint4*>(&Ks[buf][r * D + ((c ^ (r & KSW)) << 3)]) = rk[i];
+      }
+  #pragma unroll
+      for (int i = 0; i < V_LOADS; ++i) {
+        const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
+        *reinterpret_cast<uint4*>(&Vs[buf][r * BKV + ((c ^ (r & 7)) << 3)]) = rv[i];
+      }
+    };
 
-    // O^T += V^T P^T over two 32-key halves
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2) {
-      bf16x8 pf;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        pf[v] = (__bf16)s[2 * c2][v];
-        pf[4 + v] = (__bf16)s[2 * c2 + 1][v];
-      }
-      // keys of item i: 32 c2 + 4 fg + i (i < 4) and 32 c2 + 16 + 4 fg + (i - 4)
-      const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const int r = t * 16 + fr;
-        const bf16_t* row = &Vs[cur][r * BKV];
-        const int ca = ka >> 3, cb = kb >> 3;
-        const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 7)) << 3) + (ka & 7));
-        const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 7)) << 3) + (kb & 7));
-        const uint4 vv = make_uint4(va.x, va.y, vb.x, vb.y);
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
-        o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
-      }
-    }
+    f32x4 o[DT];
+  #pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+    const int qpos = q0 + fr;  // this lane's query row (position qpos + offset)
 
-    if (ch + 1 < nchunks) store_chunk_lds(cur ^ 1);
+    load_chunk_regs(0);
+    store_chunk_lds(0);
     __syncthreads();
-  }
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const int cur = ch & 1;
+      const int kv0 = ch * BKV;
+      if (ch + 1 < nchunks) load_chunk_regs(kv0 + BKV);
 
-  if (qpos < p.Tq) {
-    const float inv = 1.0f / l_run;
-    bf16_t* orow = p.out + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      uint2 w;
-      w.x = (uint32_t)f2bf(o[t][0] * inv) | ((uint32_t)f2bf(o[t][1] * inv) << 16);
-      w.y = (uint32_t)f2bf(o[t][2] * inv) | ((uint32_t)f2bf(o[t][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(orow + t * 16 + 4 * fg) = w;
+      // S^T for 4 key tiles of 16
+      f32x4 s[4];
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int r = j * 16 + fr;
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int c = ks * 4 + fg;
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[cur][r * D + ((c ^ (r & KSW)) << 3)]);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
+        }
+      }
+      // mask (only chunks that cross this wave's causal diagonal or the key count need one:
+      // the test is uniform across the wave), row max of the raw scores
+      float mx = -INFINITY;
+      const bool full = kv0 + BKV <= p.Tk &&
+                        (!p.causal || (int64_t)(kv0 + BKV - 1) <= (int64_t)q0 + p.offset);
+      if (full) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j)
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[j][v]);
+      } else {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j)
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kv = kv0 + j * 16 + 4 * fg + v;
+            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
+            s[j][v] = ok ? s[j][v] : -INFINITY;
+            mx = fmaxf(mx, s[j][v]);
+          }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // Lazy rescaling: the reference max m_run (log2 units) moves only when a row's max
+      // exceeds it by more than 8, so the unnormalised probabilities stay below 2^8 (exact
+      // in fp32, full relative precision in bf16) and O and l are rescaled only then.
+      const float mxs = mx * p.scale_log2;
+      const bool grow = mxs > m_run + 8.0f;
+      if (__any(grow)) {
+        const float m_new = grow ? mxs : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run was -inf
+        l_run *= alpha;
+  #pragma unroll
+        for (int t = 0; t < DT; ++t)
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) o[t][v] *= alpha;
+        m_run = m_new;
+      }
+      const float m_ref = m_run == -INFINITY ? 0.f : m_run;  // a row with no visible key yet
+      float rs = 0.f;
+  #pragma unroll
+      for (int j = 0; j < 4; ++j)
+  #pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][v], p.scale_log2, -m_ref));
+          s[j][v] = e;
+          rs += e;
+        }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l_run += rs;
+
+      // O^T += V^T P^T over two 32-key halves
+  #pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        bf16x8 pf;
+  #pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          pf[v] = (__bf16)s[2 * c2][v];
+          pf[4 + v] = (__bf16)s[2 * c2 + 1][v];
+        }
+        // keys of item i: 32 c2 + 4 fg + i (i < 4) and 32 c2 + 16 + 4 fg + (i - 4)
+        const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
+  #pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const int r = t * 16 + fr;
+          const bf16_t* row = &Vs[cur][r * BKV];
+          const int ca = ka >> 3, cb = kb >> 3;
+          const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 7)) << 3) + (ka & 7));
+          const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 7)) << 3) + (kb & 7));
+          const uint4 vv = make_uint4(va.x, va.y, vb.x, vb.y);
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+          o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
+        }
+      }
+
+      if (ch + 1 < nchunks) store_chunk_lds(cur ^ 1);
+      __syncthreads();
+    }
+
+    if (qpos < p.Tq) {
+      const float inv = 1.0f / l_run;
+      bf16_t* orow = p.out + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
+  #pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        uint2 w;
+        w.x = (uint32_t)f2bf(o[t][0] * inv) | ((uint32_t)f2bf(o[t][1] * inv) << 16);
+        w.y = (uint32_t)f2bf(o[t][2] * inv) | ((uint32_t)f2bf(o[t][3] * inv) << 16);
+        *reinterpret_cast<uint2*>(orow + t * 16 + 4 * fg) = w;
+      }
     }
   }
 }
@@ -511,7 +555,8 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
     }
     return ls.finish("attention_decode");
   }
-  dim3 grid((unsigned)((seq_q + 63) / 64), (unsigned)(batch * n_heads_q));
+  const int64_t nqb = (seq_q + 63) / 64;
+  dim3 grid((unsigned)(causal ? (nqb + 1) / 2 : nqb), (unsigned)(batch * n_heads_q));
   switch (head_dim) {
     case 32: attention_fwd_kernel<32><<<grid, 256, 0, ctx->stream>>>(p); break;
     case 64: attention_fwd_kernel<64><<<grid, 256, 0, ctx->stream>>>(p); break;
