@@ -123,6 +123,42 @@ def test_softmax_causal_offset(xp):
     assert ref.max_rel(y, ref.softmax(s + mask)) <= 1e-5
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("rows,cols", [(20011, 8), (50021, 384), (20011, 768), (12007, 2048)])
+def test_norms_many_rows(xp, dt, rows, cols):
+    """Many short rows (one wavefront each, lanes past the row end masked), an odd row count
+    so the last workgroup is partial; every row must match."""
+    rng = np.random.default_rng(rows + cols)
+    x = rnd(dt, rng.standard_normal((rows, cols)).astype(F32) * 1.5 - 0.25)
+    g = rnd(dt, rng.standard_normal(cols).astype(F32))
+    b = rnd(dt, rng.standard_normal(cols).astype(F32))
+    y = xp.layernorm(up(xp, x, dt), up(xp, g, dt), up(xp, b, dt), F32(1e-5)).get()
+    assert ref.max_rel(y, rnd(dt, ref.layernorm(x, g, b))) <= TOL[dt], (dt, rows, cols)
+    y = xp.rmsnorm(up(xp, x, dt), up(xp, g, dt), F32(1e-6), 1.0).get()
+    assert ref.max_rel(y, rnd(dt, ref.rmsnorm(x, g, F32(1e-6), 1.0))) <= TOL[dt], (dt, rows, cols)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("rows,cols,causal,period,offset",
+                         [(40009, 65, False, 1, 0), (30011, 1024, False, 1, 0),
+                          (40009, 97, True, 97, 0), (30011, 200, True, 37, 150),
+                          (24001, 1024, True, 1024, 0), (20011, 515, True, 512, 3)])
+def test_softmax_many_rows(xp, dt, rows, cols, causal, period, offset):
+    """Many rows, row lengths that are not a multiple of the chunk width, and causal limits
+    (row % period + offset + 1) that cross chunk and wavefront boundaries."""
+    rng = np.random.default_rng(rows + cols + period)
+    x = rnd(dt, rng.standard_normal((rows, cols)).astype(F32) * 2)
+    pitch = (cols + 7) // 8 * 8
+    d = xp.empty((rows, cols), dt, pitch=pitch)
+    d.set(x)
+    y = xp.softmax(d, causal=causal, period=period, offset=offset).get()
+    lim = np.arange(rows) % period + offset + 1 if causal else np.full(rows, cols)
+    keep = np.arange(cols)[None, :] < lim[:, None]
+    want = ref.softmax(np.where(keep, x, F32(-1e9)).astype(F32))
+    assert ref.max_rel(y, want) <= TOL[dt], (dt, rows, cols, causal)
+    assert np.all(y[~keep] == 0)
+
+
 def test_softmax_causal_golden(xp):
     import os
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "softmax_causal_small.npz"))

@@ -22,24 +22,6 @@
 
 namespace tl {
 
-// Division by a run-time invariant d with a multiply-high and a shift (the round-up
-// method of Granlund and Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994): s = ceil(log2 d), mul = floor(2^32 (2^s - d) / d) + 1,
-// n / d = (mulhi(n, mul) + n) >> s for 0 <= n < 2^31.
-struct FastDiv {
-  uint32_t mul, shr;
-};
-static inline FastDiv make_fastdiv(uint32_t d) {
-  if (d <= 1) return FastDiv{0u, 0u};
-  uint32_t s = 0;
-  while ((1ull << s) < d) ++s;
-  const uint64_t mul = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
-  return FastDiv{(uint32_t)mul, s};
-}
-__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
-  return (__umulhi(n, f.mul) + n) >> f.shr;
-}
-
 struct GemmParams {
   const void* A;
   const void* B;
@@ -870,7 +852,6 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
 // Measured on an MI355X at the config-5 decode shapes (M = 4): (4 waves, 16 steps) streams
 // the wide GEMMs fastest (GeGLU 134 MB in 23.9 us, LM head 1.05 GB in 197 us); the others
 // are kept for TL_SKINNY_CFG sweeps.
-static const int kSkinnyCfg[][2] = {{4, 16}, {4, 8}, {8, 16}, {8, 8}, {16, 4}, {8, 4}, {16, 8}};
 
 template <typename TO>
 static void launch_skinny(int cfg, dim3 grid, hipStream_t st, const GemmParams& p, float* part) {

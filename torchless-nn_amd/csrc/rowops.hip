@@ -152,7 +152,11 @@ __global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table
 // ------------------------------------------------------------------------------------
 // LayerNorm / RMSNorm (reference layers.py:415-428)
 // ------------------------------------------------------------------------------------
-// One wavefront per row, CH 16-byte chunks per lane held in registers.
+// One wavefront per row, the row held in registers as raw 16-byte chunks (CH per lane),
+// unpacked to float for each pass. Lanes whose chunk lies past the row end load the row's
+// first chunk (a line the wave fetches anyway) and mask it out, so every load is issued
+// unconditionally. LayerNorm is two-pass (mean, then squared deviations), as the reference
+// computes np.var.
 template <typename T, int CH, bool RMS>
 __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
                                                         const T* __restrict__ g,
@@ -165,36 +169,36 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * ldx;
-  float v[CH][VW];
-  float s = 0.f;
+  uint4 raw[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * 64 + lane) * VW;
-    if (col < cols) {
-      load_chunk(xr + col, v[c]);
-#pragma unroll
-      for (int e = 0; e < VW; ++e) s += RMS ? v[c][e] * v[c][e] : v[c][e];
-    } else {
-#pragma unroll
-      for (int e = 0; e < VW; ++e) v[c][e] = 0.f;
-    }
+    raw[c] = *reinterpret_cast<const uint4*>(xr + (col < cols ? col : 0));
   }
-  const float inv_n = 1.0f / (float)cols;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const bool in = (c * 64 + lane) * VW < cols;
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) s += in ? (RMS ? v[e] * v[e] : v[e]) : 0.f;
+  }
   float mean = 0.f, rstd;
   if (RMS) {
-    rstd = 1.0f / sqrtf(wave_sum(s) * inv_n + eps);
+    rstd = 1.0f / sqrtf(wave_sum(s) / (float)cols + eps);
   } else {
     mean = wave_sum(s) / (float)cols;
     float q = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int col = (c * 64 + lane) * VW;
-      if (col < cols) {
+      const bool in = (c * 64 + lane) * VW < cols;
+      float v[VW];
+      Elem<T>::unpack(raw[c], v);
 #pragma unroll
-        for (int e = 0; e < VW; ++e) {
-          const float d = v[c][e] - mean;
-          q += d * d;
-        }
+      for (int e = 0; e < VW; ++e) {
+        const float d = v[e] - mean;
+        q += in ? d * d : 0.f;
       }
     }
     rstd = 1.0f / sqrtf(wave_sum(q) / (float)cols + eps);
@@ -204,12 +208,13 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
   for (int c = 0; c < CH; ++c) {
     const int col = (c * 64 + lane) * VW;
     if (col < cols) {
-      float gv[VW], bv[VW], o[VW];
+      float v[VW], gv[VW], bv[VW], o[VW];
+      Elem<T>::unpack(raw[c], v);
       load_chunk(g + col, gv);
       if (!RMS) load_chunk(b + col, bv);
 #pragma unroll
       for (int e = 0; e < VW; ++e)
-        o[e] = RMS ? (v[c][e] * rstd) * (goff + gv[e]) : gv[e] * ((v[c][e] - mean) * rstd) + bv[e];
+        o[e] = RMS ? (v[e] * rstd) * (goff + gv[e]) : gv[e] * ((v[e] - mean) * rstd) + bv[e];
       store_chunk(yr + col, o);
     }
   }
@@ -268,9 +273,26 @@ __device__ __forceinline__ float softmax_exp(float z, float temp) {
 }
 
 // Row r keeps columns j < valid(r); the rest are written as exact zeros (the reference's
-// additive -1e9 mask underflows exp to 0). Lanes skip loading masked chunks, so a causal
-// row reads its lower-triangle part only.
-template <typename T, int CH, bool CAUSAL>
+// additive -1e9 mask underflows exp to 0). One wavefront per row, held as raw 16-byte
+// chunks. Lanes whose chunk starts at or past valid(r) load the row's first chunk instead
+// (a line the wave fetches anyway) and mask it out, so every load is issued unconditionally
+// and a causal row reads its lower-triangle part only. TAIL: the row length is not a
+// multiple of the chunk width, so the lane holding the partial last chunk loads it element
+// by element.
+template <typename T>
+__device__ __forceinline__ uint4 load_raw_partial(const T* p, int n) {
+  union {
+    uint4 u;
+    T e[16 / sizeof(T)];
+  } r;
+  r.u = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int e = 0; e < (int)(16 / sizeof(T)); ++e)
+    if (e < n) r.e[e] = p[e];
+  return r.u;
+}
+
+template <typename T, int CH, bool CAUSAL, bool TAIL>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__ x,
                                                            T* __restrict__ y, int64_t rows,
                                                            int cols, int64_t ldx, int64_t ldy,
@@ -286,23 +308,26 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
     valid = lim < cols ? (int)lim : cols;
   }
   const T* xr = x + row * ldx;
+  uint4 raw[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int col = (c * 64 + lane) * VW;
+    if (TAIL && col < valid && col + VW > cols)
+      raw[c] = load_raw_partial(xr + col, cols - col);
+    else
+      raw[c] = *reinterpret_cast<const uint4*>(xr + (col < valid ? col : 0));
+  }
   float v[CH][VW];
   float mx = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * 64 + lane) * VW;
-    if (col + VW <= valid) {
-      load_chunk(xr + col, v[c]);
-    } else if (col < valid) {
+    Elem<T>::unpack(raw[c], v[c]);
 #pragma unroll
-      for (int e = 0; e < VW; ++e)
-        v[c][e] = (col + e < valid) ? Elem<T>::load(xr + col + e) : -INFINITY;
-    } else {
-#pragma unroll
-      for (int e = 0; e < VW; ++e) v[c][e] = -INFINITY;
+    for (int e = 0; e < VW; ++e) {
+      v[c][e] = col + e < valid ? v[c][e] : -INFINITY;
+      mx = fmaxf(mx, v[c][e]);
     }
-#pragma unroll
-    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[c][e]);
   }
   mx = wave_max(mx);
   float s = 0.f;
@@ -316,17 +341,17 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
       s += ex;
     }
   }
-  const float r = 1.0f / wave_sum(s);
+  const float rs = 1.0f / wave_sum(s);
   T* yr = y + row * ldy;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * 64 + lane) * VW;
     float o[VW];
 #pragma unroll
-    for (int e = 0; e < VW; ++e) o[e] = v[c][e] * r;
+    for (int e = 0; e < VW; ++e) o[e] = v[c][e] * rs;
     if (col + VW <= cols) {
       store_chunk(yr + col, o);
-    } else if (col < cols) {
+    } else if (TAIL && col < cols) {
       for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
     }
   }
@@ -527,20 +552,21 @@ __global__ void rope_table_kernel(float* table, int64_t seq_len, int64_t head_di
   }
 }
 
-template <typename T, bool VEC>
+// One thread per (row, chunk of the first half): it loads that chunk and the matching chunk
+// of the second half, rotates both with the position's cos/sin (from the fp32 table, read
+// through L2) and writes both. Item indices are split with 32-bit multiply-high division
+// when the item count is below 2^31 (SMALL), else with 64-bit division in a grid-stride loop.
+template <typename T, bool VEC, bool SMALL>
 __global__ __launch_bounds__(256) void rope_kernel(const T* x, T* y, const float* __restrict__ table,
                                                    int64_t n_seq, int64_t seq_len,
-                                                   int64_t head_dim, int64_t seq_stride) {
+                                                   int64_t head_dim, int64_t seq_stride,
+                                                   FastDiv div_row, FastDiv div_seq) {
   constexpr int VW = VEC ? Elem<T>::kVec : 1;
   const int64_t half = head_dim / 2;
   const int64_t per_row = half / VW;
   const int64_t total = n_seq * seq_len * per_row;
   const int64_t tsz = seq_len * half;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = idx / per_row;
-    const int64_t i = (idx % per_row) * VW;
-    const int64_t sq = row / seq_len, t = row - sq * seq_len;
+  auto item = [&](int64_t row, int64_t i, int64_t sq, int64_t t) {
     const T* xr = x + sq * seq_stride + t * head_dim;
     T* yr = y + sq * seq_stride + t * head_dim;
     const float* cs = table + t * half + i;
@@ -574,6 +600,21 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* x, T* y, const float
       Elem<T>::store(yr + i, o1[0]);
       Elem<T>::store(yr + half + i, o2[0]);
     }
+  };
+  if (SMALL) {
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= (uint32_t)total) return;
+    const uint32_t row = fast_div(idx, div_row);
+    const uint32_t i = (idx - row * (uint32_t)per_row) * VW;
+    const uint32_t sq = fast_div(row, div_seq);
+    item(row, i, sq, row - sq * (uint32_t)seq_len);
+    return;
+  }
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = idx / per_row;
+    const int64_t sq = row / seq_len;
+    item(row, (idx % per_row) * VW, sq, row - sq * seq_len);
   }
 }
 
@@ -738,10 +779,9 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
   const bool vec = cols % VW == 0 && ldx % VW == 0 && ldy % VW == 0 && aligned16(x) &&
                    aligned16(y) && aligned16(g) && (RMS || aligned16(b));
   const int64_t chunks = (cols / VW + 63) / 64;
-  const unsigned gw = (unsigned)((rows + 3) / 4);
   auto wave = [&](auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
-    norm_wave_kernel<T, CH, RMS><<<gw, 256, 0, ctx->stream>>>(
+    norm_wave_kernel<T, CH, RMS><<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
         (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff);
   };
   if (vec && chunks <= 1) wave(std::integral_constant<int, 1>());
@@ -758,13 +798,18 @@ template <typename T, bool CAUSAL>
 static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
                            int64_t ldx, int64_t ldy, float temp, int64_t period, int64_t offset) {
   constexpr int VW = Elem<T>::kVec;
-  const bool vec = ldx % VW == 0 && ldy % VW == 0 && aligned16(x) && aligned16(y);
+  // masked lanes of the wave kernels read the row's first whole chunk: needs cols >= VW
+  const bool vec = ldx % VW == 0 && ldy % VW == 0 && aligned16(x) && aligned16(y) && cols >= VW;
   const int64_t chunks = (cols + VW - 1) / VW;
-  const unsigned gw = (unsigned)((rows + 3) / 4);
   auto wave = [&](auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
-    softmax_wave_kernel<T, CH, CAUSAL><<<gw, 256, 0, ctx->stream>>>(
-        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+    auto go = [&](auto tail_tag) {
+      constexpr bool TAIL = decltype(tail_tag)::value;
+      softmax_wave_kernel<T, CH, CAUSAL, TAIL><<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
+          (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+    };
+    if (cols % VW == 0) go(std::false_type());
+    else go(std::true_type());
   };
   auto block = [&](auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
@@ -808,13 +853,19 @@ static void launch_rope(tl_ctx* ctx, const void* x, void* y, const void* table, 
   const bool vec = half % VW == 0 && aligned16(x) && aligned16(y) && aligned16(table) &&
                    (seq_len * half) % 4 == 0 && seq_stride % VW == 0;
   const int64_t work = n_seq * seq_len * (vec ? half / VW : half);
-  const unsigned g = grid_for(ctx, work, 256);
-  if (vec)
-    rope_kernel<T, true><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
-                                                      n_seq, seq_len, head_dim, seq_stride);
-  else
-    rope_kernel<T, false><<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table,
-                                                       n_seq, seq_len, head_dim, seq_stride);
+  const bool small = work < (int64_t)0x7fffffff;
+  const FastDiv dr = make_fastdiv(small ? (uint32_t)(vec ? half / VW : half) : 1u);
+  const FastDiv ds = make_fastdiv(small ? (uint32_t)seq_len : 1u);
+  const unsigned g = small ? (unsigned)std::max<int64_t>(1, (work + 255) / 256) : grid_for(ctx, work, 256);
+  auto go = [&](auto vec_tag, auto small_tag) {
+    rope_kernel<T, decltype(vec_tag)::value, decltype(small_tag)::value>
+        <<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table, n_seq, seq_len,
+                                     head_dim, seq_stride, dr, ds);
+  };
+  if (vec && small) go(std::true_type(), std::true_type());
+  else if (vec) go(std::true_type(), std::false_type());
+  else if (small) go(std::false_type(), std::true_type());
+  else go(std::false_type(), std::false_type());
 }
 
 template <typename T>

@@ -122,6 +122,24 @@ __device__ __forceinline__ bf16_t f2bf(float f) {
   return __builtin_bit_cast(bf16_t, b);
 }
 
+// Division by a run-time invariant d with a multiply-high and a shift (the round-up
+// method of Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): s = ceil(log2 d), mul = floor(2^32 (2^s - d) / d) + 1,
+// n / d = (mulhi(n, mul) + n) >> s for 0 <= n < 2^31.
+struct FastDiv {
+  uint32_t mul, shr;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  if (d <= 1) return FastDiv{0u, 0u};
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  const uint64_t mul = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
+  return FastDiv{(uint32_t)mul, s};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.mul) + n) >> f.shr;
+}
+
 template <typename T> struct Elem;
 template <> struct Elem<float> {
   static constexpr int kVec = 4;  // elements per 16-byte chunk
