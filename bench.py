@@ -93,6 +93,15 @@ def row_kernel_bench(xp, reps=20):
         tab = xp.rope_table(T, D, 10000.0)
         timed(f"rope_{dt}_8x12x1024x64", lambda i: xp.rope(rx[i], tab, out=ry[i]), es * 2.0 * B * H * T * D, nrot)
         del rx, ry
+        # the config-3 vocabulary softmax: [B*T, 50257] logits at a row pitch of 50264
+        R, V, P = 8192, 50257, 50264
+        vx = []
+        for i in range(2):
+            full = xp.random_normal((R, P), seed=7, stream=i, std=3.0, dtype=dt)
+            vx.append(xp.DeviceTensor((R, V), full.dtype, pitch=P, buf=full.buf, offset=full.offset))
+        vy = [xp.empty((R, V), dt, pitch=P) for _ in range(2)]
+        timed(f"softmax_vocab_{dt}_8192x50257", lambda i: xp.softmax(vx[i], out=vy[i]), es * 2.0 * R * V, 2)
+        del vx, vy
     return out
 
 
@@ -390,6 +399,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-row-kernels", action="store_true")
+    ap.add_argument("--only-row-kernels", action="store_true",
+                    help="only time the standalone row kernels (a tuning run, no model)")
     ap.add_argument("--no-gemma", action="store_true", help="skip the config-5 decoder section")
     ap.add_argument("--no-vit", action="store_true", help="skip the config-4 ViT section")
     ap.add_argument("--sweep-gemm", action="store_true",
@@ -422,6 +433,9 @@ def main():
         log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
     if args.sweep_decode:
         print(json.dumps({"decode_sweep": decode_sweep(xp)}), flush=True)
+        return
+    if args.only_row_kernels:
+        print(json.dumps({"row_kernels": row_kernel_bench(xp)}), flush=True)
         return
     if args.sweep_gemm:
         print(json.dumps({"gemm_sweep": gemm_sweep(

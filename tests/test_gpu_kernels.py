@@ -142,7 +142,10 @@ def test_norms_many_rows(xp, dt, rows, cols):
 @pytest.mark.parametrize("rows,cols,causal,period,offset",
                          [(40009, 65, False, 1, 0), (30011, 1024, False, 1, 0),
                           (40009, 97, True, 97, 0), (30011, 200, True, 37, 150),
-                          (24001, 1024, True, 1024, 0), (20011, 515, True, 512, 3)])
+                          (24001, 1024, True, 1024, 0), (20011, 515, True, 512, 3),
+                          (77, 9000, False, 1, 0), (2500, 4104, True, 2500, 1600),
+                          (600, 5001, True, 600, 4700), (40, 50257, False, 1, 0),
+                          (64, 65000, True, 64, 64900)])
 def test_softmax_many_rows(xp, dt, rows, cols, causal, period, offset):
     """Many rows, row lengths that are not a multiple of the chunk width, and causal limits
     (row % period + offset + 1) that cross chunk and wavefront boundaries."""

@@ -370,140 +370,140 @@ __device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) 
   return r;
 }
 
-// One workgroup of NT threads per row (vocabulary-sized rows), row held in registers.
-template <typename T, int NT, int CH, bool CAUSAL>
-__global__ __launch_bounds__(NT) void softmax_block_kernel(const T* __restrict__ x,
-                                                           T* __restrict__ y, int64_t rows,
-                                                           int cols, int64_t ldx, int64_t ldy,
-                                                           float temp, int64_t period,
-                                                           int64_t offset) {
-  constexpr int VW = Elem<T>::kVec;
-  __shared__ float red[NT / 64];
-  const int64_t row = blockIdx.x;
-  int valid = cols;
-  if (CAUSAL) {
-    const int64_t lim = row % period + offset + 1;
-    valid = lim < cols ? (int)lim : cols;
-  }
-  const T* xr = x + row * ldx;
-  float v[CH][VW];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int col = (c * NT + threadIdx.x) * VW;
-    if (col + VW <= valid) {
-      load_chunk(xr + col, v[c]);
-    } else if (col < valid) {
-#pragma unroll
-      for (int e = 0; e < VW; ++e)
-        v[c][e] = (col + e < valid) ? Elem<T>::load(xr + col + e) : -INFINITY;
-    } else {
-#pragma unroll
-      for (int e = 0; e < VW; ++e) v[c][e] = -INFINITY;
-    }
-#pragma unroll
-    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[c][e]);
-  }
-  mx = block_reduce<NT>(mx, true, red);
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int col = (c * NT + threadIdx.x) * VW;
-#pragma unroll
-    for (int e = 0; e < VW; ++e) {
-      const float ex = (col + e < valid) ? softmax_exp(v[c][e] - mx, temp) : 0.f;
-      v[c][e] = ex;
-      s += ex;
-    }
-  }
-  const float r = 1.0f / block_reduce<NT>(s, false, red);
-  T* yr = y + row * ldy;
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int col = (c * NT + threadIdx.x) * VW;
-    float o[VW];
-#pragma unroll
-    for (int e = 0; e < VW; ++e) o[e] = v[c][e] * r;
-    if (col + VW <= cols) {
-      store_chunk(yr + col, o);
-    } else if (col < cols) {
-      for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
-    }
-  }
-}
-
-// Long rows (vocabulary softmax): 256 threads per row keep the row as packed 16-byte
-// chunks (raw bf16 or fp32 bits, 4 registers per chunk) instead of unpacked floats, so
-// several rows fit per CU and one row's loads overlap another's reductions and stores.
-// A partial last chunk is padded with -inf; exp is evaluated again in the output pass.
+// The packed -inf pattern of a 16-byte chunk.
 template <typename T>
 __device__ __forceinline__ uint4 neg_inf_chunk() {
   return sizeof(T) == 2 ? make_uint4(0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u)
                         : make_uint4(0xFF800000u, 0xFF800000u, 0xFF800000u, 0xFF800000u);
 }
 
-template <typename T, int NT, int CH>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT >= 1024 ? 4 : 3, 8)))
-void softmax_rowreg_kernel(const T* __restrict__ x, T* __restrict__ y, int64_t rows, int cols,
-                           int64_t ldx, int64_t ldy, float temp) {
+// Long rows (vocabulary softmax, long causal rows), one workgroup of NT threads per row, the
+// row held as raw 16-byte chunks (CH per thread). Each thread takes the max m_t of its own
+// elements (those past the row's causal limit count as -inf and come out as 0), then
+// e = 2^(k (x - m_t)) with k = log2(e) / temperature (one FMA and one exp2 per element) and
+// their sum s_t; the workgroup merges the (m_t, s_t) pairs in a single reduction into the
+// row's (M, S), and each thread writes e * 2^(k (m_t - M)) / S. KEEP holds e in fp32
+// registers between the passes; otherwise the output pass recomputes it from the chunks.
+__device__ __forceinline__ void merge_max_sum(float& m, float& s, float om, float os, float k) {
+  const float M = fmaxf(m, om);
+  if (M == -INFINITY) return;  // both empty
+  s = s * __builtin_amdgcn_exp2f((m - M) * k) + os * __builtin_amdgcn_exp2f((om - M) * k);
+  m = M;
+}
+
+template <typename T, int NT, int CH, bool CAUSAL, bool KEEP>
+__global__ __launch_bounds__(NT) void softmax_long_kernel(const T* __restrict__ x,
+                                                          T* __restrict__ y, int64_t rows,
+                                                          int cols, int64_t ldx, int64_t ldy,
+                                                          float k, int64_t period,
+                                                          int64_t offset) {
   constexpr int VW = Elem<T>::kVec;
-  __shared__ float red[NT / 64];
+  constexpr int NW = NT / 64;
+  __shared__ float wm[NW], wsum[NW];
   const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
   const T* xr = x + row * ldx;
+  int valid = cols;
+  if (CAUSAL) {
+    const int64_t lim = row % period + offset + 1;
+    valid = lim < cols ? (int)lim : cols;
+  }
+  // Elements at or past `valid` hold -inf: they drop out of the max, and 2^(k (-inf - m)) = 0,
+  // so the passes need no per-element masks and the masked outputs are exact zeros.
+  const uint4 ninf = neg_inf_chunk<T>();
   uint4 raw[CH];
-  float mx = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * NT + threadIdx.x) * VW;
-    if (col + VW <= cols) {
+    const int col = (c * NT + tid) * VW;
+    if (c * NT * VW >= valid) {
+      raw[c] = ninf;  // whole chunk past the limit (uniform)
+    } else if (col + VW <= valid) {
       raw[c] = *reinterpret_cast<const uint4*>(xr + col);
-    } else if (col < cols) {
-      float t[VW];
+    } else if (col < valid) {
+      union {
+        uint4 u;
+        T e[VW];
+      } r;
+      r.u = ninf;
 #pragma unroll
-      for (int e = 0; e < VW; ++e) t[e] = col + e < cols ? Elem<T>::load(xr + col + e) : -INFINITY;
-      raw[c] = Elem<T>::pack(t);
+      for (int e = 0; e < VW; ++e)
+        if (e < valid - col) r.e[e] = xr[col + e];
+      raw[c] = r.u;
     } else {
-      raw[c] = neg_inf_chunk<T>();
+      raw[c] = ninf;
     }
-    float v[VW];
-    Elem<T>::unpack(raw[c], v);
-#pragma unroll
-    for (int e = 0; e < VW; ++e) mx = fmaxf(mx, v[e]);
   }
-  // The empty asm makes the packed chunks opaque between passes, so each pass unpacks
-  // them again instead of keeping every unpacked float live (which would spill).
+  // The empty asm makes the packed chunks opaque between passes, so each pass unpacks them
+  // again instead of keeping every unpacked float (or every exponential) live.
   auto opaque = [&]() {
 #pragma unroll
     for (int c = 0; c < CH; ++c)
       asm volatile("" : "+v"(raw[c].x), "+v"(raw[c].y), "+v"(raw[c].z), "+v"(raw[c].w));
   };
-  mx = block_reduce<NT>(mx, true, red);
-  opaque();
-  float s = 0.f;
+  float m_t = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float v[VW];
     Elem<T>::unpack(raw[c], v);
 #pragma unroll
-    for (int e = 0; e < VW; ++e) s += softmax_exp(v[e] - mx, temp);
+    for (int e = 0; e < VW; ++e) m_t = fmaxf(m_t, v[e]);
   }
-  const float r = 1.0f / block_reduce<NT>(s, false, red);
   opaque();
+  const float mk = m_t == -INFINITY ? 0.f : m_t * k;  // a thread past the row keeps e = 0
+  float ev[KEEP ? CH : 1][VW];
+  float s_t = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk));
+      if (KEEP) ev[KEEP ? c : 0][e] = ex;
+      s_t += ex;
+    }
+  }
+  if (!KEEP) opaque();
+  float m = m_t, s = s_t;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float om = __shfl_xor(m, o, 64), os = __shfl_xor(s, o, 64);
+    merge_max_sum(m, s, om, os, k);
+  }
+  if ((tid & 63) == 0) {
+    wm[tid >> 6] = m;
+    wsum[tid >> 6] = s;
+  }
+  __syncthreads();
+  float M = wm[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, wm[w]);
+  float S = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w)
+    S += wm[w] == -INFINITY ? 0.f : wsum[w] * __builtin_amdgcn_exp2f((wm[w] - M) * k);
+  const float f = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_t - M) * k) / S;
   T* yr = y + row * ldy;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * NT + threadIdx.x) * VW;
-    if (col >= cols) continue;
-    float v[VW];
-    Elem<T>::unpack(raw[c], v);
+    const int col = (c * NT + tid) * VW;
+    if (c * NT * VW >= cols) break;  // uniform
+    float o[VW];
+    if (KEEP) {
 #pragma unroll
-    for (int e = 0; e < VW; ++e) v[e] = softmax_exp(v[e] - mx, temp) * r;
-    if (col + VW <= cols) {
-      store_chunk(yr + col, v);
+      for (int e = 0; e < VW; ++e) o[e] = ev[KEEP ? c : 0][e] * f;
     } else {
+      float v[VW];
+      Elem<T>::unpack(raw[c], v);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) o[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk)) * f;
+    }
+    if (col + VW <= cols) {
+      store_chunk(yr + col, o);
+    } else if (col < cols) {
 #pragma unroll
       for (int e = 0; e < VW; ++e)
-        if (col + e < cols) Elem<T>::store(yr + col + e, v[e]);
+        if (e < cols - col) Elem<T>::store(yr + col + e, o[e]);
     }
   }
 }
@@ -811,38 +811,52 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
     if (cols % VW == 0) go(std::false_type());
     else go(std::true_type());
   };
-  auto block = [&](auto ch_tag) {
-    constexpr int CH = decltype(ch_tag)::value;
-    softmax_block_kernel<T, 1024, CH, CAUSAL><<<(unsigned)rows, 1024, 0, ctx->stream>>>(
-        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+  // Long rows: (threads, keep e in registers) by TL_SOFTMAX_LONG_CFG (1: 1024, 2: 1024 kept,
+  // 3: 512, 4: 512 kept); by default 512 threads for bf16 rows up to 8192 chunks (three rows
+  // resident per CU) and 1024 threads otherwise, e kept for fp32. Chunks per thread: the
+  // smallest instantiated count that covers the row.
+  const int lcfg = ctx->softmax_long_cfg;
+  auto longrow = [&](auto nt_tag, bool keep) -> bool {
+    constexpr int NT = decltype(nt_tag)::value;
+    bool done = false;
+    auto try_ch = [&](auto ch_tag) {
+      constexpr int CH = decltype(ch_tag)::value;
+      if (done || (int64_t)NT * CH < chunks) return;
+      const float k = 1.4426950408889634f / temp;
+      if (keep && CH * VW <= 64)
+        softmax_long_kernel<T, NT, CH, CAUSAL, (CH * VW <= 64)><<<(unsigned)rows, NT, 0, ctx->stream>>>(
+            (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
+      else
+        softmax_long_kernel<T, NT, CH, CAUSAL, false><<<(unsigned)rows, NT, 0, ctx->stream>>>(
+            (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
+      done = true;
+    };
+    try_ch(std::integral_constant<int, 2>());
+    try_ch(std::integral_constant<int, 4>());
+    if (NT == 1024) try_ch(std::integral_constant<int, 7>());
+    try_ch(std::integral_constant<int, 8>());
+    try_ch(std::integral_constant<int, 13>());
+    try_ch(std::integral_constant<int, 16>());
+    return done;
   };
-  auto rowreg = [&](auto nt_tag, auto ch_tag) {
-    constexpr int NT = decltype(nt_tag)::value, CH = decltype(ch_tag)::value;
-    softmax_rowreg_kernel<T, NT, CH><<<(unsigned)rows, NT, 0, ctx->stream>>>(
-        (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp);
-  };
-  using I256 = std::integral_constant<int, 256>;
-  using I512 = std::integral_constant<int, 512>;
-  using I1024 = std::integral_constant<int, 1024>;
-  using C8 = std::integral_constant<int, 8>;
-  using C16 = std::integral_constant<int, 16>;
-  using C24 = std::integral_constant<int, 24>;
-  constexpr bool bf = sizeof(T) == 2;  // fp32 spills at 24 chunks per thread or 1024 threads
-  if (vec && chunks <= 64) wave(std::integral_constant<int, 1>());
-  else if (vec && chunks <= 128) wave(std::integral_constant<int, 2>());
-  else if (vec && chunks <= 256) wave(std::integral_constant<int, 4>());
-  else if (vec && chunks <= 512) wave(std::integral_constant<int, 8>());
-  else if (vec && !CAUSAL && chunks <= 256 * 8) rowreg(I256(), C8());
-  else if (vec && !CAUSAL && chunks <= 256 * 16) rowreg(I256(), C16());
-  else if (vec && !CAUSAL && bf && chunks <= 256 * 24) rowreg(I256(), C24());
-  else if (vec && !CAUSAL && chunks <= 512 * 16) rowreg(I512(), C16());
-  else if (vec && !CAUSAL && bf && chunks <= 512 * 24) rowreg(I512(), C24());
-  else if (vec && !CAUSAL && bf && chunks <= 1024 * 16) rowreg(I1024(), C16());
-  else if (vec && chunks <= 1024 * 4) block(std::integral_constant<int, 4>());
-  else if (vec && chunks <= 1024 * 8) block(std::integral_constant<int, 8>());
-  else
+  constexpr bool bf = sizeof(T) == 2;
+  if (vec && chunks <= 64) {
+    wave(std::integral_constant<int, 1>());
+  } else if (vec && chunks <= 128) {
+    wave(std::integral_constant<int, 2>());
+  } else if (vec && chunks <= 256) {
+    wave(std::integral_constant<int, 4>());
+  } else if (vec && chunks <= 512) {
+    wave(std::integral_constant<int, 8>());
+  } else if (vec && chunks <= 1024 * 16) {
+    const int c = lcfg >= 1 && lcfg <= 4 ? lcfg : (bf ? 3 : 2);
+    const bool keep = c % 2 == 0;
+    if (c >= 3 && chunks <= 512 * 16) longrow(std::integral_constant<int, 512>(), keep);
+    else longrow(std::integral_constant<int, 1024>(), keep);
+  } else {
     softmax_generic_kernel<T, CAUSAL><<<(unsigned)rows, 256, 0, ctx->stream>>>(
         (const T*)x, (T*)y, rows, cols, ldx, ldy, temp, period, offset);
+  }
 }
 
 template <typename T>

@@ -164,6 +164,7 @@ int tl_init(int device, tl_ctx** out) {
   if (const char* g = std::getenv("TL_SKINNY_CFG")) ctx->skinny_cfg = std::atoi(g);
   if (const char* g = std::getenv("TL_SKINNY_MAX_SPLIT")) ctx->skinny_max_split = std::atoi(g);
   if (const char* g = std::getenv("TL_ATTN_DECODE_CFG")) ctx->attn_decode_cfg = std::atoi(g);
+  if (const char* g = std::getenv("TL_SOFTMAX_LONG_CFG")) ctx->softmax_long_cfg = std::atoi(g);
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

@@ -55,6 +55,8 @@ struct tl_ctx {
   int skinny_cfg = 0;
   int skinny_max_split = 16;  // TL_SKINNY_MAX_SPLIT
   int attn_decode_cfg = 0;
+  // long-row softmax shape (TL_SOFTMAX_LONG_CFG): 0 default, 1..4 (threads, keep) choices
+  int softmax_long_cfg = 0;
   // grow-only scratch for kernels that combine partial results (split argmax, split-KV
   // attention); used in stream order, so one buffer serves every call on this context
   void* ws = nullptr;
