@@ -48,6 +48,54 @@ struct GemmParams {
   FastDiv div_T, div_Dh;
 };
 
+// Global-memory access through an address-space-1 pointer. The epilogue's pointers come
+// from the parameter block, so the compiler cannot prove they are global and would emit
+// flat instructions, which also count in the LDS wait counter: every wait for an LDS read
+// would then wait for the stores issued before it as well.
+// (HIP's uint2/uint4 are C++ structs whose assignment takes a generic `this`, so 8- and
+// 16-byte accesses go through native vector types.)
+template <typename T>
+__device__ __forceinline__ void gstore(T* p, const T& v) {
+  *(__attribute__((address_space(1))) T*)p = v;
+}
+template <typename T>
+__device__ __forceinline__ T gload(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)p;
+}
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void gstore16(void* p, uint4 v) {
+  const u32x4_t t = {v.x, v.y, v.z, v.w};
+  *(__attribute__((address_space(1))) u32x4_t*)p = t;
+}
+__device__ __forceinline__ void gstore8(void* p, uint2 v) {
+  const u32x2_t t = {v.x, v.y};
+  *(__attribute__((address_space(1))) u32x2_t*)p = t;
+}
+__device__ __forceinline__ uint2 gload8(const void* p) {
+  const u32x2_t t = *(const __attribute__((address_space(1))) u32x2_t*)p;
+  return make_uint2(t.x, t.y);
+}
+template <typename T>
+__device__ __forceinline__ void gstore_elem(T* p, float v) {
+  if (sizeof(T) == 4) gstore(reinterpret_cast<float*>(p), v);
+  else gstore(reinterpret_cast<bf16_t*>(p), f2bf(v));
+}
+template <typename T>
+__device__ __forceinline__ float gload_elem(const T* p) {
+  if (sizeof(T) == 4) return gload(reinterpret_cast<const float*>(p));
+  return bf2f(gload(reinterpret_cast<const bf16_t*>(p)));
+}
+__device__ __forceinline__ void gstore_f4(float* p, const float (&v)[4]) {
+  gstore16(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                         __float_as_uint(v[3])));
+}
+__device__ __forceinline__ void gload_f4(const float* p, float (&v)[4]) {
+  const u32x4_t t = *(const __attribute__((address_space(1))) u32x4_t*)p;
+  v[0] = __uint_as_float(t.x); v[1] = __uint_as_float(t.y);
+  v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
+}
+
 // Applies the epilogue to 4 consecutive columns n0..n0+3 of row m and stores them.
 template <typename TI, typename TO>
 __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64_t zi, int64_t m,
@@ -61,12 +109,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
   if (p.bias) {
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (e < cnt) v[e] = v[e] + Elem<TI>::load((const TI*)p.bias + n0 + e);
+      if (e < cnt) v[e] = v[e] + gload_elem((const TI*)p.bias + n0 + e);
   }
   if (p.geglu) {  // columns (gate f, up f, gate f+1, up f+1), n0 even
     TO* c = (TO*)p.C + zo * p.sc_o + zi * p.sc_i + m * p.ldc + n0 / 2;
-    Elem<TO>::store(c, apply_act(v[0], p.act) * v[1]);
-    if (cnt == 4) Elem<TO>::store(c + 1, apply_act(v[2], p.act) * v[3]);
+    gstore_elem(c, apply_act(v[0], p.act) * v[1]);
+    if (cnt == 4) gstore_elem(c + 1, apply_act(v[2], p.act) * v[3]);
     return;
   }
   if (p.act != TL_ACT_NONE) {
@@ -77,7 +125,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
     const TO* r = (const TO*)p.res + zo * p.sr_o + zi * p.sr_i + m * p.ldr + n0;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      if (e < cnt) v[e] = v[e] + Elem<TO>::load(r + e);
+      if (e < cnt) v[e] = v[e] + gload_elem(r + e);
   }
   if (p.qkv) {
     // Dh % 4 == 0 (checked on the host), so the 4 columns share one head of one part.
@@ -103,25 +151,25 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
       uint2 w;
       w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
       w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-      *reinterpret_cast<uint2*>(dst) = w;
+      gstore8(dst, w);
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) Elem<TO>::store(dst + e * step, v[e]);
+      for (int e = 0; e < 4; ++e) gstore_elem(dst + e * step, v[e]);
     }
     return;
   }
   TO* c = (TO*)p.C + zo * p.sc_o + zi * p.sc_i + m * p.ldc + n0;
   if (cnt == 4 && p.vec_store) {
     if (sizeof(TO) == 4) {
-      *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+      gstore_f4(reinterpret_cast<float*>(c), *reinterpret_cast<const float(*)[4]>(v));
     } else {
       uint2 w;
       w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
       w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-      *reinterpret_cast<uint2*>(c) = w;
+      gstore8(c, w);
     }
   } else {
-    for (int e = 0; e < cnt; ++e) Elem<TO>::store(c + e, v[e]);
+    for (int e = 0; e < cnt; ++e) gstore_elem(c + e, v[e]);
   }
 }
 
@@ -156,7 +204,7 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
     cnt[j] = n >= e.N ? 0 : (e.N - n >= 4 ? 4 : (int)(e.N - n));
 #pragma unroll
     for (int q = 0; q < 4; ++q)
-      bias[j][q] = (e.bias && q < cnt[j]) ? bf2f(((const bf16_t*)e.bias)[n + q]) : 0.f;
+      bias[j][q] = (e.bias && q < cnt[j]) ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
   }
   auto finish = [&](float (&v)[4], int j) {
 #pragma unroll
@@ -200,15 +248,15 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
             uint2 w;
             w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
             w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-            *reinterpret_cast<uint2*>(dst) = w;
+            gstore8(dst, w);
           } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + q, v[q]);
+            for (int q = 0; q < 4; ++q) gstore_elem(dst + q, v[q]);
           }
         } else {
           TO* dst = cbase[j] + rv;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) Elem<TO>::store(dst + (int64_t)q * e.L, v[q]);
+          for (int q = 0; q < 4; ++q) gstore_elem(dst + (int64_t)q * e.L, v[q]);
         }
       }
     }
@@ -229,10 +277,10 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
         const float h0 = apply_act(v[0], e.act) * v[1], h1 = apply_act(v[2], e.act) * v[3];
         TO* c = crow + 8 * j;
         if (sizeof(TO) == 2 && cnt[j] == 4 && e.vec_store) {
-          *reinterpret_cast<uint32_t*>(c) = (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16);
+          gstore(reinterpret_cast<uint32_t*>(c), (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16));
         } else {
-          Elem<TO>::store(c, h0);
-          if (cnt[j] == 4) Elem<TO>::store(c + 1, h1);
+          gstore_elem(c, h0);
+          if (cnt[j] == 4) gstore_elem(c + 1, h1);
         }
       }
     }
@@ -254,33 +302,32 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
         if (cnt[j] == 4 && e.vec_res) {
           float r[4];
           if (sizeof(TO) == 2) {
-            const uint2 u = *reinterpret_cast<const uint2*>(rrow + 16 * j);
+            const uint2 u = gload8(rrow + 16 * j);
             r[0] = __uint_as_float(u.x << 16); r[1] = __uint_as_float(u.x & 0xffff0000u);
             r[2] = __uint_as_float(u.y << 16); r[3] = __uint_as_float(u.y & 0xffff0000u);
           } else {
-            const float4 u = *reinterpret_cast<const float4*>(rrow + 16 * j);
-            r[0] = u.x; r[1] = u.y; r[2] = u.z; r[3] = u.w;
+            gload_f4(reinterpret_cast<const float*>(rrow + 16 * j), r);
           }
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = v[q] + r[q];
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (q < cnt[j]) v[q] = v[q] + Elem<TO>::load(rrow + 16 * j + q);
+            if (q < cnt[j]) v[q] = v[q] + gload_elem(rrow + 16 * j + q);
         }
       }
       TO* c = crow + 16 * j;
       if (cnt[j] == 4 && e.vec_store) {
         if (sizeof(TO) == 4) {
-          *reinterpret_cast<float4*>(c) = make_float4(v[0], v[1], v[2], v[3]);
+          gstore_f4(reinterpret_cast<float*>(c), v);
         } else {
           uint2 w;
           w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
           w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-          *reinterpret_cast<uint2*>(c) = w;
+          gstore8(c, w);
         }
       } else {
-        for (int q = 0; q < cnt[j]; ++q) Elem<TO>::store(c + q, v[q]);
+        for (int q = 0; q < cnt[j]; ++q) gstore_elem(c + q, v[q]);
       }
     }
   }

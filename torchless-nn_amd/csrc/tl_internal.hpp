@@ -207,10 +207,13 @@ __device__ __forceinline__ float logistic_times(float x, float two_u) {
 }
 // tanh-approximation GeLU, reference activations.py:24-28:
 //   0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
+// With u = k (x + 0.044715 x^3), k = sqrt(2/pi): the exponent -2 u log2(e) is evaluated as
+// x (c1 + c2 x^2) with c1 = -2 k log2(e), c2 = 0.044715 c1 folded (three operations).
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k = 0.7978845608028654f;  // sqrt(2/pi) rounded to fp32
-  const float u = k * (x + 0.044715f * (x * x * x));
-  return logistic_times(x, 2.0f * u);
+  const float c1 = -2.302208198144325f;    // -2 sqrt(2/pi) log2(e)
+  const float c2 = -0.1029432395800235f;   // 0.044715 * c1
+  const float e = __builtin_amdgcn_exp2f(x * __builtin_fmaf(c2, x * x, c1));
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 // SiLU through tanh, reference activations.py:41-45: x * (1 + tanh(x/2)) / 2
 __device__ __forceinline__ float silu_tanh(float x) { return logistic_times(x, x); }
