@@ -356,6 +356,51 @@ def test_gemm_qkv_split(xp, dt, heads):
         assert ref.max_rel(got.get(), want) <= TOL[dt]
 
 
+@pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x64s3", "dma128x128s3",
+                                  "dma256x256w8", "dma128x96"])
+@pytest.mark.parametrize("mnk", [(300, 524, 192), (513, 1000, 256), (64, 60, 64), (1000, 777, 128)])
+def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
+    """bf16 outputs of the direct-to-LDS tiles go through the LDS-staged epilogue: every kind
+    (plain, bias, bias+GeLU, bias+SiLU, bias+residual, residual) on ragged M and N, with
+    N % 8 != 0 (partial last 16-byte piece) and N % 4 != 0 (residual kinds then take the
+    generic epilogue); the row padding past N must stay untouched."""
+    M, N, K = mnk
+    rng = np.random.default_rng(M + 3 * N + K)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+    wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    res = ref.round_bf16(rng.standard_normal((M, N)).astype(F32))
+    ldc = (N + 7) // 8 * 8
+    dres = xp.empty((M, N), "bf16", pitch=ldc)
+    dres.set(res)
+    da, dw, db = up(xp, a, "bf16"), up(xp, wt, "bf16"), up(xp, bias, "bf16")
+    kinds = [dict(), dict(bias=True), dict(bias=True, act="gelu"), dict(bias=True, act="silu"),
+             dict(bias=True, res=True), dict(res=True)]
+    for c in kinds:
+        full = xp.empty((M, ldc), "bf16").fill(7.0)
+        out = xp.DeviceTensor((M, N), full.dtype, pitch=ldc, buf=full.buf, offset=full.offset)
+        act = {None: xp.TL_ACT_NONE, "gelu": xp.TL_ACT_GELU, "silu": xp.TL_ACT_SILU}[c.get("act")]
+        xp.gemm(da, dw, M=M, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK, C=out, ldc=ldc,
+                bias=db if c.get("bias") else None, act=act,
+                residual=dres if c.get("res") else None, ldr=ldc, tile=tile)
+        want = gemm_ref(a, wt.T, bias if c.get("bias") else None, c.get("act"),
+                        res if c.get("res") else None)
+        got = full.get()
+        assert ref.max_rel(got[:, :N], ref.round_bf16(want)) <= 2e-2, (tile, mnk, c)
+        assert np.all(got[:, N:] == 7.0), (tile, mnk, c)
+    # batched (two-level strides) plain product on the same tile
+    Bt, H = 2, 3
+    x = ref.round_bf16(rng.standard_normal((Bt, H, 96, 128)).astype(F32))
+    y = ref.round_bf16(rng.standard_normal((Bt, H, 40, 128)).astype(F32))
+    o = xp.empty((Bt, 96, H * 40), "bf16")
+    xp.gemm(up(xp, x, "bf16"), up(xp, y, "bf16"), M=96, N=40, K=128, lda=128, ldb=128,
+            b_layout=xp.TL_B_NK, C=o, ldc=H * 40, batch=Bt * H, batch_inner=H,
+            sa=(H * 96 * 128, 96 * 128), sb=(H * 40 * 128, 40 * 128), sc=(96 * H * 40, 40),
+            family="gemm_batched", tile=tile)
+    want = np.einsum("bhmk,bhnk->bmhn", x.astype(np.float64), y.astype(np.float64)).reshape(Bt, 96, H * 40)
+    assert ref.max_rel(o.get(), ref.round_bf16(want)) <= 2e-2, (tile, "batched")
+
+
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64", "256x256w4",
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
                                   "dma128x128s3", "persist256x128w8", "persist128x128",
