@@ -401,6 +401,41 @@ def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
     assert ref.max_rel(o.get(), ref.round_bf16(want)) <= 2e-2, (tile, "batched")
 
 
+@pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x96", "dma256x256w8",
+                                  "dma128x64s3"])
+@pytest.mark.parametrize("cfg", [(2, 64, 12, 12, 64, 192, 0), (3, 40, 8, 1, 32, 128, 16),
+                                 (1, 136, 2, 2, 16, 64, 0), (2, 24, 3, 1, 24, 128, 8)])
+def test_gemm_qkv_staged_scatter(xp, tile, cfg):
+    """QKV head scatter of the direct-to-LDS tiles (bf16, D/T/L/pos0 multiples of 8): Q and
+    K rows from 16-byte row pieces, V^T rows from a transposed LDS block; wave slabs that
+    straddle Q/K/V take the generic epilogue. Cache slots outside [pos0, pos0 + T) stay 0."""
+    B, T, Hq, Hkv, D, C, pos0 = cfg
+    N = (Hq + 2 * Hkv) * D
+    L = (pos0 + T + 7) // 8 * 8 + 8
+    rng = np.random.default_rng(B * T + Hq + D)
+    x = ref.round_bf16(rng.standard_normal((B * T, C)).astype(F32))
+    w = ref.round_bf16(rng.standard_normal((C, N)).astype(F32) / np.sqrt(C))
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    q = xp.empty((B, Hq, T, D), "bf16")
+    k = xp.zeros((B, Hkv, L, D), "bf16")
+    vt = xp.zeros((B, Hkv, D, L), "bf16")
+    for with_bias in (True, False):
+        xp.gemm(up(xp, x, "bf16"), up(xp, np.ascontiguousarray(w.T), "bf16"), M=B * T, N=N, K=C,
+                lda=C, ldb=C, b_layout=xp.TL_B_NK, bias=up(xp, bias, "bf16") if with_bias else None,
+                qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0), tile=tile)
+        y = ref.round_bf16(gemm_ref(x, w, bias if with_bias else None)).reshape(B, T, N)
+        qw, kw = Hq * D, Hkv * D
+        want_q = y[..., :qw].reshape(B, T, Hq, D).transpose(0, 2, 1, 3)
+        want_k = y[..., qw:qw + kw].reshape(B, T, Hkv, D).transpose(0, 2, 1, 3)
+        want_vt = y[..., qw + kw:].reshape(B, T, Hkv, D).transpose(0, 2, 3, 1)
+        kg, vg = k.get(), vt.get()
+        assert ref.max_rel(q.get(), want_q) <= 2e-2, (tile, cfg, "q")
+        assert ref.max_rel(kg[:, :, pos0:pos0 + T], want_k) <= 2e-2, (tile, cfg, "k")
+        assert ref.max_rel(vg[..., pos0:pos0 + T], want_vt) <= 2e-2, (tile, cfg, "vt")
+        assert np.all(kg[:, :, :pos0] == 0) and np.all(kg[:, :, pos0 + T:] == 0)
+        assert np.all(vg[..., :pos0] == 0) and np.all(vg[..., pos0 + T:] == 0)
+
+
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64", "256x256w4",
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
                                   "dma128x128s3", "persist256x128w8", "persist128x128",

@@ -26,7 +26,8 @@ namespace tl {
 // residual known at compile time, so the fragment loops carry no per-element tests);
 // EPI_GENERIC keeps mfma_epilogue (QKV scatter, GeGLU, fp32 output, divisor, unaligned
 // residual rows or output rows).
-enum EpiKind { EPI_GENERIC = 0, EPI_PLAIN, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_SILU, EPI_BIAS_RES, EPI_RES };
+enum EpiKind { EPI_GENERIC = 0, EPI_PLAIN, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_SILU, EPI_BIAS_RES, EPI_RES,
+               EPI_QKV, EPI_QKV_BIAS };
 
 struct GemmParams {
   const void* A;
@@ -437,6 +438,102 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& e, int64_t zo,
   }
 }
 
+// QKV head scatter through LDS (bf16; D, T, cache capacity L and write position all
+// multiples of 8). A wave whose column slab lies in Q or K stages its rows as above and
+// writes each 16-byte row piece (8 consecutive d of one head) to q[b, h, t, :] or
+// k[b, h, pos0 + t, :]. A slab in V is staged transposed (column c holds the WM rows, its
+// 16-byte units rotated by c against bank conflicts) and each unit, 8 consecutive t of one
+// d, goes to vt[b, h, d, pos0 + t .. + 7], so the transposed V rows are written whole
+// instead of with 2-byte stores. Returns false (nothing written) for a slab that straddles
+// two parts; the caller then runs the generic epilogue for that wave.
+template <bool BIAS, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ bool staged_qkv_epilogue(const GemmParams& e, int64_t mw, int64_t nw,
+                                                    f32x4 (&acc)[TM][TN], bf16_t* region) {
+  constexpr int U = WN / 8, RU = WM / 8;
+  static_assert(WN % 16 == 0 && (WM * U) % 64 == 0 && WM % 8 == 0, "staged qkv shape");
+  const int qw = e.Hq * e.Dh, kw = e.Hkv * e.Dh;
+  if (nw >= e.N) return true;  // slab past N: nothing to write
+  const int n_lo = (int)nw, n_hi = (int)min(nw + WN, e.N) - 1;
+  const int part = n_lo < qw ? 0 : (n_lo < qw + kw ? 1 : 2);
+  const int part_hi = n_hi < qw ? 0 : (n_hi < qw + kw ? 1 : 2);
+  if (part_hi != part) return false;
+  const int lane = threadIdx.x & 63, fr = lane & 15, fc = lane >> 4;
+  uint8_t* reg = reinterpret_cast<uint8_t*>(region);
+  float bias[BIAS ? TN : 1][4];
+  if (BIAS) {
+#pragma unroll
+    for (int j = 0; j < (BIAS ? TN : 1); ++j) {
+      const int64_t n = nw + 16 * j + 4 * fc;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bias[j][q] = n + q < e.N ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
+    }
+  }
+  const int base = part == 0 ? 0 : (part == 1 ? qw : qw + kw);
+  if (part < 2) {
+    // destination of this part, selected once: q [B, Hq, T, D] or k [B, Hkv, L, D] at pos0
+    const uintptr_t dbase = part == 0 ? (uintptr_t)e.q : (uintptr_t)e.k;
+    const int heads = part == 0 ? e.Hq : e.Hkv, tdim = part == 0 ? e.T : e.L;
+    const int toff = part == 0 ? 0 : e.pos0;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = 16 * i + fr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        if (BIAS) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = v[q] + bias[BIAS ? j : 0][q];
+        }
+        uint2 w;
+        w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+        w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+        const int u = 2 * j + (fc >> 1);
+        *reinterpret_cast<uint2*>(reg + (r * U + (u + r) % U) * 16 + (fc & 1) * 8) = w;
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < WM * U / 64; ++p) {
+      const int q = p * 64 + lane, r = q / U, u = q - r * U;
+      const uint4 val = *reinterpret_cast<const uint4*>(reg + (r * U + (u + r) % U) * 16);
+      const int64_t m = mw + r, n = nw + 8 * u;
+      if (m >= e.M || n >= e.N) continue;
+      const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
+      const int nn = (int)n - base;
+      const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
+      gstore16(reinterpret_cast<bf16_t*>(dbase) + ((int64_t)(b * heads + h) * tdim + t + toff) * e.Dh + d, val);
+    }
+    return true;
+  }
+  // V: transposed staging, element (column c, row r) at column c's unit (r / 8 + c) % RU
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = 16 * i + fr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = acc[i][j][q];
+        if (BIAS) v = v + bias[BIAS ? j : 0][q];
+        const int c = 16 * j + 4 * fc + q;
+        *reinterpret_cast<bf16_t*>(reg + (c * RU + ((r >> 3) + c) % RU) * 16 + (r & 7) * 2) = f2bf(v);
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < WN * RU / 64; ++p) {
+    const int q = p * 64 + lane, c = q / RU, ru = q - c * RU;
+    const uint4 val = *reinterpret_cast<const uint4*>(reg + (c * RU + (ru + c) % RU) * 16);
+    const int64_t m = mw + 8 * ru, n = nw + c;  // rows m .. m+7 share b (T % 8 == 0)
+    if (m >= e.M || n >= e.N) continue;
+    const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
+    const int nn = (int)n - base;
+    const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
+    gstore16((bf16_t*)e.vt + ((int64_t)(b * e.Hkv + h) * e.Dh + d) * e.L + t + e.pos0, val);
+  }
+  return true;
+}
+
 // Block id -> output tile: workgroups are dispatched round-robin over the 8 XCDs, so XCD x
 // runs blocks x, x+8, ...; give it the contiguous run [x q + min(x, r), ...) of the
 // grouped order.
@@ -697,6 +794,7 @@ void gemm_dma_kernel(GemmParams p) {
   }
 
   const GemmParams e = late_params();
+  bool done = false;
   if constexpr (sizeof(TO) == 2) {
     if (e.epi != EPI_GENERIC) {
       // each wave's WM x WN block goes to its own region of the stage arrays, once every
@@ -706,18 +804,21 @@ void gemm_dma_kernel(GemmParams p) {
       __syncthreads();
       bf16_t* region = stage(wave / WPA) + (wave % WPA) * (WM * WN);
       const int64_t mw = m0 + wm * WM, nw = n0 + wn * WN;
+      done = true;
       switch (e.epi) {
         case EPI_PLAIN: staged_epilogue<EPI_PLAIN, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_BIAS: staged_epilogue<EPI_BIAS, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_BIAS_GELU: staged_epilogue<EPI_BIAS_GELU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_BIAS_SILU: staged_epilogue<EPI_BIAS_SILU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_BIAS_RES: staged_epilogue<EPI_BIAS_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
-        default: staged_epilogue<EPI_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
+        case EPI_RES: staged_epilogue<EPI_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
+        case EPI_QKV_BIAS: done = staged_qkv_epilogue<true, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
+        default: done = staged_qkv_epilogue<false, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
       }
-      return;
     }
   }
-  mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
+  // one call site: a wave whose QKV slab straddles two parts continues here
+  if (!done) mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
 }
 
 // gemm_dma_persistent_kernel: gemm_dma_kernel with one workgroup per resident slot
@@ -1130,6 +1231,10 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     else if (b && r && d->act == TL_ACT_NONE) p.epi = EPI_BIAS_RES;
     else if (!b && r && d->act == TL_ACT_NONE) p.epi = EPI_RES;
   }
+  if (qkv && eo == 2 && d->divisor == 1.0f && d->act == TL_ACT_NONE && !d->residual &&
+      d->head_dim % 8 == 0 && d->seq_len % 8 == 0 && p.L % 8 == 0 && p.pos0 % 8 == 0 &&
+      ((uintptr_t)d->q % 16) == 0 && ((uintptr_t)d->k % 16) == 0 && ((uintptr_t)d->vt % 16) == 0)
+    p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
