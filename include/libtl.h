@@ -85,7 +85,8 @@ enum tl_gemm_tile {
    * its 8 waves; chosen by TL_TILE_AUTO whenever M <= 16 */
   TL_TILE_SKINNY = 14,
   TL_TILE_DMA_256x256_W8 = 15, /* direct global->LDS, 8 waves of 128x64, 2 stages */
-  TL_TILE_DMA_128x96 = 16      /* direct global->LDS, 4 waves of 64x48, 2 stages */
+  TL_TILE_DMA_128x96 = 16,     /* direct global->LDS, 4 waves of 64x48, 2 stages */
+  TL_TILE_DMA_256x96_W8 = 17   /* direct global->LDS, 8 waves of 64x48, 3 stages */
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

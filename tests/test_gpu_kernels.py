@@ -357,7 +357,7 @@ def test_gemm_qkv_split(xp, dt, heads):
 
 
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x64s3", "dma128x128s3",
-                                  "dma256x256w8", "dma128x96"])
+                                  "dma256x256w8", "dma128x96", "dma256x96w8"])
 @pytest.mark.parametrize("mnk", [(300, 524, 192), (513, 1000, 256), (64, 60, 64), (1000, 777, 128)])
 def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
     """bf16 outputs of the direct-to-LDS tiles go through the LDS-staged epilogue: every kind
@@ -402,7 +402,7 @@ def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
 
 
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x96", "dma256x256w8",
-                                  "dma128x64s3"])
+                                  "dma128x64s3", "dma256x96w8"])
 @pytest.mark.parametrize("cfg", [(2, 64, 12, 12, 64, 192, 0), (3, 40, 8, 1, 32, 128, 16),
                                  (1, 136, 2, 2, 16, 64, 0), (2, 24, 3, 1, 24, 128, 8)])
 def test_gemm_qkv_staged_scatter(xp, tile, cfg):
@@ -439,7 +439,7 @@ def test_gemm_qkv_staged_scatter(xp, tile, cfg):
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64", "256x256w4",
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
                                   "dma128x128s3", "persist256x128w8", "persist128x128",
-                                  "dma256x256w8", "dma128x96"])
+                                  "dma256x256w8", "dma128x96", "dma256x96w8"])
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (64, 64, 64), (513, 129, 776), (700, 300, 640)])
 def test_gemm_every_tile_shape(xp, tile, mnk):
     """Forces each MFMA tile shape on ragged M/N and a K tail, with a full epilogue."""

@@ -708,10 +708,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 void gemm_dma_kernel(GemmParams p) {
   constexpr int NW = WGM * WGN, BK = 64;
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
-  constexpr int GA = BM / 8, GB = BN / 8, L = (GA + GB) / NW;  // 1 KB groups per wave
-  static_assert((GA + GB) % NW == 0 && TM >= 1 && TN >= 1, "bad tile/wave split");
+  // 1 KB load groups per K step: GA of A, then GB of B. Waves 0..R-1 issue LMAX of them,
+  // the others LMAX - 1 (when NW does not divide the count), each wave waiting on its own.
+  constexpr int GA = BM / 8, GB = BN / 8, GT = GA + GB;
+  constexpr int LMAX = (GT + NW - 1) / NW, R = GT - (LMAX - 1) * NW;
+  static_assert(TM >= 1 && TN >= 1, "bad tile/wave split");
   static_assert(STAGES == 2 || STAGES == 3, "2 or 3 stages");
-  static_assert(L * (STAGES - 2) <= 63, "vmcnt range");
+  static_assert(LMAX * (STAGES - 2) <= 63, "vmcnt range");
   constexpr int SZ = (BM + BN) * BK;
   __shared__ __attribute__((aligned(16))) bf16_t S0[SZ];
   __shared__ __attribute__((aligned(16))) bf16_t S1[SZ];
@@ -721,6 +724,8 @@ void gemm_dma_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave - wm * WGN;
+  const bool full = wave < R;  // this wave issues LMAX groups per K step
+  const int g0 = full ? wave * LMAX : R * LMAX + (wave - R) * (LMAX - 1);
   const int64_t z = blockIdx.z;
   const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
   int tm, tn;
@@ -728,22 +733,23 @@ void gemm_dma_kernel(GemmParams p) {
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const bf16_t* Ab = (const bf16_t*)p.A + zo * p.sa_o + zi * p.sa_i + m0 * p.lda;
   const bf16_t* Bb = (const bf16_t*)p.B + zo * p.sb_o + zi * p.sb_i + n0 * p.ldb;
-  uint32_t off[L];
+  uint32_t off[LMAX];
   {
     const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
     const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
     const int rin = lane >> 3, c = (lane & 7) ^ rin;
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int g = wave * L + j;
+    for (int j = 0; j < LMAX; ++j) {
+      const int g = min(g0 + j, GT - 1);
       off[j] = g < GA ? (uint32_t)(min(8 * g + rin, a_last) * p.lda + c * 8)
                       : (uint32_t)(min(8 * (g - GA) + rin, b_last) * p.ldb + c * 8);
     }
   }
   auto issue = [&](bf16_t* S, int64_t k0) {
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int g = wave * L + j;
+    for (int j = 0; j < LMAX; ++j) {
+      if (j == LMAX - 1 && !full) break;
+      const int g = g0 + j;
       const bf16_t* src = (g < GA ? Ab : Bb) + k0 + off[j];
       dma_load16(src, lds_offset(S + g * 512));
     }
@@ -786,8 +792,12 @@ void gemm_dma_kernel(GemmParams p) {
       const int t = kt + u;
       if (t >= nk) break;
       // tiles t+1 .. t+STAGES-2 may stay in flight
-      if (STAGES == 3 && t + 1 < nk) dma_stage_sync<L * (STAGES - 2)>();
-      else dma_stage_sync<0>();
+      if (STAGES == 3 && t + 1 < nk) {
+        if (full) dma_stage_sync<LMAX * (STAGES - 2)>();
+        else dma_stage_sync<(LMAX - 1) * (STAGES - 2)>();
+      } else {
+        dma_stage_sync<0>();
+      }
       if (t + STAGES - 1 < nk) issue(stage((u + STAGES - 1) % STAGES), (int64_t)(t + STAGES - 1) * BK);
       compute(stage(u));
     }
@@ -1079,7 +1089,7 @@ static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 2
                                    {256, 256, 256}, {256, 128, 512}, {128, 128, 256},
                                    {256, 128, 512}, {128, 64, 256},  {128, 128, 256},
                                    {256, 128, 512}, {128, 128, 256}, {16, 16, 256},
-                                   {256, 256, 512}, {128, 96, 256}};
+                                   {256, 256, 512}, {128, 96, 256},  {256, 96, 512}};
 // resident workgroups per CU of the persistent variants (LDS: 144 KB and 64 KB)
 static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_256x128_W8 ? 1 : 2; }
 
@@ -1095,6 +1105,17 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
     // many 256x256 tiles (LM head, large square): 8 waves of 128x64 read the least LDS and
     // L2 per flop (787 TF on the LM head vs 627; 1335 TF at 8192^3)
     if (tiles(256, 256) >= 4LL * cus) return TL_TILE_DMA_256x256_W8;
+    // 256-row tiles with a 3-stage pipeline (two K steps of loads in flight, one workgroup
+    // per CU) when they fill at least one round: inside a forward the weights arrive cold and
+    // the activations from the previous kernel, and the deeper pipeline beats two 2-stage
+    // 128-row workgroups per CU (GPT-2 prefill 4.06 -> 3.88 ms with 256x128 alone) though
+    // it is slower on operands hot in cache. Width 96 or 128, whichever wastes less area in
+    // the last round (GPT-2: 96 fills whole rounds at N = 768, 2304 and 3072).
+    const int64_t t96w = tiles(256, 96), t128w = tiles(256, 128);
+    if (K >= 256 && t96w >= cus) {
+      const int64_t w96 = (t96w + cus - 1) / cus * 96, w128 = (t128w + cus - 1) / cus * 128;
+      return w96 <= w128 ? TL_TILE_DMA_256x96_W8 : TL_TILE_DMA_256x128_W8;
+    }
     // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
     // workgroups wastes the least area (N = 768 or 2304: 128x96; 3072: 128x128)
     const int64_t slots = 2LL * cus;
@@ -1145,6 +1166,7 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
     case TL_TILE_PERSIST_128x128: gemm_dma_persistent_kernel<TO, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_256x256_W8: gemm_dma_kernel<TO, 256, 256, 2, 4, 2, 2><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_DMA_128x96: gemm_dma_kernel<TO, 128, 96, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_DMA_256x96_W8: gemm_dma_kernel<TO, 256, 96, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
     default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
   }
 }
@@ -1165,7 +1187,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_128x96, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_256x96_W8, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
