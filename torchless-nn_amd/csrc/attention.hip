@@ -147,7 +147,10 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
     f32x4 o[DT];
   #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;
+    // m_run: the row's reference max (log2 units, the same in the 4 lanes of a row);
+    // l_part: this lane's share of the row sum (its own key columns), reduced across the 4
+    // lanes once after the last chunk
+    float m_run = -INFINITY, l_part = 0.f;
     const int qpos = q0 + fr;  // this lane's query row (position qpos + offset)
 
     load_chunk_regs(0);
@@ -192,17 +195,20 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
             mx = fmaxf(mx, s[j][v]);
           }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       // Lazy rescaling: the reference max m_run (log2 units) moves only when a row's max
       // exceeds it by more than 8, so the unnormalised probabilities stay below 2^8 (exact
-      // in fp32, full relative precision in bf16) and O and l are rescaled only then.
-      const float mxs = mx * p.scale_log2;
-      const bool grow = mxs > m_run + 8.0f;
-      if (__any(grow)) {
+      // in fp32, full relative precision in bf16) and O and l are rescaled only then. A
+      // lane's own max decides whether any row may grow; only then (the first visible chunk,
+      // rarely after) is the row max taken across the row's 4 lanes, so the common chunk
+      // needs no cross-lane exchange.
+      if (__any(mx * p.scale_log2 > m_run + 8.0f)) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mxs = mx * p.scale_log2;
+        const bool grow = mxs > m_run + 8.0f;  // the same in the row's 4 lanes
         const float m_new = grow ? mxs : m_run;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 when m_run was -inf
-        l_run *= alpha;
+        l_part *= alpha;
   #pragma unroll
         for (int t = 0; t < DT; ++t)
   #pragma unroll
@@ -210,18 +216,14 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
         m_run = m_new;
       }
       const float m_ref = m_run == -INFINITY ? 0.f : m_run;  // a row with no visible key yet
-      float rs = 0.f;
   #pragma unroll
       for (int j = 0; j < 4; ++j)
   #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][v], p.scale_log2, -m_ref));
           s[j][v] = e;
-          rs += e;
+          l_part += e;
         }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l_run += rs;
 
       // O^T += V^T P^T over two 32-key halves
   #pragma unroll
@@ -251,6 +253,8 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
       __syncthreads();
     }
 
+    float l_run = l_part + __shfl_xor(l_part, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
     if (qpos < p.Tq) {
       const float inv = 1.0f / l_run;
       bf16_t* orow = p.out + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
