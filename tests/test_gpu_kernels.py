@@ -527,6 +527,31 @@ def test_gemm_skinny_qkv_cache_and_gated(xp, C):
     assert ref.max_rel(h.get(), want) <= 2e-2
 
 
+@pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x96", "dma256x256w8",
+                                  "dma128x64s3", "dma256x96w8"])
+@pytest.mark.parametrize("mnk", [(300, 1040, 192), (513, 1032, 128), (64, 2048, 64)])
+def test_gemm_gated_staged(xp, tile, mnk):
+    """Gated (GeGLU) products of the direct-to-LDS tiles: pairs (gate f, up f) interleaved
+    in N give act(gate) * up in [M, N/2]; N/2 % 8 == 0 takes the LDS-staged epilogue,
+    N/2 % 8 != 0 the generic one; GeLU and SiLU; padding past N/2 untouched."""
+    M, N, K = mnk
+    F = N // 2
+    rng = np.random.default_rng(M + N + K)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+    w = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+    ldc = (F + 7) // 8 * 8 + 8
+    t = gemm_ref(a, w.T)
+    for act, code, fn in (("gelu", xp.TL_ACT_GELU, ref.gelu), ("silu", xp.TL_ACT_SILU, ref.silu)):
+        full = xp.empty((M, ldc), "bf16").fill(7.0)
+        h = xp.DeviceTensor((M, F), full.dtype, pitch=ldc, buf=full.buf, offset=full.offset)
+        xp.gemm(up(xp, a, "bf16"), up(xp, w, "bf16"), M=M, N=N, K=K, lda=K, ldb=K,
+                b_layout=xp.TL_B_NK, C=h, ldc=ldc, act=code, geglu=True, tile=tile)
+        want = fn(t[:, 0::2].astype(F32)) * t[:, 1::2]
+        got = full.get()
+        assert ref.max_rel(got[:, :F], ref.round_bf16(want)) <= 2e-2, (tile, mnk, act)
+        assert np.all(got[:, F:] == 7.0), (tile, mnk, act)
+
+
 def test_gemm_skinny_rejects_tall(xp):
     a = xp.zeros((17, 64), "bf16")
     w = xp.zeros((32, 64), "bf16")

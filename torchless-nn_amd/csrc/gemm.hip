@@ -27,7 +27,7 @@ namespace tl {
 // EPI_GENERIC keeps mfma_epilogue (QKV scatter, GeGLU, fp32 output, divisor, unaligned
 // residual rows or output rows).
 enum EpiKind { EPI_GENERIC = 0, EPI_PLAIN, EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_SILU, EPI_BIAS_RES, EPI_RES,
-               EPI_QKV, EPI_QKV_BIAS };
+               EPI_QKV, EPI_QKV_BIAS, EPI_GEGLU_GELU, EPI_GEGLU_SILU };
 
 struct GemmParams {
   const void* A;
@@ -534,6 +534,42 @@ __device__ __forceinline__ bool staged_qkv_epilogue(const GemmParams& e, int64_t
   return true;
 }
 
+// Gated (GeGLU) epilogue through LDS: columns come in (gate f, up f) pairs, so a lane's 4
+// results give 2 outputs act(gate) * up; the wave's WN / 2 output columns are staged as
+// packed pairs and written as 16-byte row pieces (bf16, no bias, N / 2 % 8 == 0).
+template <int KIND, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void staged_geglu_epilogue(const GemmParams& e, int64_t zo, int64_t zi,
+                                                      int64_t mw, int64_t nw,
+                                                      f32x4 (&acc)[TM][TN], bf16_t* region) {
+  constexpr int U = WN / 16;  // 16-byte output pieces per row (8 outputs each)
+  static_assert(WN % 16 == 0 && (WM * U) % 64 == 0, "staged gated shape");
+  const int lane = threadIdx.x & 63, fr = lane & 15, fc = lane >> 4;
+  uint8_t* reg = reinterpret_cast<uint8_t*>(region);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int r = 16 * i + fr;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const f32x4 v = acc[i][j];
+      const float h0 = (KIND == EPI_GEGLU_GELU ? gelu_tanh(v[0]) : silu_tanh(v[0])) * v[1];
+      const float h1 = (KIND == EPI_GEGLU_GELU ? gelu_tanh(v[2]) : silu_tanh(v[2])) * v[3];
+      // output columns 8 j + 2 fc, +1 of this wave: piece j, bytes 4 fc
+      *reinterpret_cast<uint32_t*>(reg + (r * U + (j + r) % U) * 16 + 4 * fc) =
+          (uint32_t)f2bf(h0) | ((uint32_t)f2bf(h1) << 16);
+    }
+  }
+  bf16_t* cz = (bf16_t*)e.C + zo * e.sc_o + zi * e.sc_i;
+  const int64_t nout = e.N / 2, ow = nw / 2;
+#pragma unroll
+  for (int p = 0; p < WM * U / 64; ++p) {
+    const int q = p * 64 + lane, r = q / U, u = q - r * U;
+    const uint4 val = *reinterpret_cast<const uint4*>(reg + (r * U + (u + r) % U) * 16);
+    const int64_t m = mw + r, n = ow + 8 * u;
+    if (m >= e.M || n >= nout) continue;
+    gstore16(cz + m * e.ldc + n, val);
+  }
+}
+
 // Block id -> output tile: workgroups are dispatched round-robin over the 8 XCDs, so XCD x
 // runs blocks x, x+8, ...; give it the contiguous run [x q + min(x, r), ...) of the
 // grouped order.
@@ -823,6 +859,8 @@ void gemm_dma_kernel(GemmParams p) {
         case EPI_BIAS_RES: staged_epilogue<EPI_BIAS_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_RES: staged_epilogue<EPI_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_QKV_BIAS: done = staged_qkv_epilogue<true, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
+        case EPI_GEGLU_GELU: staged_geglu_epilogue<EPI_GEGLU_GELU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
+        case EPI_GEGLU_SILU: staged_geglu_epilogue<EPI_GEGLU_SILU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         default: done = staged_qkv_epilogue<false, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
       }
     }
@@ -1257,6 +1295,9 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       d->head_dim % 8 == 0 && d->seq_len % 8 == 0 && p.L % 8 == 0 && p.pos0 % 8 == 0 &&
       ((uintptr_t)d->q % 16) == 0 && ((uintptr_t)d->k % 16) == 0 && ((uintptr_t)d->vt % 16) == 0)
     p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;
+  if (geglu && eo == 2 && !d->bias && d->divisor == 1.0f && (d->N / 2) % 8 == 0 && d->ldc % 8 == 0 &&
+      ((uintptr_t)d->C % 16) == 0 && d->sc_o % 8 == 0 && d->sc_i % 8 == 0)
+    p.epi = d->act == TL_ACT_GELU ? EPI_GEGLU_GELU : EPI_GEGLU_SILU;
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
