@@ -274,9 +274,9 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
 // kv head (Hq / Hkv heads x Tq positions, at most 16) form one MFMA column block, so every
 // key and value is read once per kv head rather than once per query head; the key range is
 // split over many workgroups so the cache streams from HBM in parallel (flash-decoding,
-// Dao et al. 2023). Each wave takes 64 keys and keeps its scores, probabilities and P.V in
+// Dao et al. 2023). Each wave takes 16 J keys and keeps its scores, probabilities and P.V in
 // registers with the same layouts as attention_fwd_kernel (K fragments and V^T fragments are
-// read straight from global memory: each is used by one MFMA of one wave). The 4 waves of a
+// read straight from global memory: each is used by one MFMA of one wave). The NW waves of a
 // workgroup merge their (max, sum, O) in LDS and write one partial per workgroup;
 // attention_combine_kernel rescales the partials by their maxima and writes O / l.
 // ---------------------------------------------------------------------------------------
@@ -314,19 +314,45 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
   const bf16_t* vh = p.vt + (int64_t)bh * D * p.Lk;
   const int kc0 = (blockIdx.x * NW + wave) * KPW;
 
+  // All of this wave's K and V^T fragments are requested up front (the V^T reads do not
+  // depend on the softmax), so the wave waits for one memory round trip, not two.
+  bf16x8 kf[J][KS];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int key = kc0 + 16 * j + col;
+    const bool kin = key < p.Tk;
+    const bf16_t* krow = kh + (int64_t)(kin ? key : 0) * D + 8 * grp;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[j][ks] = kin ? *reinterpret_cast<const bf16x8*>(krow + 32 * ks) : zero;
+  }
+  // V^T rows in the key order of the P.V B operand: keys 32 hp + 4 grp + 0..3 and
+  // 32 hp + 16 + 4 grp + 0..3 (values past Tk zeroed, since 0 * NaN would not be 0)
+  uint2 vfa[J / 2][DT], vfb[J / 2][DT];
+#pragma unroll
+  for (int hp = 0; hp < J / 2; ++hp) {
+    const int ka = kc0 + 32 * hp + 4 * grp, kb = ka + 16;
+    const bool ina = ka < p.Tk, inb = kb < p.Tk;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
+      uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
+      uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
+      if (ina && ka + 4 > p.Tk) va = keep_first4(va, p.Tk - ka);
+      if (inb && kb + 4 > p.Tk) vb = keep_first4(vb, p.Tk - kb);
+      vfa[hp][dt] = va;
+      vfb[hp][dt] = vb;
+    }
+  }
+
   // S^T = K Q^T for J tiles of 16 keys: lane holds keys kc0 + 16 j + 4 grp + i of row col
   f32x4 s[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int key = kc0 + 16 * j + col;
-    const bool kin = key < p.Tk;
-    const bf16_t* krow = kh + (int64_t)(kin ? key : 0) * D + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 kf = kin ? *reinterpret_cast<const bf16x8*>(krow + 32 * ks) : zero;
-      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j][ks], qf[ks], s[j], 0, 0, 0);
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -366,15 +392,9 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
       pf[i] = (__bf16)s[2 * hp][i];
       pf[4 + i] = (__bf16)s[2 * hp + 1][i];
     }
-    const int ka = kc0 + 32 * hp + 4 * grp, kb = ka + 16;
-    const bool ina = ka < p.Tk, inb = kb < p.Tk;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
-      uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
-      uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
-      if (ina && ka + 4 > p.Tk) va = keep_first4(va, p.Tk - ka);
-      if (inb && kb + 4 > p.Tk) vb = keep_first4(vb, p.Tk - kb);
+      const uint2 va = vfa[hp][dt], vb = vfb[hp][dt];
       const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
     }
@@ -532,10 +552,12 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
   const double bytes = 2.0 * (bh * seq_q * head_dim * 2 + (double)batch * n_heads_kv * seq_k * head_dim * 2);
   LaunchScope ls(ctx, TL_KF_ATTENTION, flops, bytes);
   const int64_t rows_per_kv = (n_heads_q / n_heads_kv) * seq_q;
-  if (rows_per_kv <= 16) {  // decode: split the keys over workgroups of 4 x 64 keys
+  if (rows_per_kv <= 16) {  // decode: split the keys over many small workgroups
     DecodeWs w;
-    // (waves per workgroup, 16-key tiles per wave)
-    static const int kDecodeCfg[][2] = {{4, 2}, {4, 4}, {1, 4}, {2, 2}, {1, 2}, {4, 2}, {2, 4}};
+    // (waves per workgroup, 16-key tiles per wave); the default, 2 waves x 32 keys, was
+    // fastest on an MI355X at the config-5 decode shape (B = 4, 2176 keys, D = 256):
+    // 12.0 us per layer with the combine vs 13.5 us for 4 waves x 32 keys
+    static const int kDecodeCfg[][2] = {{2, 2}, {4, 4}, {1, 4}, {2, 2}, {1, 2}, {4, 2}, {2, 4}};
     const int cfg = ctx->attn_decode_cfg >= 1 && ctx->attn_decode_cfg <= 6 ? ctx->attn_decode_cfg : 0;
     const int nw = kDecodeCfg[cfg][0], jt = kDecodeCfg[cfg][1];
     w.nblk = (int)((seq_k + 16 * nw * jt - 1) / (16 * nw * jt));
