@@ -1148,11 +1148,12 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
     // the activations from the previous kernel, and the deeper pipeline beats two 2-stage
     // 128-row workgroups per CU (GPT-2 prefill 4.06 -> 3.88 ms with 256x128 alone) though
     // it is slower on operands hot in cache. Width 96 or 128, whichever wastes less area in
-    // the last round (GPT-2: 96 fills whole rounds at N = 768, 2304 and 3072).
+    // the last round, 128 on a tie (GPT-2: 96 at N = 768 and 2304; at N = 3072 both fill
+    // whole rounds and 128's fewer, larger tiles measured 3.79 vs 3.88 ms per forward).
     const int64_t t96w = tiles(256, 96), t128w = tiles(256, 128);
     if (K >= 256 && t96w >= cus) {
       const int64_t w96 = (t96w + cus - 1) / cus * 96, w128 = (t128w + cus - 1) / cus * 128;
-      return w96 <= w128 ? TL_TILE_DMA_256x96_W8 : TL_TILE_DMA_256x128_W8;
+      return w96 < w128 ? TL_TILE_DMA_256x96_W8 : TL_TILE_DMA_256x128_W8;
     }
     // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
     // workgroups wastes the least area (N = 768 or 2304: 128x96; 3072: 128x128)
