@@ -78,7 +78,10 @@ enum tl_gemm_tile {
   TL_TILE_DMA_256x128_W8 = 9,  /* 8 waves, 3 stages */
   TL_TILE_DMA_128x64_S3 = 10,  /* 3 stages */
   TL_TILE_DMA_128x128_S3 = 11, /* 3 stages */
-  /* persistent direct-to-LDS variants (one workgroup per resident slot; batch 1) */
+  /* persistent direct-to-LDS variants: one workgroup per resident slot, the next tile's first
+   * K steps loaded while the current tile stores its epilogue. bf16 output with plain, bias,
+   * bias+activation or residual epilogue, batch 1, N % 8 == 0; other calls run the
+   * non-persistent tile of the same shape */
   TL_TILE_PERSIST_256x128_W8 = 12,
   TL_TILE_PERSIST_128x128 = 13,
   /* weight streaming for M <= 16 (decode steps): 16 rows of B per workgroup, K split over
@@ -86,7 +89,9 @@ enum tl_gemm_tile {
   TL_TILE_SKINNY = 14,
   TL_TILE_DMA_256x256_W8 = 15, /* direct global->LDS, 8 waves of 128x64, 2 stages */
   TL_TILE_DMA_128x96 = 16,     /* direct global->LDS, 4 waves of 64x48, 2 stages */
-  TL_TILE_DMA_256x96_W8 = 17   /* direct global->LDS, 8 waves of 64x48, 3 stages */
+  TL_TILE_DMA_256x96_W8 = 17,  /* direct global->LDS, 8 waves of 64x48, 3 stages */
+  TL_TILE_PERSIST_256x96_W8 = 18,  /* persistent (see above), 3 stages */
+  TL_TILE_PERSIST_256x256_W8 = 19  /* persistent (see above), 2 stages */
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

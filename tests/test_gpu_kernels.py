@@ -357,7 +357,8 @@ def test_gemm_qkv_split(xp, dt, heads):
 
 
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x64s3", "dma128x128s3",
-                                  "dma256x256w8", "dma128x96", "dma256x96w8"])
+                                  "dma256x256w8", "dma128x96", "dma256x96w8", "persist256x96w8",
+                                  "persist256x128w8", "persist128x128", "persist256x256w8"])
 @pytest.mark.parametrize("mnk", [(300, 524, 192), (513, 1000, 256), (64, 60, 64), (1000, 777, 128)])
 def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
     """bf16 outputs of the direct-to-LDS tiles go through the LDS-staged epilogue: every kind
@@ -401,6 +402,47 @@ def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
     assert ref.max_rel(o.get(), ref.round_bf16(want)) <= 2e-2, (tile, "batched")
 
 
+PERSIST_PAIRS = [("persist256x96w8", "dma256x96w8"), ("persist256x128w8", "dma256x128w8"),
+                 ("persist128x128", "dma128x128"), ("persist256x256w8", "dma256x256w8")]
+
+
+@pytest.mark.parametrize("mnk", [(4100, 4104, 64), (4100, 4104, 128), (1030, 2056, 320)])
+def test_gemm_persistent_pipeline(xp, mnk):
+    """The persistent tiles: with more output tiles than resident workgroups each workgroup
+    walks several, and with 1- and 2-step K loops one or two tiles' epilogue stores are in
+    flight at a K-step wait. Every staged epilogue kind must equal the non-persistent tile of
+    the same shape bit for bit (same MFMA order, same epilogue arithmetic) and the fp64
+    product to bf16 tolerance; the pieces past N and the row past M stay untouched."""
+    M, N, K = mnk
+    rng = np.random.default_rng(M + 5 * N + K)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+    wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    res = ref.round_bf16(rng.standard_normal((M, N)).astype(F32))
+    ldc = N + 8
+    dres = xp.empty((M, N), "bf16", pitch=ldc)
+    dres.set(res)
+    da, dw, db = up(xp, a, "bf16"), up(xp, wt, "bf16"), up(xp, bias, "bf16")
+    kinds = [dict(), dict(bias=True, act="gelu"), dict(bias=True, res=True), dict(res=True)]
+    for c in kinds:
+        want = ref.round_bf16(gemm_ref(a, wt.T, bias if c.get("bias") else None, c.get("act"),
+                                       res if c.get("res") else None))
+        act = {None: xp.TL_ACT_NONE, "gelu": xp.TL_ACT_GELU}[c.get("act")]
+        for pair in PERSIST_PAIRS:
+            outs = []
+            for tile in pair:
+                full = xp.empty((M + 1, ldc), "bf16").fill(7.0)
+                out = xp.DeviceTensor((M, N), full.dtype, pitch=ldc, buf=full.buf, offset=full.offset)
+                xp.gemm(da, dw, M=M, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK, C=out, ldc=ldc,
+                        bias=db if c.get("bias") else None, act=act,
+                        residual=dres if c.get("res") else None, ldr=ldc, tile=tile)
+                outs.append(full.get())
+            got, base = outs
+            assert np.array_equal(got, base), (pair, mnk, c)
+            assert ref.max_rel(got[:M, :N], want) <= 2e-2, (pair, mnk, c)
+            assert np.all(got[:, N:] == 7.0) and np.all(got[M] == 7.0), (pair, mnk, c)
+
+
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x96", "dma256x256w8",
                                   "dma128x64s3", "dma256x96w8"])
 @pytest.mark.parametrize("cfg", [(2, 64, 12, 12, 64, 192, 0), (3, 40, 8, 1, 32, 128, 16),
@@ -439,7 +481,8 @@ def test_gemm_qkv_staged_scatter(xp, tile, cfg):
 @pytest.mark.parametrize("tile", ["256x256", "256x128", "128x128", "128x64", "64x64", "256x256w4",
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
                                   "dma128x128s3", "persist256x128w8", "persist128x128",
-                                  "dma256x256w8", "dma128x96", "dma256x96w8"])
+                                  "dma256x256w8", "dma128x96", "dma256x96w8", "persist256x96w8",
+                                  "persist256x256w8"])
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (64, 64, 64), (513, 129, 776), (700, 300, 640)])
 def test_gemm_every_tile_shape(xp, tile, mnk):
     """Forces each MFMA tile shape on ragged M/N and a K tail, with a full epilogue."""

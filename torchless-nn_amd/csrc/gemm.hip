@@ -361,32 +361,46 @@ __device__ __forceinline__ void grouped_tile(int i, const GemmParams& p, int& tm
 // the store issue time per tile drops about 4x). Piece u of row r sits at slot (u + r) % U,
 // which spreads the fragment writes over the LDS banks. Only this wave touches its region
 // and the LDS operations of one wave complete in order, so the reads need no barrier.
-template <int KIND, int TM, int TN, int WM, int WN>
-__device__ __forceinline__ void staged_epilogue(const GemmParams& e, int64_t zo, int64_t zi,
-                                                int64_t mw, int64_t nw, f32x4 (&acc)[TM][TN],
-                                                bf16_t* region) {
-  constexpr bool BIAS = KIND == EPI_BIAS || KIND == EPI_BIAS_GELU || KIND == EPI_BIAS_SILU ||
-                        KIND == EPI_BIAS_RES;
-  constexpr bool RES = KIND == EPI_BIAS_RES || KIND == EPI_RES;
-  constexpr int U = WN / 8;
-  static_assert(WN % 16 == 0 && (WM * U) % 64 == 0, "staged epilogue shape");
-  const int lane = threadIdx.x & 63, fr = lane & 15, fc = lane >> 4;
-  uint8_t* reg = reinterpret_cast<uint8_t*>(region);
-  float bias[BIAS ? TN : 1][4];
-  if (BIAS) {
+template <int KIND>
+struct EpiTraits {
+  static constexpr bool BIAS = KIND == EPI_BIAS || KIND == EPI_BIAS_GELU || KIND == EPI_BIAS_SILU ||
+                               KIND == EPI_BIAS_RES;
+  static constexpr bool RES = KIND == EPI_BIAS_RES || KIND == EPI_RES;
+};
+
+// The bias values of a lane's fragment columns nw + 16 j + 4 (lane / 16) + q (0 past N).
+template <int KIND, int TN>
+__device__ __forceinline__ void load_epi_bias(const GemmParams& e, int64_t nw,
+                                              float (&bias)[EpiTraits<KIND>::BIAS ? TN : 1][4]) {
+  if constexpr (EpiTraits<KIND>::BIAS) {
+    const int fc = (threadIdx.x & 63) >> 4;
 #pragma unroll
-    for (int j = 0; j < (BIAS ? TN : 1); ++j) {
+    for (int j = 0; j < TN; ++j) {
       const int64_t n = nw + 16 * j + 4 * fc;
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         bias[j][q] = n + q < e.N ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
     }
   }
-  const bf16_t* rz = RES ? (const bf16_t*)e.res + zo * e.sr_o + zi * e.sr_i : nullptr;
+}
+
+// Applies epilogue KIND to the fragment rows i = I0 .. I0 + NI - 1 of a wave's accumulators
+// (block rows 16 I0 .. 16 (I0 + NI) - 1, starting at global row mw + 16 I0) and writes them,
+// rounded once to bf16, to the region as 16-byte row pieces: piece u of staged row r at slot
+// (r * U + (u + r) % U), U = WN / 8 (the rotation spreads the fragment writes over the LDS
+// banks).
+template <int KIND, int TM, int TN, int WN, int I0, int NI>
+__device__ __forceinline__ void stage_rows(const GemmParams& e, const bf16_t* rz, int64_t mw,
+                                           int64_t nw, f32x4 (&acc)[TM][TN],
+                                           const float (&bias)[EpiTraits<KIND>::BIAS ? TN : 1][4],
+                                           uint8_t* reg) {
+  constexpr bool BIAS = EpiTraits<KIND>::BIAS, RES = EpiTraits<KIND>::RES;
+  constexpr int U = WN / 8;
+  const int lane = threadIdx.x & 63, fr = lane & 15, fc = lane >> 4;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int r = 16 * i + fr;
-    const int64_t m = mw + r;
+  for (int ii = 0; ii < NI; ++ii) {
+    const int i = I0 + ii, r = 16 * ii + fr;
+    const int64_t m = mw + 16 * i + fr;
     // rows past M are computed and staged but never stored; their residual reads stay on
     // the last row
     const bf16_t* rrow = RES ? rz + (m < e.M ? m : e.M - 1) * e.ldr + nw + 4 * fc : nullptr;
@@ -419,6 +433,27 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& e, int64_t zo,
       *reinterpret_cast<uint2*>(reg + (r * U + (u + r) % U) * 16 + (fc & 1) * 8) = w;
     }
   }
+}
+
+// bf16 epilogue through LDS. Each wave applies its epilogue kind to its WM x WN results in
+// fp32 (bias, then activation, then residual, as mfma_epilogue does), stages them in its own
+// LDS region (stage_rows) and reads them back as 16-byte row pieces, so each global store
+// instruction writes whole row segments of 64 / U rows instead of 32-byte pieces of 16 rows
+// (4x fewer cache lines touched per byte: the store issue time per tile drops about 4x).
+// Only this wave touches its region and the LDS operations of one wave complete in order,
+// so the reads need no barrier.
+template <int KIND, int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void staged_epilogue(const GemmParams& e, int64_t zo, int64_t zi,
+                                                int64_t mw, int64_t nw, f32x4 (&acc)[TM][TN],
+                                                bf16_t* region) {
+  constexpr int U = WN / 8;
+  static_assert(WN % 16 == 0 && (WM * U) % 64 == 0, "staged epilogue shape");
+  const int lane = threadIdx.x & 63;
+  uint8_t* reg = reinterpret_cast<uint8_t*>(region);
+  float bias[EpiTraits<KIND>::BIAS ? TN : 1][4];
+  load_epi_bias<KIND, TN>(e, nw, bias);
+  const bf16_t* rz = EpiTraits<KIND>::RES ? (const bf16_t*)e.res + zo * e.sr_o + zi * e.sr_i : nullptr;
+  stage_rows<KIND, TM, TN, WN, 0, TM>(e, rz, mw, nw, acc, bias, reg);
   bf16_t* cz = (bf16_t*)e.C + zo * e.sc_o + zi * e.sc_i;
 #pragma unroll
   for (int p = 0; p < WM * U / 64; ++p) {
@@ -869,21 +904,51 @@ void gemm_dma_kernel(GemmParams p) {
   if (!done) mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
 }
 
-// gemm_dma_persistent_kernel: gemm_dma_kernel with one workgroup per resident slot
-// (gridDim.x = CUs x workgroups per CU, a multiple of 8). Workgroup b runs on XCD b % 8 and
-// walks that XCD's contiguous run of the grouped tile order with stride gridDim.x / 8.
-// Its K steps form one flattened pipeline across its tiles: the first steps of the next
-// tile are loaded while the current tile finishes and stores its epilogue, so a short K
-// loop (12 steps at K = 768) no longer pays the load latency once per tile. Batch == 1.
-template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
+// Stores of a persistent tile's staged rows through a buffer resource: a piece outside the
+// M x N output gets offset 0x80000000, past the resource's num_records, and the hardware
+// drops it. Every lane of every wave therefore issues the same number of store instructions
+// per tile, which the K pipeline's wait counts rely on.
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_c_rsrc(const GemmParams& e) {
+  // raw buffer (stride 0); 0x00020000: the gfx9 data-format word for untyped dword access
+  const uint32_t extent = (uint32_t)(((e.M - 1) * e.ldc + e.N) * 2);
+  return __builtin_amdgcn_make_buffer_rsrc(e.C, (short)0, (int)extent, 0x00020000);
+}
+
+// gemm_dma_persistent_kernel: one workgroup per resident slot (gridDim.x = CUs x workgroups
+// per CU, a multiple of 8), bf16 output with a staged epilogue kind (PLAIN .. RES), batch 1,
+// N % 8 == 0 and an output extent below 2 GiB (host-checked). Workgroup b runs on XCD b % 8
+// and walks that XCD's contiguous run of the grouped tile order with stride gridDim.x / 8,
+// so the XCD's workgroups share A and B panels in its L2.
+//
+// Its K steps form one flattened pipeline across its tiles: the loads of the next tile's
+// first STAGES - 1 steps are in flight while the current tile finishes, stages its epilogue
+// in the LDS stage it has just consumed (in NH row groups when the tile is larger than one
+// stage) and stores it. A short K loop (12 steps at K = 768) then pays the first-load latency
+// once per workgroup, not once per tile.
+//
+// Wait counts: vmcnt counts the direct-to-LDS loads and the epilogue stores of a wave in
+// issue order. Step t needs its own loads; issued after them are the next STAGES - 2 steps'
+// loads (LMAX or LMAX - 1 per step for this wave) and the SPT stores of every tile that ended
+// in steps t - STAGES + 1 .. t - 1. Bias and residual loads inside an epilogue are waited for
+// before its stores, so they only make a wait stricter.
+template <int KIND, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void gemm_dma_persistent_kernel(GemmParams p) {
   constexpr int NW = WGM * WGN, BK = 64;
   constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 16, TN = WN / 16;
-  constexpr int GA = BM / 8, GB = BN / 8, L = (GA + GB) / NW;
-  static_assert((GA + GB) % NW == 0 && TM >= 1 && TN >= 1, "bad tile/wave split");
-  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 stages");
+  constexpr int GA = BM / 8, GB = BN / 8, GT = GA + GB;
+  constexpr int LMAX = (GT + NW - 1) / NW, R = GT - (LMAX - 1) * NW;
   constexpr int SZ = (BM + BN) * BK;
+  // row groups of the staged epilogue: NW regions of WM / NH rows x WN must fit one stage
+  constexpr int NH = (BM * BN <= SZ) ? 1 : 2;
+  constexpr int NI = TM / NH, U = WN / 8;
+  constexpr int SPG = 16 * NI * U / 64;  // store instructions per wave per row group
+  constexpr int SPT = NH * SPG;           // ... per tile
+  static_assert(TM >= 1 && TN >= 1 && TM % NH == 0, "bad tile/wave split");
+  static_assert(BM * BN <= NH * SZ && (16 * NI * U) % 64 == 0 && WN % 16 == 0, "epilogue staging");
+  static_assert(STAGES == 2 || STAGES == 3, "2 or 3 stages");
+  static_assert(LMAX * (STAGES - 2) + 2 * SPT <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(16))) bf16_t S0[SZ];
   __shared__ __attribute__((aligned(16))) bf16_t S1[SZ];
   __shared__ __attribute__((aligned(16))) bf16_t S2[STAGES > 2 ? SZ : 8];
@@ -892,10 +957,12 @@ void gemm_dma_persistent_kernel(GemmParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WGN, wn = wave - wm * WGN;
+  const bool full = wave < R;  // this wave issues LMAX groups per K step
+  const int g0 = full ? wave * LMAX : R * LMAX + (wave - R) * (LMAX - 1);
   const int ntiles = p.tiles_m * p.tiles_n;
   const int bid = blockIdx.x, x = bid & 7, lb = bid >> 3, per_x = (int)gridDim.x >> 3;
-  const int q = ntiles >> 3, r = ntiles & 7;
-  const int cs = x * q + min(x, r), cn = q + (x < r ? 1 : 0);
+  const int q8 = ntiles >> 3, r8 = ntiles & 7;
+  const int cs = x * q8 + min(x, r8), cn = q8 + (x < r8 ? 1 : 0);
   const int my_tiles = lb < cn ? (cn - lb + per_x - 1) / per_x : 0;
   const int nk = (int)(p.K / BK);
   const int total = my_tiles * nk;
@@ -905,23 +972,41 @@ void gemm_dma_persistent_kernel(GemmParams p) {
     m0 = (int64_t)tm * BM;
     n0 = (int64_t)tn * BN;
   };
+
+  // issue side: the tile and K step of the next load, its panel bases and row offsets
+  int i_rr = 0, i_kk = 0;
+  const bf16_t* iA = nullptr;
+  const bf16_t* iB = nullptr;
+  uint32_t off[LMAX];
   const int rin = lane >> 3, cch = (lane & 7) ^ rin;
-  auto issue_step = [&](bf16_t* S, int h) {
-    const int rr = h / nk, kk = h - rr * nk;
-    int64_t m0, n0;
-    tile_origin(rr, m0, n0);
-    const bf16_t* Ab = (const bf16_t*)p.A + m0 * p.lda + (int64_t)kk * BK;
-    const bf16_t* Bb = (const bf16_t*)p.B + n0 * p.ldb + (int64_t)kk * BK;
-    const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
-    const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
+  auto issue = [&](bf16_t* S) {
+    if (i_kk == 0) {
+      int64_t m0, n0;
+      tile_origin(i_rr, m0, n0);
+      iA = (const bf16_t*)p.A + m0 * p.lda;
+      iB = (const bf16_t*)p.B + n0 * p.ldb;
+      const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
+      const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int g = wave * L + j;
-      const bf16_t* src = g < GA ? Ab + min(8 * g + rin, a_last) * p.lda + cch * 8
-                                 : Bb + min(8 * (g - GA) + rin, b_last) * p.ldb + cch * 8;
-      dma_load16(src, lds_offset(S + g * 512));
+      for (int j = 0; j < LMAX; ++j) {
+        const int g = min(g0 + j, GT - 1);
+        off[j] = g < GA ? (uint32_t)(min(8 * g + rin, a_last) * p.lda + cch * 8)
+                        : (uint32_t)(min(8 * (g - GA) + rin, b_last) * p.ldb + cch * 8);
+      }
+    }
+    const int64_t k0 = (int64_t)i_kk * BK;
+#pragma unroll
+    for (int j = 0; j < LMAX; ++j) {
+      if (j == LMAX - 1 && !full) break;
+      const int g = g0 + j;
+      dma_load16((g < GA ? iA : iB) + k0 + off[j], lds_offset(S + g * 512));
+    }
+    if (++i_kk == nk) {
+      i_kk = 0;
+      ++i_rr;
     }
   };
+
   f32x4 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -929,57 +1014,97 @@ void gemm_dma_persistent_kernel(GemmParams p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, fc = lane >> 4;
   const int a_frag = (wm * WM + fr) * BK, b_frag = BM * BK + (wn * WN + fr) * BK;
-  // Both 32-wide K halves' fragments are read before the first MFMA when the wave tile is
-  // small enough (their LDS latency then overlaps the first half's MFMAs); larger wave
-  // tiles read and consume one half at a time to bound register use.
   auto compute = [&](const bf16_t* S) {
-    constexpr bool kBoth = TM * TN <= 16;
     bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 3;
-      if (s == 0 || !kBoth) {
+    for (int h = 0; h < 2; ++h) {
+      const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
 #pragma unroll
-        for (int h = s; h < (kBoth ? 2 : s + 1); ++h) {
-          const int swh = ((h * 4 + fc) ^ (fr & 7)) << 3;
+      for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
 #pragma unroll
-          for (int i = 0; i < TM; ++i) af[h][i] = *reinterpret_cast<const bf16x8*>(&S[a_frag + i * 16 * BK + swh]);
+      for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
+    }
 #pragma unroll
-          for (int j = 0; j < TN; ++j) bfr[h][j] = *reinterpret_cast<const bf16x8*>(&S[b_frag + j * 16 * BK + swh]);
-        }
-      }
-      (void)sw;
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s][j], af[s][i], acc[i][j], 0, 0, 0);
-      if (!kBoth) __builtin_amdgcn_sched_barrier(0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[h][j], af[h][i], acc[i][j], 0, 0, 0);
+    schedule_kstep<TM + TN, TM * TN>();
   };
-  auto finish_tile = [&](int rr) {
+
+  // the staged epilogue of tile rr into stage S (every wave has finished reading S)
+  auto finish_tile = [&](int rr, bf16_t* S) {
     int64_t m0, n0;
     tile_origin(rr, m0, n0);
     const GemmParams e = late_params();
-    mfma_epilogue<TO, TM, TN>(e, 0, 0, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
+    const int64_t mw = m0 + wm * WM, nw = n0 + wn * WN;
+    const BufRsrc rs = make_c_rsrc(e);
+    float bias[EpiTraits<KIND>::BIAS ? TN : 1][4];
+    load_epi_bias<KIND, TN>(e, nw, bias);
+    const bf16_t* rz = EpiTraits<KIND>::RES ? (const bf16_t*)e.res : nullptr;
+    uint8_t* reg = reinterpret_cast<uint8_t*>(S + wave * (16 * NI * WN));
+    auto write_group = [&](int i0) {
+#pragma unroll
+      for (int pc = 0; pc < SPG; ++pc) {
+        const int qq = pc * 64 + lane, r = qq / U, u = qq - r * U;
+        const uint4 v = *reinterpret_cast<const uint4*>(reg + (r * U + (u + r) % U) * 16);
+        const int64_t m = mw + 16 * i0 + r, n = nw + 8 * u;
+        const uint32_t o = (m < e.M && n < e.N) ? (uint32_t)((m * e.ldc + n) * 2) : 0x80000000u;
+        const u32x4_t t = {v.x, v.y, v.z, v.w};
+        __builtin_amdgcn_raw_buffer_store_b128(t, rs, (int)o, 0, 0);
+      }
+    };
+    stage_rows<KIND, TM, TN, WN, 0, NI>(e, rz, mw, nw, acc, bias, reg);
+    write_group(0);
+    if constexpr (NH == 2) {
+      stage_rows<KIND, TM, TN, WN, NI, NI>(e, rz, mw, nw, acc, bias, reg);
+      write_group(NI);
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
+
 #pragma unroll
   for (int i = 0; i < STAGES - 1; ++i)
-    if (i < total) issue_step(stage(i), i);
-  for (int g0 = 0; g0 < total; g0 += STAGES) {
+    if (i < total) issue(stage(i));
+  int c_rr = 0, c_kk = 0;  // compute side: tile and K step
+  bool e1 = false, e2 = false;  // a tile ended at step t - 1 / t - 2
+  for (int t0 = 0; t0 < total; t0 += STAGES) {
 #pragma unroll
     for (int u = 0; u < STAGES; ++u) {
-      const int g = g0 + u;
-      if (g >= total) break;
-      if (STAGES == 3 && g + 1 < total) dma_stage_sync<L * (STAGES - 2)>();
-      else dma_stage_sync<0>();
-      if (g + STAGES - 1 < total) issue_step(stage((u + STAGES - 1) % STAGES), g + STAGES - 1);
+      const int t = t0 + u;
+      if (t >= total) break;
+      const int ends = (int)e1 + (int)(STAGES == 3 && e2);
+      if (STAGES == 3 && t + 1 < total) {
+        if (full) {
+          if (ends == 0) dma_stage_sync<LMAX>();
+          else if (ends == 1) dma_stage_sync<LMAX + SPT>();
+          else dma_stage_sync<LMAX + 2 * SPT>();
+        } else {
+          if (ends == 0) dma_stage_sync<LMAX - 1>();
+          else if (ends == 1) dma_stage_sync<LMAX - 1 + SPT>();
+          else dma_stage_sync<LMAX - 1 + 2 * SPT>();
+        }
+      } else {
+        if (ends == 0) dma_stage_sync<0>();
+        else if (ends == 1) dma_stage_sync<SPT>();
+        else dma_stage_sync<2 * SPT>();
+      }
+      if (t + STAGES - 1 < total) issue(stage((u + STAGES - 1) % STAGES));
       compute(stage(u));
-      if ((g + 1) % nk == 0) finish_tile(g / nk);
+      e2 = e1;
+      e1 = ++c_kk == nk;
+      if (e1) {
+        // every wave has read stage u (a plain barrier: no wait on the loads in flight)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        finish_tile(c_rr, stage(u));
+        c_kk = 0;
+        ++c_rr;
+      }
     }
   }
 }
@@ -1127,9 +1252,24 @@ static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 2
                                    {256, 256, 256}, {256, 128, 512}, {128, 128, 256},
                                    {256, 128, 512}, {128, 64, 256},  {128, 128, 256},
                                    {256, 128, 512}, {128, 128, 256}, {16, 16, 256},
-                                   {256, 256, 512}, {128, 96, 256},  {256, 96, 512}};
-// resident workgroups per CU of the persistent variants (LDS: 144 KB and 64 KB)
-static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_256x128_W8 ? 1 : 2; }
+                                   {256, 256, 512}, {128, 96, 256},  {256, 96, 512},
+                                   {256, 96, 512},  {256, 256, 512}};
+static bool is_persistent(int tile) {
+  return tile == TL_TILE_PERSIST_256x128_W8 || tile == TL_TILE_PERSIST_128x128 ||
+         tile == TL_TILE_PERSIST_256x96_W8 || tile == TL_TILE_PERSIST_256x256_W8;
+}
+// the non-persistent tile of the same shape
+static int persistent_fallback(int tile) {
+  switch (tile) {
+    case TL_TILE_PERSIST_256x128_W8: return TL_TILE_DMA_256x128_W8;
+    case TL_TILE_PERSIST_128x128: return TL_TILE_DMA_128x128;
+    case TL_TILE_PERSIST_256x96_W8: return TL_TILE_DMA_256x96_W8;
+    default: return TL_TILE_DMA_256x256_W8;
+  }
+}
+// resident workgroups per CU of the persistent variants (LDS: 64 KB for 128x128, 128 KB or
+// more for the others)
+static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_128x128 ? 2 : 1; }
 
 // Tile choice, from MI355X sweeps of the GPT-2-small (M = 8192) and ViT-S/4 (M = 33280)
 // GEMMs and an 8192^3 square: the direct-to-LDS kernels (K % 64 == 0) run best with 256x256
@@ -1201,12 +1341,30 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
     case TL_TILE_DMA_256x128_W8: gemm_dma_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_DMA_128x64_S3: gemm_dma_kernel<TO, 128, 64, 2, 2, 2, 3><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_128x128_S3: gemm_dma_kernel<TO, 128, 128, 2, 2, 1, 3><<<grid, 256, 0, st>>>(p); break;
-    case TL_TILE_PERSIST_256x128_W8: gemm_dma_persistent_kernel<TO, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
-    case TL_TILE_PERSIST_128x128: gemm_dma_persistent_kernel<TO, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_256x256_W8: gemm_dma_kernel<TO, 256, 256, 2, 4, 2, 2><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_DMA_128x96: gemm_dma_kernel<TO, 128, 96, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_256x96_W8: gemm_dma_kernel<TO, 256, 96, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
     default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
+  }
+}
+
+template <int KIND>
+static void launch_persistent_kind(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
+  switch (tile) {
+    case TL_TILE_PERSIST_256x128_W8: gemm_dma_persistent_kernel<KIND, 256, 128, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_PERSIST_128x128: gemm_dma_persistent_kernel<KIND, 128, 128, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
+    case TL_TILE_PERSIST_256x96_W8: gemm_dma_persistent_kernel<KIND, 256, 96, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
+    default: gemm_dma_persistent_kernel<KIND, 256, 256, 2, 4, 2, 2><<<grid, 512, 0, st>>>(p); break;
+  }
+}
+static void launch_persistent(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
+  switch (p.epi) {
+    case EPI_PLAIN: launch_persistent_kind<EPI_PLAIN>(tile, grid, st, p); break;
+    case EPI_BIAS: launch_persistent_kind<EPI_BIAS>(tile, grid, st, p); break;
+    case EPI_BIAS_GELU: launch_persistent_kind<EPI_BIAS_GELU>(tile, grid, st, p); break;
+    case EPI_BIAS_SILU: launch_persistent_kind<EPI_BIAS_SILU>(tile, grid, st, p); break;
+    case EPI_BIAS_RES: launch_persistent_kind<EPI_BIAS_RES>(tile, grid, st, p); break;
+    default: launch_persistent_kind<EPI_RES>(tile, grid, st, p); break;
   }
 }
 
@@ -1226,7 +1384,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_256x96_W8, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_PERSIST_256x256_W8, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -1345,8 +1503,23 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (mfma) {
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
-    const bool persistent = tile == TL_TILE_PERSIST_256x128_W8 || tile == TL_TILE_PERSIST_128x128;
-    if (persistent && batch != 1) tile = tile == TL_TILE_PERSIST_128x128 ? TL_TILE_DMA_128x128 : TL_TILE_DMA_256x128_W8;
+    // the persistent kernels store through a buffer resource: whole 16-byte pieces, byte
+    // offsets below 2^31
+    const bool persist_ok = batch == 1 && !f32out && p.epi >= EPI_PLAIN && p.epi <= EPI_RES &&
+                            d->N % 8 == 0 && ((d->M - 1) * d->ldc + d->N) * 2 < (int64_t)0x7fffffff;
+    if (is_persistent(tile) && !persist_ok) tile = persistent_fallback(tile);
+    // Automatic choice: with a K loop of at most 8 steps and two or more tiles per CU, the
+    // next tile's first loads pay off when issued under the current tile's epilogue
+    // (ViT-S/4 FFN1 +12%, out-proj +5%); at K = 768 the two variants tie and with one tile
+    // per CU the persistent bookkeeping costs 4-10%.
+    if (!d->tile && persist_ok && d->K <= 512 &&
+        (tile == TL_TILE_DMA_256x96_W8 || tile == TL_TILE_DMA_256x128_W8)) {
+      const TileShape& t = kTiles[tile];
+      const int64_t nt = ((d->M + t.bm - 1) / t.bm) * ((d->N + t.bn - 1) / t.bn);
+      if (nt >= 2LL * (ctx->num_cus > 0 ? ctx->num_cus : 256))
+        tile = tile == TL_TILE_DMA_256x96_W8 ? TL_TILE_PERSIST_256x96_W8 : TL_TILE_PERSIST_256x128_W8;
+    }
+    const bool persistent = is_persistent(tile);
     const TileShape& s = kTiles[tile];
     p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
     p.tiles_n = (int)((d->N + s.bn - 1) / s.bn);
@@ -1359,7 +1532,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       if (grid.x == 0) grid.x = 8;
     }
     LaunchScope ls(ctx, family, flops, bytes);
-    if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
+    if (persistent) launch_persistent(tile, grid, ctx->stream, p);
+    else if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
     else launch_mfma<bf16_t>(tile, grid, ctx->stream, p);
     return ls.finish("gemm_mfma");
   }
