@@ -639,6 +639,31 @@ def test_attention_fused(xp, D, causal, T):
     assert ref.max_rel(out.get(), want) <= 2e-2, (D, causal, T)
 
 
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("tk_lk", [(65, 72), (130, 136)])
+def test_attention_fused_capacity_padding(xp, D, causal, tk_lk):
+    """Prefill with a key capacity past the valid keys (ViT-S/4: 65 keys in 72): positions
+    [Tk, Lk) of k and vt are never written by the model, here NaN, and must not reach the
+    output (their scores are masked, and a zero probability times NaN would not be zero)."""
+    Tk, Lk = tk_lk
+    B, H, Tq = 2, 3, Tk
+    rng = np.random.default_rng(D + Lk)
+    q = ref.round_bf16(rng.standard_normal((B, H, Tq, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, H, Lk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, H, D, Lk)).astype(F32))
+    k[:, :, Tk:] = np.nan
+    vt[:, :, :, Tk:] = np.nan
+    out = xp.empty((B, Tq, H * D), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=H,
+                 n_heads_kv=H, divisor=divisor, causal=causal, seq_k=Tk)
+    got = out.get()
+    assert np.all(np.isfinite(got)), (D, causal, tk_lk)
+    want = attention_ref(q, k[:, :, :Tk], vt[:, :, :, :Tk], H, H, divisor, causal, 0)
+    assert ref.max_rel(got, want) <= 2e-2, (D, causal, tk_lk)
+
+
 @pytest.mark.parametrize("heads", [(8, 1), (4, 2)])
 def test_attention_fused_grouped_heads_and_offset(xp, heads):
     """Multi-/grouped-query heads and a query block that sits at the end of a longer key

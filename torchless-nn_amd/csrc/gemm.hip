@@ -731,10 +731,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 // a barrier. A load group is 8 tile rows x 8 chunks = 1 KB: lane l fills row l / 8, slot
 // l % 8, which holds logical chunk (l % 8) ^ (row % 8), the XOR swizzle the fragment
 // reads undo.
-// One global_load_lds_dwordx4 through inline asm: the compiler does not track these loads,
-// so it adds no wait of its own before reading the other stages (it cannot tell the stage
-// arrays apart and would drain every load in flight); the kernel orders them with
-// dma_stage_sync. M0 (the LDS base of the 64 lanes' 16-byte slots) is saved and restored.
 // Scheduling pattern for one K step of fragment reads and MFMAs: NR reads of the first
 // half, then the second half's NR reads each followed by a share of the first half's NM
 // MFMAs, then the second half's NM MFMAs. The fragment registers of both halves stay live,
@@ -755,24 +751,6 @@ __device__ __forceinline__ void schedule_kstep() {
   __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
 }
 
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
-}
-__device__ __forceinline__ void dma_load16(const void* src, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(src)
-      : "memory");
-}
-template <int N>
-__device__ __forceinline__ void dma_stage_sync() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
-}
 
 template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))

@@ -223,4 +223,31 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
+// Direct global -> LDS loads (gemm.hip, attention.hip). One global_load_lds_dwordx4 through
+// inline asm: each lane of the wave writes its 16 bytes at LDS base + 16 * lane, the base
+// (uniform) in M0, which is saved and restored. The compiler does not track these loads, so
+// it adds no wait of its own before reading the other LDS buffers (it cannot tell them apart
+// and would drain every load in flight); kernels order them with dma_stage_sync, which
+// waits until at most N of the wave's vector memory operations are outstanding (vmcnt counts
+// loads and stores in issue order) and its LDS operations are done, then meets the other
+// waves at a barrier.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+__device__ __forceinline__ void dma_load16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+template <int N>
+__device__ __forceinline__ void dma_stage_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 }  // namespace tl
