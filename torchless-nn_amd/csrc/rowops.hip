@@ -152,12 +152,38 @@ __global__ __launch_bounds__(256) void embed_kernel(const I* ids, const T* table
 // ------------------------------------------------------------------------------------
 // LayerNorm / RMSNorm (reference layers.py:415-428)
 // ------------------------------------------------------------------------------------
+// 16-byte loads and stores, non-temporal (streamed past the caches) when NT.
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const void* p) {
+  if constexpr (NT) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void store16(void* p, const uint4& w) {
+  if constexpr (NT) {
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    const v4u t = {w.x, w.y, w.z, w.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<v4u*>(p));
+  } else {
+    *reinterpret_cast<uint4*>(p) = w;
+  }
+}
+
 // One wavefront per row, the row held in registers as raw 16-byte chunks (CH per lane),
 // unpacked to float for each pass. Lanes whose chunk lies past the row end load the row's
 // first chunk (a line the wave fetches anyway) and mask it out, so every load is issued
 // unconditionally. LayerNorm is two-pass (mean, then squared deviations), as the reference
-// computes np.var.
-template <typename T, int CH, bool RMS>
+// computes np.var. When a lane's chunks of gamma (and beta) fit in 16 more registers
+// (CH * sizeof(T) <= 16) they are loaded with the row, so their latency overlaps the row's
+// instead of following the reductions. NT: the row is read and the output written
+// non-temporally (the host sets it for tensors far larger than the caches, where nothing
+// would be re-read from them).
+template <typename T, int CH, bool RMS, bool NT>
 __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
                                                         const T* __restrict__ g,
                                                         const T* __restrict__ b,
@@ -165,15 +191,24 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
                                                         int64_t ldx, int64_t ldy, float eps,
                                                         float goff) {
   constexpr int VW = Elem<T>::kVec;
+  constexpr bool PRE = CH * sizeof(T) <= 16;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * ldx;
-  uint4 raw[CH];
+  uint4 raw[CH], graw[PRE ? CH : 1], braw[PRE && !RMS ? CH : 1];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * 64 + lane) * VW;
-    raw[c] = *reinterpret_cast<const uint4*>(xr + (col < cols ? col : 0));
+    raw[c] = load16<NT>(xr + (col < cols ? col : 0));
+  }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int col = (c * 64 + lane) * VW;
+      graw[c] = *reinterpret_cast<const uint4*>(g + (col < cols ? col : 0));
+      if constexpr (!RMS) braw[c] = *reinterpret_cast<const uint4*>(b + (col < cols ? col : 0));
+    }
   }
   float s = 0.f;
 #pragma unroll
@@ -210,12 +245,17 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
     if (col < cols) {
       float v[VW], gv[VW], bv[VW], o[VW];
       Elem<T>::unpack(raw[c], v);
-      load_chunk(g + col, gv);
-      if (!RMS) load_chunk(b + col, bv);
+      if constexpr (PRE) {
+        Elem<T>::unpack(graw[c], gv);
+        if constexpr (!RMS) Elem<T>::unpack(braw[c], bv);
+      } else {
+        load_chunk(g + col, gv);
+        if constexpr (!RMS) load_chunk(b + col, bv);
+      }
 #pragma unroll
       for (int e = 0; e < VW; ++e)
         o[e] = RMS ? (v[e] * rstd) * (goff + gv[e]) : gv[e] * ((v[e] - mean) * rstd) + bv[e];
-      store_chunk(yr + col, o);
+      store16<NT>(yr + col, Elem<T>::pack(o));
     }
   }
 }
@@ -292,7 +332,13 @@ __device__ __forceinline__ uint4 load_raw_partial(const T* p, int n) {
   return r.u;
 }
 
-template <typename T, int CH, bool CAUSAL, bool TAIL>
+//
+// exp(z / temp) is evaluated as 2^(z k) with k = log2(e) / temp, one uniform division per
+// thread: a per-element z / temp compiles to a full-precision division sequence (about ten
+// VALU instructions per element), and a short bf16 row is bound by VALU issue, not HBM.
+// Masked elements hold -inf, so 2^((-inf - max) k) = 0 needs no per-element select.
+// NT: row loads and stores are non-temporal (set by the host for large fp32 tensors).
+template <typename T, int CH, bool CAUSAL, bool TAIL, bool NT>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__ x,
                                                            T* __restrict__ y, int64_t rows,
                                                            int cols, int64_t ldx, int64_t ldy,
@@ -307,6 +353,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
     const int64_t lim = row % period + offset + 1;
     valid = lim < cols ? (int)lim : cols;
   }
+  const float k = 1.4426950408889634f / temp;
   const T* xr = x + row * ldx;
   uint4 raw[CH];
 #pragma unroll
@@ -315,7 +362,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
     if (TAIL && col < valid && col + VW > cols)
       raw[c] = load_raw_partial(xr + col, cols - col);
     else
-      raw[c] = *reinterpret_cast<const uint4*>(xr + (col < valid ? col : 0));
+      raw[c] = load16<NT>(xr + (col < valid ? col : 0));
   }
   float v[CH][VW];
   float mx = -INFINITY;
@@ -330,13 +377,13 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
     }
   }
   mx = wave_max(mx);
+  const float mref = mx == -INFINITY ? 0.f : mx;  // a row with no visible column
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
 #pragma unroll
     for (int e = 0; e < VW; ++e) {
-      const float ex = (col + e < valid) ? softmax_exp(v[c][e] - mx, temp) : 0.f;
+      const float ex = __builtin_amdgcn_exp2f((v[c][e] - mref) * k);
       v[c][e] = ex;
       s += ex;
     }
@@ -350,7 +397,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
 #pragma unroll
     for (int e = 0; e < VW; ++e) o[e] = v[c][e] * rs;
     if (col + VW <= cols) {
-      store_chunk(yr + col, o);
+      store16<NT>(yr + col, Elem<T>::pack(o));
     } else if (TAIL && col < cols) {
       for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
     }
@@ -792,10 +839,19 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
   const bool vec = cols % VW == 0 && ldx % VW == 0 && ldy % VW == 0 && aligned16(x) &&
                    aligned16(y) && aligned16(g) && (RMS || aligned16(b));
   const int64_t chunks = (cols / VW + 63) / 64;
+  // Rows far larger than the caches (here >= 64 MiB in) are streamed non-temporally: bf16
+  // LayerNorm over [16384, 4096] 5.26 -> 5.81 TB/s with gamma/beta loaded early, fp32
+  // 5.30 -> 5.75 TB/s. Smaller tensors keep cached stores, since the next kernel reads them.
+  const bool nt = rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
   auto wave = [&](auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
-    norm_wave_kernel<T, CH, RMS><<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
-        (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff);
+    auto go = [&](auto nt_tag) {
+      norm_wave_kernel<T, CH, RMS, decltype(nt_tag)::value>
+          <<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
+              (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff);
+    };
+    if (nt) go(std::true_type());
+    else go(std::false_type());
   };
   if (vec && chunks <= 1) wave(std::integral_constant<int, 1>());
   else if (vec && chunks <= 2) wave(std::integral_constant<int, 2>());
@@ -814,15 +870,20 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
   // masked lanes of the wave kernels read the row's first whole chunk: needs cols >= VW
   const bool vec = ldx % VW == 0 && ldy % VW == 0 && aligned16(x) && aligned16(y) && cols >= VW;
   const int64_t chunks = (cols + VW - 1) / VW;
+  // Non-temporal row access for fp32 tensors far larger than the caches (causal fp32
+  // [8, 12, 1024, 1024]: 5.04 -> 5.41 TB/s in a probe; the same change slowed bf16 rows).
+  const bool nt = sizeof(T) == 4 && rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
   auto wave = [&](auto ch_tag) {
     constexpr int CH = decltype(ch_tag)::value;
-    auto go = [&](auto tail_tag) {
+    auto go = [&](auto tail_tag, auto nt_tag) {
       constexpr bool TAIL = decltype(tail_tag)::value;
-      softmax_wave_kernel<T, CH, CAUSAL, TAIL><<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
-          (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
+      softmax_wave_kernel<T, CH, CAUSAL, TAIL, decltype(nt_tag)::value>
+          <<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
+              (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
     };
-    if (cols % VW == 0) go(std::false_type());
-    else go(std::true_type());
+    if (cols % VW != 0) go(std::true_type(), std::false_type());
+    else if (nt) go(std::false_type(), std::true_type());
+    else go(std::false_type(), std::false_type());
   };
   // Long rows: (threads, keep e in registers) by TL_SOFTMAX_LONG_CFG (1: 1024, 2: 1024 kept,
   // 3: 512, 4: 512 kept, with cached loads and stores). By default (5) 512 threads for rows
