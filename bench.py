@@ -7,7 +7,8 @@ resident in HBM. Prints one JSON line (see the fields below) with:
   roofline    the dense bf16 MFMA GEMMs (QKV, out-proj, FFN1, FFN2, LM head): algorithmic
               FLOPs / summed kernel time from HIP events around each launch, vs 2.5 PFLOP/s
   row_kernels standalone LayerNorm / RMSNorm / causal softmax / RoPE
-              in GB/s of algorithmic bytes vs 8 TB/s
+              in GB/s of algorithmic bytes vs 8 TB/s, and vs a plain copy of the same
+              bytes timed the same way (the measured ceiling at that size)
   cpu_baseline the NumPy restatement (oracle/) on a bounded sample of the same workload
 """
 import argparse
@@ -49,7 +50,7 @@ def row_kernel_bench(xp, reps=20):
     out = {}
     rng = np.random.default_rng(0)
 
-    def timed(name, fn, nbytes, nbuf):
+    def run_ms(fn, nbuf):
         for i in range(2):
             fn(i % nbuf)
         xp.synchronize()
@@ -58,10 +59,27 @@ def row_kernel_bench(xp, reps=20):
         for i in range(reps):
             fn(i % nbuf)
         e1.record()
-        ms = e0.elapsed_ms(e1) / reps
-        out[name] = {"gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "us": round(ms * 1e3, 2),
-                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "bytes": int(nbytes)}
+        return e0.elapsed_ms(e1) / reps
+
+    def copy_gbs(nbytes, nbuf):
+        """A plain device copy (tl_cast fp32 -> fp32) moving the same bytes, half read and
+        half written, over as many rotating buffers and timed the same way: the measured
+        ceiling of a streaming kernel of this size (launch and ramp included)."""
+        n = int(nbytes // 8)
+        src = [xp.empty((n,), "fp32") for _ in range(nbuf)]
+        dst = [xp.empty((n,), "fp32") for _ in range(nbuf)]
+        lib, h = xp.lib(), xp.ctx().handle
+        ms = run_ms(lambda i: xp.check(lib.tl_cast(h, src[i].ptr, dst[i].ptr, n, 0, 0)), nbuf)
+        del src, dst
+        return 8.0 * n / (ms * 1e-3) / 1e9
+
+    def timed(name, fn, nbytes, nbuf):
+        ms = run_ms(fn, nbuf)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        cp = copy_gbs(nbytes, nbuf)
+        out[name] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 2),
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": int(nbytes),
+                     "copy_gbs": round(cp, 1), "frac_of_copy": round(gbs / cp, 4)}
         log(f"{name}: {out[name]}")
 
     for dt, es in (("fp32", 4), ("bf16", 2)):

@@ -44,6 +44,29 @@ def test_fill_cast_add_transpose(xp):
         assert z.get().tolist() == [0] * 7
 
 
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 2047, 2048, 2049, 100003])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_cast_every_pair_and_tail(xp, n, aligned):
+    """tl_cast: the 16-byte-piece kernel (aligned operands, 8 elements per thread plus an
+    element-wise tail) and the element-wise kernel (a source off 16-byte alignment), bit for
+    bit against NumPy's round-to-nearest-even narrowing and exact widening/copies."""
+    a = np.random.default_rng(n).standard_normal(n + 1).astype(F32) * 3
+    a[1] = np.float32(-0.0)
+    host = a[:n] if aligned else a[1:]
+    lib, h = xp.lib(), xp.ctx().handle
+    for dx in ("fp32", "bf16"):
+        full = xp.array(a if dx == "fp32" else ref.round_bf16(a), dtype=dx)
+        src = xp.DeviceTensor((n,), full.dtype, buf=full.buf,
+                              offset=full.offset + (0 if aligned else full.dtype.itemsize))
+        for dy in ("fp32", "bf16"):
+            out = xp.empty((n,), dy)
+            xp.check(lib.tl_cast(h, src.ptr, out.ptr, n, src.dtype.code, out.dtype.code))
+            want = ref.round_bf16(host) if "bf16" in (dx, dy) else host
+            got = np.asarray(out.get(), F32)
+            assert np.array_equal(got.view(np.uint32), np.asarray(want, F32).view(np.uint32)), \
+                (dx, dy, n, aligned)
+
+
 # ---- LayerNorm / RMSNorm ------------------------------------------------------------------
 NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (33, 4096), (2, 5000), (4, 8192), (3, 12000)]
 
@@ -124,10 +147,13 @@ def test_softmax_causal_offset(xp):
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
-@pytest.mark.parametrize("rows,cols", [(20011, 8), (50021, 384), (20011, 768), (12007, 2048)])
+@pytest.mark.parametrize("rows,cols", [(20011, 8), (50021, 384), (20011, 768), (12007, 2048),
+                                       (8209, 4096)])
 def test_norms_many_rows(xp, dt, rows, cols):
-    """Many short rows (one wavefront each, lanes past the row end masked), an odd row count
-    so the last workgroup is partial; every row must match."""
+    """Many short rows (one wavefront each, lanes past the row end masked, or none when the
+    row fills the wave's chunks), an odd row count so the last workgroup is partial; every row
+    must match. Inputs of 64 MiB and more (fp32 384 / 2048 / 4096 columns, bf16 4096) take the
+    non-temporal path."""
     rng = np.random.default_rng(rows + cols)
     x = rnd(dt, rng.standard_normal((rows, cols)).astype(F32) * 1.5 - 0.25)
     g = rnd(dt, rng.standard_normal(cols).astype(F32))
