@@ -232,6 +232,13 @@ int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, d
  * y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i+D/2] cos + x[i] sin. In place is allowed. */
 int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
                 int64_t seq_len, int64_t head_dim, int64_t seq_stride, int32_t dtype);
+/* tl_rope_fwd over two tensors rotated by the same T positions, in one launch: set 1 is
+ * (x1, y1, n_seq1, seq_stride1), set 2 (x2, y2, n_seq2, seq_stride2); either set may be
+ * empty (n_seq 0, pointers may then be null). Used for the queries and the new cache keys
+ * of one multi-query attention call. No reference counterpart (the reference has no RoPE). */
+int tl_rope2_fwd(tl_ctx* ctx, const void* x1, void* y1, int64_t n_seq1, int64_t seq_stride1,
+                 const void* x2, void* y2, int64_t n_seq2, int64_t seq_stride2,
+                 const void* table, int64_t seq_len, int64_t head_dim, int32_t dtype);
 /* Replaces GeLU.forward / SiLU.forward (reference activations.py:24-28, 41-45). */
 int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype);
 /* out[r] = first index of the maximum of row r (NaN counts as the maximum), int64.

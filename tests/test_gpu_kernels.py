@@ -214,6 +214,38 @@ def test_rope(xp, dt, shape):
         assert ref.max_rel(y, ref.rope(x, cos, sin)) <= TOL[dt], (dt, shape, pos0)
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,L,pos0", [(4, 8, 1, 1, 256, 136, 129),
+                                                 (2, 4, 2, 7, 64, 24, 9),
+                                                 (1, 3, 1, 5, 6, 16, 0)])
+def test_rope2_queries_and_cache_keys(xp, dt, B, Hq, Hkv, T, D, L, pos0):
+    """tl_rope2_fwd (queries packed [B, Hq, T, D] plus the new rows of a [B, Hkv, L, D] key
+    cache at pos0) equals the oracle's rotation of each, and leaves the rest of the cache
+    untouched; an empty second set is allowed. D = 6 takes the element-wise kernel."""
+    rng = np.random.default_rng(B * 1000 + T * 10 + D)
+    q = rnd(dt, rng.standard_normal((B, Hq, T, D)).astype(F32))
+    kc = rnd(dt, rng.standard_normal((B, Hkv, L, D)).astype(F32))
+    tab = xp.rope_table(T, D, 10000.0, pos0)
+    cos, sin = ref.rope_table(T, D, 10000.0, pos0)
+    dq, dk = up(xp, q, dt), up(xp, kc, dt)
+    es = dk.dtype.itemsize
+    ks = xp.DeviceTensor((B * Hkv, T, D), dk.dtype, buf=dk.buf, offset=dk.offset + pos0 * D * es)
+    xp.rope2(dq, ks, tab, T, n_seq2=B * Hkv, seq_stride2=L * D)
+    assert ref.max_rel(dq.get(), ref.rope(q, cos, sin)) <= TOL[dt], (dt, "q")
+    got_k, want_k = dk.get(), kc.copy()
+    want_k[:, :, pos0:pos0 + T] = ref.rope(kc[:, :, pos0:pos0 + T], cos, sin)
+    assert ref.max_rel(got_k[:, :, pos0:pos0 + T], want_k[:, :, pos0:pos0 + T]) <= TOL[dt], (dt, "k")
+    outside = np.ones(L, bool)
+    outside[pos0:pos0 + T] = False
+    assert np.array_equal(got_k[:, :, outside], kc[:, :, outside])
+    # bit-identical to two single-set launches, and the second set may be empty
+    dq2 = up(xp, q, dt)
+    xp.rope(dq2, tab, out=dq2)
+    dq3 = up(xp, q, dt)
+    xp.rope2(dq3, ks, tab, T, n_seq2=0)
+    assert np.array_equal(dq.get(), dq2.get()) and np.array_equal(dq3.get(), dq2.get())
+
+
 # ---- activations --------------------------------------------------------------------------
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("n", [1, 13, 4096, 1000003])

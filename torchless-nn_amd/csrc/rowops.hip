@@ -638,23 +638,35 @@ __global__ void rope_table_kernel(float* table, int64_t seq_len, int64_t head_di
   }
 }
 
+// One sequence set of a RoPE launch: n_seq sequences of seq_len rows, seq_stride elements
+// apart (x == y allowed).
+struct RopeSet {
+  const void* x;
+  void* y;
+  int64_t n_seq, seq_stride;
+};
+
 // One thread per (row, chunk of the first half): it loads that chunk and the matching chunk
 // of the second half, rotates both with the position's cos/sin (from the fp32 table, read
-// through L2) and writes both. Item indices are split with 32-bit multiply-high division
-// when the item count is below 2^31 (SMALL), else with 64-bit division in a grid-stride loop.
+// through L2) and writes both. Items of set 0 come first, then those of set 1 (a second
+// tensor rotated by the same positions, e.g. the queries and the new cache keys of one
+// attention call, so one launch serves both; n_seq = 0 leaves it empty). Item indices are
+// split with 32-bit multiply-high division when the item count is below 2^31 (SMALL), else
+// with 64-bit division in a grid-stride loop.
 template <typename T, bool VEC, bool SMALL>
-__global__ __launch_bounds__(256) void rope_kernel(const T* x, T* y, const float* __restrict__ table,
-                                                   int64_t n_seq, int64_t seq_len,
-                                                   int64_t head_dim, int64_t seq_stride,
+__global__ __launch_bounds__(256) void rope_kernel(RopeSet s0, RopeSet s1,
+                                                   const float* __restrict__ table,
+                                                   int64_t seq_len, int64_t head_dim,
                                                    FastDiv div_row, FastDiv div_seq) {
   constexpr int VW = VEC ? Elem<T>::kVec : 1;
   const int64_t half = head_dim / 2;
   const int64_t per_row = half / VW;
-  const int64_t total = n_seq * seq_len * per_row;
+  const int64_t total0 = s0.n_seq * seq_len * per_row;
+  const int64_t total = total0 + s1.n_seq * seq_len * per_row;
   const int64_t tsz = seq_len * half;
-  auto item = [&](int64_t row, int64_t i, int64_t sq, int64_t t) {
-    const T* xr = x + sq * seq_stride + t * head_dim;
-    T* yr = y + sq * seq_stride + t * head_dim;
+  auto item = [&](const RopeSet& st, int64_t i, int64_t sq, int64_t t) {
+    const T* xr = (const T*)st.x + sq * st.seq_stride + t * head_dim;
+    T* yr = (T*)st.y + sq * st.seq_stride + t * head_dim;
     const float* cs = table + t * half + i;
     const float* sn = table + tsz + t * half + i;
     float a[VW], b[VW], c[VW], s[VW], o1[VW], o2[VW];
@@ -688,19 +700,23 @@ __global__ __launch_bounds__(256) void rope_kernel(const T* x, T* y, const float
     }
   };
   if (SMALL) {
-    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= (uint32_t)total) return;
+    const bool second = idx >= (uint32_t)total0;
+    if (second) idx -= (uint32_t)total0;
     const uint32_t row = fast_div(idx, div_row);
     const uint32_t i = (idx - row * (uint32_t)per_row) * VW;
     const uint32_t sq = fast_div(row, div_seq);
-    item(row, i, sq, row - sq * (uint32_t)seq_len);
+    item(second ? s1 : s0, i, sq, row - sq * (uint32_t)seq_len);
     return;
   }
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t row = idx / per_row;
+    const bool second = idx >= total0;
+    const int64_t j = second ? idx - total0 : idx;
+    const int64_t row = j / per_row;
     const int64_t sq = row / seq_len;
-    item(row, (idx % per_row) * VW, sq, row - sq * seq_len);
+    item(second ? s1 : s0, (j % per_row) * VW, sq, row - sq * seq_len);
   }
 }
 
@@ -969,21 +985,24 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
 }
 
 template <typename T>
-static void launch_rope(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
-                        int64_t seq_len, int64_t head_dim, int64_t seq_stride) {
+static void launch_rope(tl_ctx* ctx, const RopeSet& s0, const RopeSet& s1, const void* table,
+                        int64_t seq_len, int64_t head_dim) {
   constexpr int VW = Elem<T>::kVec;
   const int64_t half = head_dim / 2;
-  const bool vec = half % VW == 0 && aligned16(x) && aligned16(y) && aligned16(table) &&
-                   (seq_len * half) % 4 == 0 && seq_stride % VW == 0;
-  const int64_t work = n_seq * seq_len * (vec ? half / VW : half);
+  auto set_vec = [&](const RopeSet& st) {
+    return st.n_seq == 0 ||
+           (aligned16(st.x) && aligned16(st.y) && st.seq_stride % VW == 0);
+  };
+  const bool vec = half % VW == 0 && aligned16(table) && (seq_len * half) % 4 == 0 &&
+                   set_vec(s0) && set_vec(s1);
+  const int64_t work = (s0.n_seq + s1.n_seq) * seq_len * (vec ? half / VW : half);
   const bool small = work < (int64_t)0x7fffffff;
   const FastDiv dr = make_fastdiv(small ? (uint32_t)(vec ? half / VW : half) : 1u);
   const FastDiv ds = make_fastdiv(small ? (uint32_t)seq_len : 1u);
   const unsigned g = small ? (unsigned)std::max<int64_t>(1, (work + 255) / 256) : grid_for(ctx, work, 256);
   auto go = [&](auto vec_tag, auto small_tag) {
     rope_kernel<T, decltype(vec_tag)::value, decltype(small_tag)::value>
-        <<<g, 256, 0, ctx->stream>>>((const T*)x, (T*)y, (const float*)table, n_seq, seq_len,
-                                     head_dim, seq_stride, dr, ds);
+        <<<g, 256, 0, ctx->stream>>>(s0, s1, (const float*)table, seq_len, head_dim, dr, ds);
   };
   if (vec && small) go(std::true_type(), std::true_type());
   else if (vec) go(std::true_type(), std::false_type());
@@ -1275,9 +1294,31 @@ int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t 
   TL_REQUIRE(x && y && table, "null pointer");
   const double es = (double)dtype_size(dtype);
   LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * n_seq * seq_len * head_dim);
-  if (dtype == TL_F32) launch_rope<float>(ctx, x, y, table, n_seq, seq_len, head_dim, seq_stride);
-  else launch_rope<bf16_t>(ctx, x, y, table, n_seq, seq_len, head_dim, seq_stride);
+  const RopeSet s0{x, y, n_seq, seq_stride}, s1{nullptr, nullptr, 0, 0};
+  if (dtype == TL_F32) launch_rope<float>(ctx, s0, s1, table, seq_len, head_dim);
+  else launch_rope<bf16_t>(ctx, s0, s1, table, seq_len, head_dim);
   return ls.finish("rope_fwd");
+}
+
+int tl_rope2_fwd(tl_ctx* ctx, const void* x1, void* y1, int64_t n_seq1, int64_t seq_stride1,
+                 const void* x2, void* y2, int64_t n_seq2, int64_t seq_stride2,
+                 const void* table, int64_t seq_len, int64_t head_dim, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n_seq1 >= 0 && n_seq2 >= 0 && seq_len > 0 && head_dim > 0 && head_dim % 2 == 0,
+             "bad sizes");
+  TL_REQUIRE((n_seq1 == 0 || seq_stride1 >= seq_len * head_dim) &&
+                 (n_seq2 == 0 || seq_stride2 >= seq_len * head_dim),
+             "seq_stride < seq_len * head_dim");
+  if (n_seq1 + n_seq2 == 0) return TL_OK;
+  TL_REQUIRE(table && (n_seq1 == 0 || (x1 && y1)) && (n_seq2 == 0 || (x2 && y2)), "null pointer");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * (n_seq1 + n_seq2) * seq_len * head_dim);
+  const RopeSet s0{x1, y1, n_seq1, seq_stride1}, s1{x2, y2, n_seq2, seq_stride2};
+  if (dtype == TL_F32) launch_rope<float>(ctx, s0, s1, table, seq_len, head_dim);
+  else launch_rope<bf16_t>(ctx, s0, s1, table, seq_len, head_dim);
+  return ls.finish("rope2_fwd");
 }
 
 int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype) {

@@ -390,10 +390,10 @@ class MultiQueryAttention(Layer):
             k, vt = xp.empty((B, Hkv, L, D), dt), xp.empty((B, Hkv, D, L), dt)
         linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0))
         table = _rope_table(T, D, self.rope_base, pos0)
-        xp.rope(q, table, out=q)
+        # queries and this call's cache keys rotated in one launch
         kslice = xp.DeviceTensor((B * Hkv, T, D), dt, buf=k.buf,
                                  offset=k.offset + pos0 * D * dt.itemsize)
-        xp.rope(kslice, table, out=kslice, seq_len=T, n_seq=B * Hkv, seq_stride=L * D)
+        xp.rope2(q, kslice, table, T, n_seq2=B * Hkv, seq_stride2=L * D)
         Tk = pos0 + T
         divisor = float(np.float32(D ** 0.5))
         heads = xp.empty((B, T, Hq * D), dt)

@@ -173,6 +173,7 @@ SIGNATURES = {
     "tl_softmax_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32, _I64, _I64, _I32],
     "tl_rope_table": [_P, _P, _I64, _I64, _F64, _I64],
     "tl_rope_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I32],
+    "tl_rope2_fwd": [_P, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _I64, _I32],
     "tl_act_fwd": [_P, _P, _P, _I64, _I32, _I32],
     "tl_argmax": [_P, _P, _I64, _I64, _I64, _I32, _P],
     "tl_gemm": [_P, ctypes.POINTER(_GemmDesc)],
@@ -619,6 +620,38 @@ def rope(x: DeviceTensor, table: DeviceTensor, out=None, seq_len=None, n_seq=Non
     lib_, h = _c()
     check(lib_.tl_rope_fwd(h, x.ptr, out.ptr, table.ptr, n, T, D, stride, x.dtype.code))
     return out
+
+
+def _rope_set(x: DeviceTensor, T, D, n_seq, seq_stride):
+    """(n, stride) of one RoPE operand, checked against its buffer (in place)."""
+    if not x.contiguous:
+        raise ValueError("rope needs a contiguous tensor")
+    if x.shape[-1] != D:
+        raise ValueError("rope operands must share the head dim")
+    n = n_seq if n_seq is not None else x.size // (T * D)
+    stride = seq_stride if seq_stride is not None else T * D
+    if n > 0 and x.offset + ((n - 1) * stride + T * D) * x.dtype.itemsize > x.buf.nbytes:
+        raise ValueError(f"rope over {n} sequences {stride} elements apart runs past the end "
+                         f"of its buffer")
+    return n, stride
+
+
+def rope2(x1: DeviceTensor, x2: DeviceTensor, table: DeviceTensor, seq_len, n_seq1=None,
+          seq_stride1=None, n_seq2=None, seq_stride2=None):
+    """In-place rotate-half RoPE of two tensors by the same `seq_len` positions in one launch
+    (the queries and the new cache keys of an attention call); each operand is either packed
+    [.., T, D] or `n_seq` sequences `seq_stride` elements apart, as in `rope`."""
+    if x1.dtype is not x2.dtype:
+        raise ValueError("rope2 operands must share a dtype")
+    D, T = x1.shape[-1], seq_len
+    n1, st1 = _rope_set(x1, T, D, n_seq1, seq_stride1)
+    n2, st2 = _rope_set(x2, T, D, n_seq2, seq_stride2)
+    lib_, h = _c()
+    check(lib_.tl_rope2_fwd(h, x1.ptr, x1.ptr, n1, st1, x2.ptr, x2.ptr, n2, st2, table.ptr, T, D,
+                            x1.dtype.code))
+    x1._version += 1
+    x2._version += 1
+    return x1, x2
 
 
 def activation(x: DeviceTensor, act: int, out=None):
