@@ -1480,6 +1480,11 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   }
   if (mfma) {
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
+    if (!d->tile)
+      for (const auto& r : ctx->tile_rules)
+        if (r.M == d->M && r.N == d->N && r.K == d->K && r.tile > 0 &&
+            r.tile <= TL_TILE_PERSIST_256x256_W8 && r.tile != TL_TILE_SKINNY)
+          tile = r.tile;
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
     // the persistent kernels store through a buffer resource: whole 16-byte pieces, byte
     // offsets below 2^31

@@ -165,6 +165,15 @@ int tl_init(int device, tl_ctx** out) {
   if (const char* g = std::getenv("TL_SKINNY_MAX_SPLIT")) ctx->skinny_max_split = std::atoi(g);
   if (const char* g = std::getenv("TL_ATTN_DECODE_CFG")) ctx->attn_decode_cfg = std::atoi(g);
   if (const char* g = std::getenv("TL_SOFTMAX_LONG_CFG")) ctx->softmax_long_cfg = std::atoi(g);
+  if (const char* g = std::getenv("TL_GEMM_TILE_FOR")) {
+    long long m, n, k;
+    int t, used;
+    for (const char* q = g; std::sscanf(q, " %lld , %lld , %lld = %d%n", &m, &n, &k, &t, &used) == 4;) {
+      ctx->tile_rules.push_back({(int64_t)m, (int64_t)n, (int64_t)k, t});
+      q += used;
+      while (*q == ';' || *q == ' ') ++q;
+    }
+  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;

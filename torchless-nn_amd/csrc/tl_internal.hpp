@@ -57,6 +57,13 @@ struct tl_ctx {
   int attn_decode_cfg = 0;
   // long-row softmax shape (TL_SOFTMAX_LONG_CFG): 0 default, 1..4 (threads, keep) choices
   int softmax_long_cfg = 0;
+  // per-shape GEMM tile overrides for automatic calls (TL_GEMM_TILE_FOR="M,N,K=tile;...",
+  // tile a tl_gemm_tile value): tuning sweeps inside a whole forward
+  struct TileRule {
+    int64_t M, N, K;
+    int tile;
+  };
+  std::vector<TileRule> tile_rules;
   // grow-only scratch for kernels that combine partial results (split argmax, split-KV
   // attention); used in stream order, so one buffer serves every call on this context
   void* ws = nullptr;
