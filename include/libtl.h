@@ -179,6 +179,8 @@ int tl_kprof_query(tl_ctx* ctx, int family, int64_t* launches, double* total_ms,
 /* y[i] = value (a kernel, not hipMemset, so it is safe under graph capture).
  * Replaces init_zeros_tensor (reference backend.py:33-34). */
 int tl_fill(tl_ctx* ctx, void* y, int64_t n, int32_t dtype, double value);
+/* y[i] = x[i] converted (fp32 <-> bf16 with round-to-nearest-even, or a copy). x and y may
+ * be the same pointer only when the types match; otherwise they must not overlap. */
 int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dtype_x, int32_t dtype_y);
 /* y[e] = mean + std * N(0,1), drawn on the device: Philox4x32-10 keyed by `seed` with
  * counter (e / 4, stream), Box-Muller on its output word pairs. Replaces

@@ -67,6 +67,20 @@ def test_cast_every_pair_and_tail(xp, n, aligned):
                 (dx, dy, n, aligned)
 
 
+def test_cast_rejects_overlapping_operands(xp):
+    """An in-place copy of one type is allowed; a conversion into its own (or an overlapping)
+    buffer would race between threads and is refused before any launch."""
+    lib, h = xp.lib(), xp.ctx().handle
+    a = xp.array(np.arange(64, dtype=F32), dtype="fp32")
+    xp.check(lib.tl_cast(h, a.ptr, a.ptr, 64, 0, 0))
+    assert np.array_equal(a.get(), np.arange(64, dtype=F32))
+    for dy, off in ((1, 0), (1, 64), (0, 4)):
+        rc = lib.tl_cast(h, a.ptr, a.ptr + off, 32, 0, dy)
+        assert rc != 0 and "overlap" in xp.last_error(), (dy, off)
+    xp.synchronize()
+    assert np.array_equal(a.get(), np.arange(64, dtype=F32))
+
+
 # ---- LayerNorm / RMSNorm ------------------------------------------------------------------
 NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (33, 4096), (2, 5000), (4, 8192), (3, 12000)]
 

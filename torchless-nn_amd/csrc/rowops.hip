@@ -1108,6 +1108,12 @@ int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dx, int32_t 
   TL_REQUIRE(dtype_is_float(dx) && dtype_is_float(dy), "cast supports fp32 and bf16 only");
   if (n == 0) return TL_OK;
   TL_REQUIRE(x && y, "null pointer");
+  {
+    const uintptr_t xa = (uintptr_t)x, ya = (uintptr_t)y;
+    const uintptr_t xe = xa + (uintptr_t)n * dtype_size(dx), ye = ya + (uintptr_t)n * dtype_size(dy);
+    TL_REQUIRE((dx == dy && xa == ya) || xe <= ya || ye <= xa,
+               "cast operands overlap (only an in-place copy of one type is allowed)");
+  }
   LaunchScope ls(ctx, TL_KF_MISC, 0, (double)n * (dtype_size(dx) + dtype_size(dy)));
   if (aligned16(x) && aligned16(y) && (n + 2047) / 2048 <= (int64_t)0xffffffffu) {
     const unsigned gv = (unsigned)((n + 2047) / 2048);
