@@ -387,6 +387,50 @@ def decode_sweep(xp, reps=50):
     return out
 
 
+CHAR_CFG = dict(vocab=65, ctx=128, layers=4, d=128, heads=4, act="gelu")
+
+
+def char_gpt_bench(xp, steps=50, warmup=5):
+    """BASELINE config 1, the reference's own CPU-runnable case: the char-level GPT forward in
+    fp32 (vocab 65, ctx 128, 4 layers, d 128, 4 heads, GeLU, batch 4 x 128 ids) on the device.
+    Too small for a roofline (0.95 GFLOP, ~50 launches): reported as latency."""
+    import gpt
+    net, _ = gpt.build_gpt(CHAR_CFG, dtype="fp32")
+    gpt.seed_parameters(net, 0)
+    ids = xp.array(np.random.default_rng(0).integers(0, 65, (4, 128)).astype(np.int32))
+    for _ in range(warmup):
+        net.predict(ids)
+    xp.synchronize()
+    e0, e1 = xp.Event(), xp.Event()
+    e0.record()
+    for _ in range(steps):
+        net.predict(ids)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    out = {"workload": "char-level GPT forward (BASELINE config 1): vocab 65, ctx 128, 4 layers, "
+                       "d 128, 4 heads, GeLU, fp32, batch 4 x 128 token ids, weights seeded",
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(512 / (ms * 1e-3), 1)}
+    log(f"char gpt config 1: {out}")
+    return out
+
+
+def cpu_baseline_char_gpt(runs=3):
+    """Config 1 on the host: the oracle's NumPy forward (op for op the reference's
+    XP_RUNTIME=CPU path), median of `runs` after one warm-up."""
+    from oracle import numpy_ref as ref
+    params = ref.gpt_params(CHAR_CFG, 0)
+    ids = np.random.default_rng(0).integers(0, 65, (4, 128))
+    ref.gpt_forward(ids, params, CHAR_CFG)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        ref.gpt_forward(ids, params, CHAR_CFG)
+        ts.append(time.perf_counter() - t0)
+    ms = float(np.median(ts)) * 1e3
+    return {"ms_per_step": round(ms, 3), "tokens_per_s": round(512 / (ms * 1e-3), 1),
+            "kind": "port", "sample": f"the whole config-1 forward, median of {runs} runs"}
+
+
 def cpu_baseline(sample_seqs=5, sample_T=SEQ):
     """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
     of the workload: `sample_seqs` sequences of T tokens of the same model."""
@@ -448,7 +492,7 @@ def main():
             xp.check(xp.lib().tl_cast(xp.ctx().handle, src.ptr, dst.ptr, n, 0, 0))
         xp.synchronize()
         del src, dst
-        log("copy calibration: 3 x cast_kernel<float,float> over 256 MiB")
+        log("copy calibration: 3 x cast_vec_kernel<float,float> over 256 MiB")
     if args.sweep_decode:
         print(json.dumps({"decode_sweep": decode_sweep(xp)}), flush=True)
         return
@@ -518,7 +562,11 @@ def main():
     rows = {} if args.no_row_kernels else row_kernel_bench(xp)
     gem = None if args.no_gemma else gemma_bench(xp)
     vit_line = None if args.no_vit else vit_bench(xp)
+    char = char_gpt_bench(xp)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
+    if not args.no_cpu_baseline:
+        char["cpu_baseline"] = cpu_baseline_char_gpt()
+        log(f"char gpt config 1 cpu baseline: {char['cpu_baseline']}")
     if cpu:
         log(f"cpu baseline: {cpu}")
 
@@ -539,6 +587,7 @@ def main():
         "row_kernels": rows,
         "gemma_decoder": gem,
         "vit_classifier": vit_line,
+        "char_gpt": char,
     }
     print(json.dumps(line), flush=True)
 
