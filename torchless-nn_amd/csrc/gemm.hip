@@ -1479,12 +1479,16 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     return ls.finish("gemm_skinny");
   }
   if (mfma) {
-    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, ctx->num_cus > 0 ? ctx->num_cus : 256);
+    const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus);
+    bool fixed = d->tile != 0;  // a caller's tile, or a TL_GEMM_TILE_FOR one, is kept as is
     if (!d->tile)
       for (const auto& r : ctx->tile_rules)
         if (r.M == d->M && r.N == d->N && r.K == d->K && r.tile > 0 &&
-            r.tile <= TL_TILE_PERSIST_256x256_W8 && r.tile != TL_TILE_SKINNY)
+            r.tile <= TL_TILE_PERSIST_256x256_W8 && r.tile != TL_TILE_SKINNY) {
           tile = r.tile;
+          fixed = true;
+        }
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
     // the persistent kernels store through a buffer resource: whole 16-byte pieces, byte
     // offsets below 2^31
@@ -1495,11 +1499,18 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     // next tile's first loads pay off when issued under the current tile's epilogue
     // (ViT-S/4 FFN1 +12%, out-proj +5%); at K = 768 the two variants tie and with one tile
     // per CU the persistent bookkeeping costs 4-10%.
-    if (!d->tile && persist_ok && d->K <= 512 &&
-        (tile == TL_TILE_DMA_256x96_W8 || tile == TL_TILE_DMA_256x128_W8)) {
+    // With at least 8 tiles of 128x128 per CU the two-per-CU persistent 128x128 tile walks
+    // 6+ tiles per workgroup and beats the 256-row persistent ones inside the model
+    // (ViT-S/4 FFN1, 33280 x 1536, K = 384: 2.77 -> 2.69 ms per forward; out-proj, 1.5 tiles
+    // per workgroup, is slower on it).
+    const int64_t t128 = ((d->M + 127) / 128) * ((d->N + 127) / 128);
+    if (!fixed && persist_ok && d->K <= 512 && d->K % 64 == 0 && t128 >= 8LL * cus) {
+      tile = TL_TILE_PERSIST_128x128;
+    } else if (!fixed && persist_ok && d->K <= 512 &&
+               (tile == TL_TILE_DMA_256x96_W8 || tile == TL_TILE_DMA_256x128_W8)) {
       const TileShape& t = kTiles[tile];
       const int64_t nt = ((d->M + t.bm - 1) / t.bm) * ((d->N + t.bn - 1) / t.bn);
-      if (nt >= 2LL * (ctx->num_cus > 0 ? ctx->num_cus : 256))
+      if (nt >= 2LL * cus)
         tile = tile == TL_TILE_DMA_256x96_W8 ? TL_TILE_PERSIST_256x96_W8 : TL_TILE_PERSIST_256x128_W8;
     }
     const bool persistent = is_persistent(tile);
