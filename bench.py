@@ -407,9 +407,25 @@ def char_gpt_bench(xp, steps=50, warmup=5):
         net.predict(ids)
     e1.record()
     ms = e0.elapsed_ms(e1) / steps
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        net.predict(ids)
+    host_ms = (time.perf_counter() - t0) / steps * 1e3  # issue time (the queue runs ahead)
+    xp.synchronize()
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    for _ in range(steps):
+        net.predict(ids)
+    xp.synchronize()
+    fam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
     out = {"workload": "char-level GPT forward (BASELINE config 1): vocab 65, ctx 128, 4 layers, "
                        "d 128, 4 heads, GeLU, fp32, batch 4 x 128 token ids, weights seeded",
-           "ms_per_step": round(ms, 4), "tokens_per_s": round(512 / (ms * 1e-3), 1)}
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(512 / (ms * 1e-3), 1),
+           "host_issue_ms_per_step": round(host_ms, 4),
+           "kernel_breakdown": {f: {"ms_per_step": round(r["ms"] / steps, 4),
+                                    "launches_per_step": r["launches"] // steps}
+                                for f, r in fam.items() if r["launches"]}}
     log(f"char gpt config 1: {out}")
     return out
 

@@ -1168,9 +1168,14 @@ __global__ __launch_bounds__(64) void gemm_skinny_reduce_kernel(GemmParams p, co
   epilogue4<bf16_t, TO>(p, zo, zi, r, (int64_t)blockIdx.x * 16 + 4 * g, v);
 }
 
+// 64x64 tiles, 32-wide K steps, 4x4 outputs per thread. The next K step's A and B elements
+// are loaded into registers while the current step is computed from LDS, so each step costs
+// its FMAs rather than a global-memory round trip (512x128x512: 32 dependent 16-wide steps
+// took 54 us).
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
-  constexpr int BM = 64, BN = 64, BK = 16;
+  constexpr int BM = 64, BN = 64, BK = 32;
+  constexpr int LA = BM * BK / 256, LB = BN * BK / 256;
   __shared__ float As[BK][BM + 4];
   __shared__ float Bs[BK][BN + 4];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -1181,27 +1186,50 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
   const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
   const TI* A = (const TI*)p.A + zo * p.sa_o + zi * p.sa_i;
   const TI* B = (const TI*)p.B + zo * p.sb_o + zi * p.sb_i;
-  float acc[4][4] = {};
-  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
+  float ra[LA], rb[LB];
+  // element e of this thread: A row idx / BK, k idx % BK; B (K x N) k idx / BN, column
+  // idx % BN, or (N x K) column idx / BK, k idx % BK; consecutive threads read consecutive
+  // addresses in every layout
+  auto load = [&](int64_t k0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < LA; ++e) {
+      const int idx = e * 256 + tid, r = idx / BK, kk = idx % BK;
+      const int64_t gm = m0 + r, gk = k0 + kk;
+      ra[e] = (gm < p.M && gk < p.K) ? Elem<TI>::load(A + gm * p.lda + gk) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < LB; ++e) {
       const int idx = e * 256 + tid;
-      {
-        const int r = idx / BK, kk = idx % BK;
-        const int64_t gm = m0 + r, gk = k0 + kk;
-        As[kk][r] = (gm < p.M && gk < p.K) ? Elem<TI>::load(A + gm * p.lda + gk) : 0.f;
-      }
       if (p.b_kn) {
         const int kk = idx / BN, c = idx % BN;
         const int64_t gn = n0 + c, gk = k0 + kk;
-        Bs[kk][c] = (gn < p.N && gk < p.K) ? Elem<TI>::load(B + gk * p.ldb + gn) : 0.f;
+        rb[e] = (gn < p.N && gk < p.K) ? Elem<TI>::load(B + gk * p.ldb + gn) : 0.f;
       } else {
         const int c = idx / BK, kk = idx % BK;
         const int64_t gn = n0 + c, gk = k0 + kk;
-        Bs[kk][c] = (gn < p.N && gk < p.K) ? Elem<TI>::load(B + gn * p.ldb + gk) : 0.f;
+        rb[e] = (gn < p.N && gk < p.K) ? Elem<TI>::load(B + gn * p.ldb + gk) : 0.f;
       }
     }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int e = 0; e < LA; ++e) {
+      const int idx = e * 256 + tid;
+      As[idx % BK][idx / BK] = ra[e];
+    }
+#pragma unroll
+    for (int e = 0; e < LB; ++e) {
+      const int idx = e * 256 + tid;
+      if (p.b_kn) Bs[idx / BN][idx % BN] = rb[e];
+      else Bs[idx % BK][idx / BK] = rb[e];
+    }
+  };
+  float acc[4][4] = {};
+  load(0);
+  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
+    store();
     __syncthreads();
+    if (k0 + BK < p.K) load(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; ++kk) {
       float a[4], b[4];
