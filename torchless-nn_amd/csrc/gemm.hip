@@ -1172,8 +1172,13 @@ __global__ __launch_bounds__(64) void gemm_skinny_reduce_kernel(GemmParams p, co
 // are loaded into registers while the current step is computed from LDS, so each step costs
 // its FMAs rather than a global-memory round trip (512x128x512: 32 dependent 16-wide steps
 // took 54 us).
+//
+// Split K (part != nullptr): workgroup (tile, blockIdx.y) covers K range [y kc, (y + 1) kc)
+// and writes its raw 64x64 sums to part[(z, tile, y)]; gemm_simt_reduce_kernel adds the
+// gridDim.y parts in order and runs the epilogue. Used when the tiles alone leave most CUs
+// idle and K is long (512x128x512: 16 tiles).
 template <typename TI, typename TO>
-__global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
+__global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p, float* part, int64_t kc) {
   constexpr int BM = 64, BN = 64, BK = 32;
   constexpr int LA = BM * BK / 256, LB = BN * BK / 256;
   __shared__ float As[BK][BM + 4];
@@ -1225,11 +1230,13 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
     }
   };
   float acc[4][4] = {};
-  load(0);
-  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
+  const int64_t kb = part ? (int64_t)blockIdx.y * kc : 0;
+  const int64_t ke = part ? min(p.K, kb + kc) : p.K;
+  load(kb);
+  for (int64_t k0 = kb; k0 < ke; k0 += BK) {
     store();
     __syncthreads();
-    if (k0 + BK < p.K) load(k0 + BK);
+    if (k0 + BK < ke) load(k0 + BK);
 #pragma unroll
     for (int kk = 0; kk < BK; ++kk) {
       float a[4], b[4];
@@ -1244,8 +1251,38 @@ __global__ __launch_bounds__(256) void gemm_simt_kernel(GemmParams p) {
     }
     __syncthreads();
   }
+  if (part) {
+    float* dst = part + ((z * gridDim.x + tile) * gridDim.y + blockIdx.y) * (BM * BN);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<float4*>(dst + (ty * 4 + i) * BN + tx * 4) =
+          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) epilogue4<TI, TO>(p, zo, zi, m0 + ty * 4 + i, n0 + tx * 4, acc[i]);
+}
+
+// One workgroup per (z, tile): the `split` partial 64x64 sums in K order, then the epilogue.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void gemm_simt_reduce_kernel(GemmParams p, const float* part,
+                                                               int split) {
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int64_t z = blockIdx.z;
+  const int64_t zo = z / p.batch_inner, zi = z % p.batch_inner;
+  const int tile = blockIdx.x;
+  const int64_t m0 = (int64_t)(tile / p.tiles_n) * 64;
+  const int64_t n0 = (int64_t)(tile % p.tiles_n) * 64;
+  const float* src = part + (z * gridDim.x + tile) * (int64_t)split * 4096;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < split; ++k) {
+      const float4 t = *reinterpret_cast<const float4*>(src + k * 4096 + (ty * 4 + i) * 64 + tx * 4);
+      v[0] += t.x; v[1] += t.y; v[2] += t.z; v[3] += t.w;
+    }
+    epilogue4<TI, TO>(p, zo, zi, m0 + ty * 4 + i, n0 + tx * 4, v);
+  }
 }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1563,13 +1600,39 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.tiles_n = (int)((d->N + 63) / 64);
   TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
   dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+  // Split K (K >= 256) over workgroups while the parts still fit in one round on the CUs and
+  // each keeps at least two 32-wide K steps (512x128x512: 16 tiles x 8 parts).
+  const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+  const int64_t tiles = (int64_t)grid.x * batch;
+  int64_t split = 1;
+  while (d->K >= 256 && split < 16 && tiles * split * 2 <= cus && d->K / (split * 2) >= 64)
+    split *= 2;
+  float* part = nullptr;
+  int64_t kc = d->K;
+  if (split > 1) {
+    kc = ((d->K + split - 1) / split + 31) / 32 * 32;
+    split = (d->K + kc - 1) / kc;
+    void* ws;
+    rc = workspace(ctx, (size_t)tiles * split * 4096 * sizeof(float), &ws);
+    if (rc) return rc;
+    part = (float*)ws;
+    grid.y = (unsigned)split;
+  }
   LaunchScope ls(ctx, family, flops, bytes);
+  auto go = [&](auto ti, auto to) {
+    using TI = decltype(ti);
+    using TO = decltype(to);
+    gemm_simt_kernel<TI, TO><<<grid, 256, 0, ctx->stream>>>(p, part, kc);
+    if (part)
+      gemm_simt_reduce_kernel<TI, TO><<<dim3(grid.x, 1, grid.z), 256, 0, ctx->stream>>>(
+          p, part, (int)split);
+  };
   if (d->dtype_in == TL_F32) {
-    if (f32out) gemm_simt_kernel<float, float><<<grid, 256, 0, ctx->stream>>>(p);
-    else gemm_simt_kernel<float, bf16_t><<<grid, 256, 0, ctx->stream>>>(p);
+    if (f32out) go(float(), float());
+    else go(float(), bf16_t());
   } else {
-    if (f32out) gemm_simt_kernel<bf16_t, float><<<grid, 256, 0, ctx->stream>>>(p);
-    else gemm_simt_kernel<bf16_t, bf16_t><<<grid, 256, 0, ctx->stream>>>(p);
+    if (f32out) go(bf16_t(), float());
+    else go(bf16_t(), bf16_t());
   }
   return ls.finish("gemm_simt");
 }
