@@ -535,34 +535,24 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
          out_dtype=None, batch=1, batch_inner=1, sa=(0, 0), sb=(0, 0), sc=(0, 0), bias=None,
          residual=None, ldr=0, sr=(0, 0), act=TL_ACT_NONE, divisor=1.0, qkv=None,
          family="gemm_mfma", tile="auto", geglu=False):
-    d = _GemmDesc()
-    d.M, d.N, d.K = M, N, K
-    d.A, d.lda, d.B, d.ldb, d.b_layout = A.ptr, lda, B.ptr, ldb, b_layout
-    d.C, d.ldc = (C.ptr if C is not None else None), ldc
-    d.dtype_in = A.dtype.code
-    d.dtype_out = as_dtype(out_dtype).code if out_dtype is not None else A.dtype.code
-    d.batch, d.batch_inner = batch, batch_inner
-    d.sa_o, d.sa_i = sa
-    d.sb_o, d.sb_i = sb
-    d.sc_o, d.sc_i = sc
-    d.bias = bias.ptr if bias is not None else None
-    d.residual = residual.ptr if residual is not None else None
-    d.ldr = ldr
-    d.sr_o, d.sr_i = sr
-    d.act, d.divisor = act, float(divisor)
-    d.family = KFAMILY[family]
-    d.tile = GEMM_TILES[tile]
     if qkv is not None:
         q, k, vt, T, Hq, Hkv, Dh = qkv[:7]
         kv_len, kv_pos0 = (qkv[7], qkv[8]) if len(qkv) > 7 else (0, 0)
-        d.epilogue = TL_EPI_QKV_SPLIT
-        d.q, d.k, d.vt = q.ptr, k.ptr, vt.ptr
-        d.seq_len, d.n_heads_q, d.n_heads_kv, d.head_dim = T, Hq, Hkv, Dh
-        d.kv_len, d.kv_pos0 = kv_len, kv_pos0
-    elif geglu:
-        d.epilogue = TL_EPI_GEGLU
+        epi, qp, kp, vp = TL_EPI_QKV_SPLIT, q.ptr, k.ptr, vt.ptr
     else:
-        d.epilogue = TL_EPI_STORE
+        epi = TL_EPI_GEGLU if geglu else TL_EPI_STORE
+        qp = kp = vp = None
+        T = Hq = Hkv = Dh = kv_len = kv_pos0 = 0
+    code_in = A.dtype.code
+    # one positional constructor call, in the field order of _GemmDesc
+    d = _GemmDesc(M, N, K, A.ptr, lda, B.ptr, ldb, b_layout,
+                  C.ptr if C is not None else None, ldc, code_in,
+                  as_dtype(out_dtype).code if out_dtype is not None else code_in,
+                  batch, batch_inner, sa[0], sa[1], sb[0], sb[1], sc[0], sc[1],
+                  bias.ptr if bias is not None else None,
+                  residual.ptr if residual is not None else None, ldr, sr[0], sr[1],
+                  act, float(divisor), epi, qp, kp, vp, T, Hq, Hkv, Dh, kv_len, kv_pos0,
+                  KFAMILY[family], GEMM_TILES[tile])
     lib_, h = _c()
     check(lib_.tl_gemm(h, ctypes.byref(d)))
 
