@@ -324,7 +324,7 @@ GEMM_CASES = [  # M, N, K (fp32: few tiles with K >= 256 split K over workgroups
     # 128x128x768 in 8 parts, 300x70x1000 with a short last part)
     (1, 1, 8), (5, 7, 8), (64, 64, 64), (130, 70, 72), (128, 128, 768), (257, 300, 136),
     (512, 2304, 768), (1000, 65, 128), (8, 50257, 64), (512, 128, 512), (300, 70, 1000),
-    (64, 64, 2000),
+    (64, 64, 2000), (2048, 1040, 260),  # fp32 with B [N, K]: the fp32 matrix-core kernel
 ]
 
 

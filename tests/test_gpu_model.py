@@ -47,6 +47,21 @@ def test_char_gpt_fp32_end_to_end(tl):
     assert np.array_equal(tl["xp"].argmax(probs).get(), np.argmax(probs.get(), -1))
 
 
+def test_gpt_fp32_on_the_fp32_matrix_cores(tl):
+    """An fp32 GPT large enough that its FFN, LM-head and batched attention products take the
+    fp32 MFMA kernel (>= 128 output tiles of 128x128; weights packed [N, K]) and its smaller
+    ones the VALU kernel: logits and probabilities within 1e-5 of the oracle, device argmax
+    ids equal to NumPy's on the same logits."""
+    cfg = dict(vocab=1030, ctx=512, layers=2, d=256, heads=4, act="gelu")
+    ids = np.random.default_rng(21).integers(0, cfg["vocab"], (4, 512))
+    net, probs, logits = run_gpt(tl, cfg, ids, "fp32", seed=2)
+    want_p, want_l = ref.gpt_forward(ids, ref.gpt_params(cfg, 2), cfg, return_logits=True)
+    got_l = logits.get()
+    assert ref.max_rel(got_l, want_l) <= 1e-5
+    assert ref.max_rel(probs.get(), want_p) <= 1e-5
+    assert np.array_equal(tl["xp"].argmax(logits).get(), np.argmax(got_l, -1))
+
+
 def test_char_gpt_uint8_ids_like_the_notebook(tl):
     cfg = dict(vocab=65, ctx=128, layers=1, d=128, heads=4, act="silu")
     ids = np.random.default_rng(2).integers(0, 65, (2, 50)).astype(np.uint8)

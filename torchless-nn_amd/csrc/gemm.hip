@@ -719,6 +719,120 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
   mfma_epilogue<TO, TM, TN>(e, zo, zi, m0 + wm * WM + fr, n0 + wn * WN + 4 * fc, acc);
 }
 
+// gemm_mfma_f32_kernel: fp32 operands on the matrix cores (v_mfma_f32_16x16x4f32: fp32
+// products, fp32 accumulation), for the fp32 models (the reference's default FLOAT_TYPE).
+// The gemm_mfma_kernel scheme with 4-byte elements: A [M, K] and B [N, K] both K-contiguous
+// (K % 4 == 0, rows 16-byte aligned), 32-element K steps as 8 chunks of 16 B per row,
+// XOR-swizzled in LDS, double-buffered through registers. A lane's 16-byte fragment feeds
+// four MFMAs: MFMA q takes element q of every lane's chunk, so the four lane groups supply
+// K indices 4c + q of their chunks c; A and B use the same assignment, which covers each K
+// index of the step once. B is the first MFMA operand, so a lane's four results are four
+// consecutive output columns of one row, the layout epilogue4 stores.
+template <typename TO, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_f32_kernel(GemmParams p) {
+  constexpr int NT = 64 * WGM * WGN;
+  constexpr int BK = 32;                   // fp32 elements of K per step: 8 chunks of 16 B
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int RPP = NT / 8;              // tile rows one load pass covers
+  constexpr int A_CH = BM / RPP, B_CH = BN / RPP;
+  static_assert(BM % RPP == 0 && BN % RPP == 0 && RPP % 8 == 0, "bad tile/thread split");
+  static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
+  __shared__ __attribute__((aligned(16))) float As[2][BM * BK];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * BK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave - wm * WGN;
+  const int64_t z = blockIdx.z;
+  const int64_t zo = z / p.batch_inner, zi = z - zo * p.batch_inner;
+  int tm, tn;
+  map_tile(blockIdx.x, p, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t K = p.K;
+
+  const float* Ab = (const float*)p.A + zo * p.sa_o + zi * p.sa_i + m0 * p.lda;
+  const float* Bb = (const float*)p.B + zo * p.sb_o + zi * p.sb_i + n0 * p.ldb;
+  const int lr = tid >> 3, lc = tid & 7;
+  const int slot = lr * BK + ((lc ^ (lr & 7)) << 2);
+  uint32_t a_off[A_CH], b_off[B_CH];
+  {
+    // rows past M or N are clamped to the last row: computed, never stored
+    const int a_last = (int)min((int64_t)BM - 1, p.M - 1 - m0);
+    const int b_last = (int)min((int64_t)BN - 1, p.N - 1 - n0);
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) a_off[i] = (uint32_t)(min(i * RPP + lr, a_last) * p.lda + lc * 4);
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) b_off[i] = (uint32_t)(min(i * RPP + lr, b_last) * p.ldb + lc * 4);
+  }
+  uint4 ra[A_CH], rb[B_CH];
+  auto load_tile = [&](int64_t k0) {
+    const float* a = Ab + k0;
+    const float* b = Bb + k0;
+    if (k0 + BK <= K) {
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const uint4*>(a + a_off[i]);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const uint4*>(b + b_off[i]);
+    } else {  // K tail: K % 4 == 0, so a chunk is either fully inside K or fully outside
+      const bool in = k0 + lc * 4 < K;
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i)
+        ra[i] = in ? *reinterpret_cast<const uint4*>(a + a_off[i]) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < B_CH; ++i)
+        rb[i] = in ? *reinterpret_cast<const uint4*>(b + b_off[i]) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<uint4*>(&As[buf][slot + i * RPP * BK]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<uint4*>(&Bs[buf][slot + i * RPP * BK]) = rb[i];
+  };
+
+  f32x4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (int)((K + BK - 1) / BK);
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  const int fr = lane & 15, fc = lane >> 4;
+  const int a_frag = (wm * WM + fr) * BK, b_frag = (wn * WN + fr) * BK;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tile((int64_t)(kt + 1) * BK);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 2;
+      f32x4 af[TM], bfr[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f32x4*>(&As[cur][a_frag + i * 16 * BK + sw]);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const f32x4*>(&Bs[cur][b_frag + j * 16 * BK + sw]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bfr[j][q], af[i][q], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) store_tile(cur ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      epilogue4<float, TO>(p, zo, zi, m0 + wm * WM + fr + 16 * i, n0 + wn * WN + 16 * j + 4 * fc, v);
+    }
+}
+
 // gemm_dma_kernel: same tiling and epilogue as gemm_mfma_kernel, for K % 64 == 0. Operand
 // tiles move from global memory straight into LDS (global_load_lds_dwordx4: each lane of a
 // wave writes its 16 bytes at LDS base + 16 * lane), so the pipeline can run STAGES - 1
@@ -1513,7 +1627,15 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   const double flops = 2.0 * d->M * d->N * d->K * batch;
   const double bytes = batch * (es_in * ((double)d->M * d->K + (double)d->N * d->K) +
                                 (double)eo * d->M * d->N * (d->residual ? 2 : 1));
-  const int family = mfma ? d->family : TL_KF_GEMM_SIMT;
+  // fp32 operands on the matrix cores under the same layout rules (4-element alignment) when
+  // there are at least 128 output tiles of 128x128; fewer stay on the split-K VALU kernel.
+  const bool mfma32 = d->dtype_in == TL_F32 && d->b_layout == TL_B_NK && d->K % 4 == 0 &&
+                      d->lda % 4 == 0 && d->ldb % 4 == 0 && d->sa_o % 4 == 0 &&
+                      d->sa_i % 4 == 0 && d->sb_o % 4 == 0 && d->sb_i % 4 == 0 &&
+                      al16(d->A) && al16(d->B) && d->lda * 128 < (1LL << 31) &&
+                      d->ldb * 128 < (1LL << 31) &&
+                      ((d->M + 127) / 128) * ((d->N + 127) / 128) * batch >= 128;
+  const int family = (mfma || mfma32) ? d->family : TL_KF_GEMM_SIMT;
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
   const bool f32out = d->dtype_out == TL_F32;
   const bool skinny = mfma && (d->tile == TL_TILE_SKINNY || (d->tile == TL_TILE_AUTO && d->M <= 16));
@@ -1595,6 +1717,16 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     else if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
     else launch_mfma<bf16_t>(tile, grid, ctx->stream, p);
     return ls.finish("gemm_mfma");
+  }
+  if (mfma32) {
+    p.tiles_m = (int)((d->M + 127) / 128);
+    p.tiles_n = (int)((d->N + 127) / 128);
+    TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+    LaunchScope ls(ctx, family, flops, bytes);
+    if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    return ls.finish("gemm_mfma_f32");
   }
   p.tiles_m = (int)((d->M + 63) / 64);
   p.tiles_n = (int)((d->N + 63) / 64);

@@ -49,7 +49,9 @@ def linear(x2d, w, bias=None, act=xp.TL_ACT_NONE, residual=None, out=None, qkv=N
         raise ValueError(f"matmul shape mismatch: {x2d.shape} @ {w.shape}")
     if qkv is None and out is None:
         out = xp.empty((M, N), x2d.dtype)
-    if w.dtype is xp.bfloat16:
+    # bf16 always, fp32 when the product is large enough for the fp32 matrix-core kernel
+    # (at least 128 output tiles of 128x128, K % 4 == 0): both read B as [N, K]
+    if w.dtype is xp.bfloat16 or (K % 4 == 0 and -(-M // 128) * -(-N // 128) >= 128):
         B, ldb, layout = _packed_nk(w), K, xp.TL_B_NK
     else:
         B, ldb, layout = w, w.pitch, xp.TL_B_KN
