@@ -387,6 +387,39 @@ def decode_sweep(xp, reps=50):
     return out
 
 
+def gpt2_fp32_bench(xp, steps=3, warmup=1):
+    """The headline model in fp32, the reference's default FLOAT_TYPE (what a drop-in user
+    runs without XP_FLOAT=bf16): large products on the fp32 matrix cores, attention
+    materialised (scores, causal softmax, P.V) as the reference computes it."""
+    import gpt
+    net, _ = gpt.build_gpt(CFG, dtype="fp32")
+    gpt.seed_parameters(net, 0)
+    ids = xp.array(np.random.default_rng(1).integers(0, CFG["vocab"], (BATCH, SEQ)).astype(np.int32))
+    for _ in range(warmup):
+        net.predict(ids)
+    xp.synchronize()
+    e0, e1 = xp.Event(), xp.Event()
+    e0.record()
+    for _ in range(steps):
+        net.predict(ids)
+    e1.record()
+    ms = e0.elapsed_ms(e1) / steps
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    net.predict(ids)
+    xp.synchronize()
+    fam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
+    out = {"workload": "GPT-2-small-shape prefill (config 3 shape) in fp32: B 8, T 1024",
+           "ms_per_step": round(ms, 3), "tokens_per_s": round(BATCH * SEQ / (ms * 1e-3), 1),
+           "kernel_breakdown": {f: {"ms_per_step": round(r["ms"], 3), "launches_per_step": r["launches"],
+                                    "tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1) if r["flops"] else None}
+                                for f, r in fam.items() if r["launches"]}}
+    log(f"gpt2 fp32: {json.dumps(out)}")
+    del net
+    return out
+
+
 CHAR_CFG = dict(vocab=65, ctx=128, layers=4, d=128, heads=4, act="gelu")
 
 
@@ -481,6 +514,7 @@ def main():
                     help="only time the standalone row kernels (a tuning run, no model)")
     ap.add_argument("--no-gemma", action="store_true", help="skip the config-5 decoder section")
     ap.add_argument("--no-vit", action="store_true", help="skip the config-4 ViT section")
+    ap.add_argument("--no-gpt2-fp32", action="store_true", help="skip the fp32 GPT-2 section")
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
@@ -579,6 +613,7 @@ def main():
     gem = None if args.no_gemma else gemma_bench(xp)
     vit_line = None if args.no_vit else vit_bench(xp)
     char = char_gpt_bench(xp)
+    f32 = None if args.no_gpt2_fp32 else gpt2_fp32_bench(xp)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     if not args.no_cpu_baseline:
         char["cpu_baseline"] = cpu_baseline_char_gpt()
@@ -604,6 +639,7 @@ def main():
         "gemma_decoder": gem,
         "vit_classifier": vit_line,
         "char_gpt": char,
+        "gpt2_fp32": f32,
     }
     print(json.dumps(line), flush=True)
 
