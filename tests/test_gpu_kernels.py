@@ -407,9 +407,12 @@ def test_gemm_batched_two_level(xp, dt):
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("heads", [(4, 4), (8, 1), (4, 2)])
-def test_gemm_qkv_split(xp, dt, heads):
+@pytest.mark.parametrize("dims", [(2, 24, 64, 16), (8, 512, 128, 64)])
+def test_gemm_qkv_split(xp, dt, heads, dims):
+    """The head scatter epilogue; at (8, 512, 128, 64) the fp32 product has >= 128 tiles of
+    128x128 and runs on the fp32 matrix-core kernel."""
     Hq, Hkv = heads
-    B, T, C, D = 2, 24, 64, 16
+    B, T, C, D = dims
     N = (Hq + 2 * Hkv) * D
     rng = np.random.default_rng(Hq * 10 + Hkv)
     x = rnd(dt, rng.standard_normal((B * T, C)).astype(F32))
