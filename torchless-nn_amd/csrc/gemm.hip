@@ -1460,6 +1460,9 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
     const int64_t a96 = (t96 + slots - 1) / slots * 128 * 96;
     if (t96 >= cus) return a96 < a128 ? TL_TILE_DMA_128x96 : TL_TILE_DMA_128x128;
   }
+  // at most 64 rows per product (the ViT patch projection, batched over images, M = 64,
+  // K = 48): 128-row tiles would compute half padding (36.6 -> 22.5 us in the model)
+  if (M <= 64) return TL_TILE_64x64;
   if (t128 >= 16LL * cus) return TL_TILE_128x128;
   if (t64 >= (int64_t)cus) return TL_TILE_128x64;
   return TL_TILE_64x64;
