@@ -480,27 +480,43 @@ def cpu_baseline_char_gpt(runs=3):
             "kind": "port", "sample": f"the whole config-1 forward, median of {runs} runs"}
 
 
-def cpu_baseline(sample_seqs=5, sample_T=SEQ):
-    """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
-    of the workload: `sample_seqs` sequences of T tokens of the same model."""
-    from oracle import numpy_ref as ref
-    threads = None
+def _blas_info():
+    """(threads, "vendor version") of the BLAS NumPy calls, from threadpoolctl."""
     try:
         from threadpoolctl import threadpool_info
-        threads = max(int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas")
+        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        if blas:
+            b = blas[0]
+            return int(b.get("num_threads", 1)), f"{b.get('internal_api', '?')} {b.get('version', '?')}"
     except Exception:
         pass
+    return 1, "unknown"
+
+
+def cpu_baseline(sample_seqs=2, sample_T=SEQ, runs=3):
+    """The oracle's NumPy forward (op for op the reference's CPU runtime) on a bounded sample
+    of the workload: `sample_seqs` sequences of T tokens of the same model; one warm-up run,
+    then the median of `runs`."""
+    from oracle import numpy_ref as ref
+    threads, blas = _blas_info()
     params = ref.gpt_params(CFG, 0)
     ids = np.random.default_rng(1).integers(0, CFG["vocab"], (sample_seqs, sample_T))
-    t0 = time.perf_counter()
     ref.gpt_forward(ids, params, CFG)
-    dt = time.perf_counter() - t0
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        ref.gpt_forward(ids, params, CFG)
+        ts.append(time.perf_counter() - t0)
+    dt = float(np.median(ts))
     return {"value": round(sample_seqs * sample_T / dt, 1), "unit": "tokens/s",
-            "cores": threads or 1, "kind": "port",
+            "cores": threads, "kind": "port",
             "sample": (f"{sample_seqs} x {sample_T} tokens of the same GPT-2-small-shape forward, "
-                       f"fp32 NumPy (oracle/numpy_ref.py), one run of {dt:.1f} s; sgemm on "
-                       f"{threads} BLAS threads, ufuncs single-threaded; "
-                       f"os.cpu_count()={os.cpu_count()}, affinity={len(os.sched_getaffinity(0))}")}
+                       f"fp32 NumPy (oracle/numpy_ref.py); one warm-up, then the median of {runs} "
+                       f"runs ({', '.join(f'{t:.2f}' for t in ts)} s); sgemm multi-threaded on "
+                       f"{threads} threads of {blas} (OPENBLAS_NUM_THREADS="
+                       f"{os.environ.get('OPENBLAS_NUM_THREADS', 'unset')}), NumPy ufuncs "
+                       f"single-threaded; os.cpu_count()={os.cpu_count()}, "
+                       f"affinity={len(os.sched_getaffinity(0))}")}
 
 
 def main():

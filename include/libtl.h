@@ -152,7 +152,7 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr);
 int tl_free(tl_ctx* ctx, void* ptr);
 int tl_empty_cache(tl_ctx* ctx);
 int tl_mem_stats(tl_ctx* ctx, size_t* bytes_in_use, size_t* bytes_cached);
-/* Host<->device copies. Replace `xp.array(host)` (reference network.py:297, 332) and
+/* Host<->device copies. Replace `xp.array(host)` (reference network.py:117-118, 152-153) and
  * `.get()` (reference demo.ipynb:1535). h2d returns once the host buffer may be reused. */
 int tl_memcpy_h2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
 int tl_memcpy_d2h(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
@@ -244,15 +244,16 @@ int tl_rope2_fwd(tl_ctx* ctx, const void* x1, void* y1, int64_t n_seq1, int64_t 
 /* Replaces GeLU.forward / SiLU.forward (reference activations.py:24-28, 41-45). */
 int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype);
 /* out[r] = first index of the maximum of row r (NaN counts as the maximum), int64.
- * Replaces xp.argmax(y_hat, axis=-1) (reference network.py:315, 338). */
+ * Replaces xp.argmax(y_hat, axis=-1) (reference network.py:135, 158). */
 int tl_argmax(tl_ctx* ctx, const void* x, int64_t rows, int64_t cols, int64_t ldx,
               int32_t dtype, void* out_ids);
 /* Every matmul of the forward: reference layers.py:208, 286, 293, 303, 306, 372, 373,
  * transformer_adapters.py:49, 93, 176. */
 int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* desc);
 /* Fused causal attention for q [B, Hq, Tq, D], k [B, Hkv, Lk, D], vt [B, Hkv, D, Lk] of which
- * the first seq_k keys are valid (Lk = kv_capacity, 0 meaning seq_k; a key/value cache
- * beyond seq_k must hold finite values): out[b, t, h*D + d] with row pitch ld_out, scores
+ * the first seq_k keys are valid (Lk = kv_capacity, 0 meaning seq_k; positions at or past
+ * seq_k may hold anything, NaN included: they are never read as scores or values, because
+ * the kernels zero what they load from there): out[b, t, h*D + d] with row pitch ld_out, scores
  * divided by `divisor`; query head h reads kv head h / (Hq / Hkv); query t sits at key
  * position t + offset. Replaces reference layers.py:293-304 (scores, mask, softmax, P.V,
  * head merge) in one kernel. */

@@ -27,7 +27,13 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
                    pinned pieces above; gemma_greedy ids are argmax of its own rows
   patchify         brute-force index loops (token i*(W/p1)+j, feature (a*p1+c2)*C+ch)
   vit_projector    brute-force loops over the same formula at a tiny shape
-  vit_forward      composition of pinned pieces; images are independent (batch split)
+  vit_forward      golden fixture tests/golden/vit_tiny.npz: brute-force float64 loops of
+                   the whole notebook ViT (patch order, projector, class/register rows,
+                   positions, unmasked blocks, LayerNorm, VitMLPHead on token 0, SiLU,
+                   Dense, softmax) written independently of this module; class scores and
+                   probabilities both compared; images are independent (batch split)
+  dense            brute-force float64 loops at a tiny shape with a non-zero bias
+  vit_head         brute-force loops reading token 0 (not another token) plus the bias
   mha              brute-force per-head loops in float64 (golden fixture); permutation
                    weights pin the head split/merge order
   embed_front      brute-force gather + add
@@ -218,7 +224,7 @@ def embed_back(x, table):
 
 
 def argmax(x):
-    """network.py:315, 338: xp.argmax(y_hat, axis=-1) (NumPy: first max, first NaN)."""
+    """network.py:135, 158: xp.argmax(y_hat, axis=-1) (NumPy: first max, first NaN)."""
     return np.argmax(x, axis=-1)
 
 
@@ -479,9 +485,10 @@ def vit_params(cfg, seed, scale=0.02, bf16=False):
     return out
 
 
-def vit_forward(x, params, cfg, bf16=False):
+def vit_forward(x, params, cfg, bf16=False, return_logits=False):
     """demo.ipynb cell 8 composition: projector -> encoder blocks (no mask) -> LayerNorm ->
-    class-token head (-> SiLU -> Dense when the head has a hidden layer) -> SoftMax."""
+    class-token head (-> SiLU -> Dense when the head has a hidden layer) -> SoftMax. With
+    return_logits, also the class scores the SoftMax reads."""
     rnd = round_bf16 if bf16 else None
     r = rnd or (lambda a: a)
     x = r(np.asarray(x, dtype=F32))
@@ -495,4 +502,5 @@ def vit_forward(x, params, cfg, bf16=False):
     if cfg.get("head_hidden"):
         y = r(silu(y))
         y = r(dense(y, params["dense.w"], params["dense.b"]))
-    return r(softmax(y))
+    probs = r(softmax(y))
+    return (probs, y) if return_logits else probs

@@ -41,6 +41,14 @@ def matvec(row, w, bias=None):
     return out
 
 
+def silu(v):
+    """reference activations.py:41-45, x (1 + tanh(x/2)) / 2, written here in its logistic
+    form x / (1 + exp(-x)) (the same function: (1 + tanh(x/2)) / 2 = 1 / (1 + exp(-x)))."""
+    if v < -700:
+        return 0.0
+    return v / (1.0 + math.exp(-v))
+
+
 def softmax_row(s, lim=None):
     lim = len(s) if lim is None else lim
     m = max(s[:lim])
@@ -49,8 +57,9 @@ def softmax_row(s, lim=None):
     return [v / t for v in e]
 
 
-def attention(x, wqkv, bqkv, wo, bo, H):
-    """reference layers.py:286-306 with the decoder mask (layers.py:254-256, 296)."""
+def attention(x, wqkv, bqkv, wo, bo, H, causal=True):
+    """reference layers.py:286-306; with `causal` the decoder mask (layers.py:254-256, 296),
+    without it every query attends to every key (the ViT encoder, decoder=False)."""
     T, C = len(x), len(x[0])
     D = C // H
     qkv = [matvec(x[t], wqkv, bqkv) for t in range(T)]
@@ -59,7 +68,7 @@ def attention(x, wqkv, bqkv, wo, bo, H):
         for i in range(T):
             s = [sum(qkv[i][h * D + d] * qkv[j][C + h * D + d] for d in range(D)) / math.sqrt(D)
                  for j in range(T)]
-            p = softmax_row(s, i + 1)
+            p = softmax_row(s, i + 1 if causal else T)
             for d in range(D):
                 heads[i][h * D + d] = sum(p[j] * qkv[j][2 * C + h * D + d] for j in range(T))
     return [matvec(heads[t], wo, bo) for t in range(T)]
@@ -107,6 +116,73 @@ def gpt_params(cfg, seed, scale=0.02):
     return P
 
 
+VIT_BLOCK_KEYS = ("g1", "be1", "wqkv", "bqkv", "wo", "bo", "g2", "be2", "w1", "bb1", "w2", "bb2")
+
+
+def vit_params(cfg, seed, scale):
+    """Seeded fill in layer.parameters order: VitProjector [projection, cls_reg_tokens,
+    positional_embeddings] (reference transformer_adapters.py:25-31), the encoder blocks
+    (layers.py:458), the final LayerNorm, VitMLPHead [W, b] (transformer_adapters.py:80-86)
+    and the head's Dense [W, b] (layers.py:200-204). N(0,1)*scale, +1 on LayerNorm gammas.
+    Returns the names in order and the arrays."""
+    C, H, W = cfg["image"]
+    p0, p1 = cfg["patch"]
+    d, R, F = cfg["d"], 1 + cfg["registers"], cfg["head_hidden"]
+    L = (H // p0) * (W // p1)
+    shapes = [("proj", (p0 * p1 * C, d)), ("cls", (R, d)), ("pos", (R + L, d))]
+    for l in range(cfg["layers"]):
+        shapes += [(f"b{l}.{k}", s) for k, s in zip(VIT_BLOCK_KEYS, [
+            (d,), (d,), (d, 3 * d), (3 * d,), (d, d), (d,), (d,), (d,), (d, 4 * d), (4 * d,),
+            (4 * d, d), (d,)])]
+    shapes += [("lnf.g", (d,)), ("lnf.be", (d,)), ("head.w", (d, F)), ("head.b", (F,)),
+               ("dense.w", (F, cfg["classes"])), ("dense.b", (cfg["classes"],))]
+    rng = np.random.default_rng(seed)
+    P = {}
+    for name, shape in shapes:
+        a = rng.standard_normal(shape, dtype=F32) * F32(scale)
+        if name.endswith(".g1") or name.endswith(".g2") or name == "lnf.g":
+            a = a + F32(1.0)
+        P[name] = a
+    return [n for n, _ in shapes], P
+
+
+def vit_brute(images, P, cfg):
+    """The notebook ViT classifier (demo.ipynb cell 8) in float64 loops: patch tokens in the
+    order of reference transformer_adapters.py:39-47 (token i * (W/p1) + j, feature
+    (row in patch * p1 + column in patch) * C + channel), projection without bias (:49),
+    class/register rows first (:51-52), positions added (:54), encoder blocks without a
+    mask (layers.py:463-467), final LayerNorm, VitMLPHead on token 0 (:89-95), SiLU, Dense
+    (layers.py:206-209), softmax. Returns (head output, class logits, probabilities)."""
+    C, H, W = cfg["image"]
+    p0, p1 = cfg["patch"]
+    nh, nw = H // p0, W // p1
+    R, heads = 1 + cfg["registers"], cfg["heads"]
+    head_all, logits_all, probs_all = [], [], []
+    for img in images:
+        toks = []
+        for i in range(nh):
+            for j in range(nw):
+                toks.append([img[ch][i * p0 + a][j * p1 + b]
+                             for a in range(p0) for b in range(p1) for ch in range(C)])
+        rows = [list(P["cls"][r]) for r in range(R)] + [matvec(t, P["proj"]) for t in toks]
+        x = [[v + P["pos"][t][c] for c, v in enumerate(row)] for t, row in enumerate(rows)]
+        for l in range(cfg["layers"]):
+            g = lambda k: P[f"b{l}.{k}"]
+            a = attention(ln_rows(x, g("g1"), g("be1")), g("wqkv"), g("bqkv"), g("wo"), g("bo"),
+                          heads, causal=False)
+            y = [[x[t][c] + a[t][c] for c in range(len(x[0]))] for t in range(len(x))]
+            h = [[silu(v) for v in matvec(r, g("w1"), g("bb1"))] for r in ln_rows(y, g("g2"), g("be2"))]
+            f = [matvec(r, g("w2"), g("bb2")) for r in h]
+            x = [[y[t][c] + f[t][c] for c in range(len(y[0]))] for t in range(len(y))]
+        x = ln_rows(x, P["lnf.g"], P["lnf.be"])
+        hd = matvec(x[0], P["head.w"], P["head.b"])
+        lg = matvec([silu(v) for v in hd], P["dense.w"], P["dense.b"])
+        head_all.append(hd)
+        logits_all.append(lg)
+        probs_all.append(softmax_row(lg))
+    return np.array(head_all), np.array(logits_all), np.array(probs_all)
+
+
 def main():
     # tiny GPT: scale 0.5 so that attention and GeLU are far from linear
     cfg = dict(vocab=11, ctx=6, layers=2, d=8, heads=2, act="gelu")
@@ -131,6 +207,19 @@ def main():
     p = np.array([[softmax_row(row.tolist(), i + 1) for i, row in enumerate(blk)]
                   for blk in s.astype(np.float64)])
     np.savez(os.path.join(HERE, "softmax_causal_small.npz"), scores=s, probs=p)
+
+    # tiny notebook-style ViT: non-square patches of a non-square image (so a transposed
+    # patch order fails), one register token, SiLU encoder, hidden SiLU head
+    vcfg = dict(image=(3, 4, 6), patch=(2, 3), d=8, heads=2, layers=2, act="silu",
+                registers=1, classes=5, head_hidden=6)
+    names, VP = vit_params(vcfg, seed=11, scale=0.5)
+    imgs = np.random.default_rng(12).standard_normal((3,) + vcfg["image"]).astype(F32)
+    head, logits, probs = vit_brute(imgs.astype(np.float64).tolist(),
+                                    {k: v.astype(np.float64).tolist() for k, v in VP.items()}, vcfg)
+    np.savez(os.path.join(HERE, "vit_tiny.npz"), images=imgs, head=head, logits=logits,
+             probs=probs, param_order=np.array(names),
+             **{"cfg_" + k: np.array(v) for k, v in vcfg.items()},
+             **{"p_" + k: v for k, v in VP.items()})
     print("fixtures written to", HERE)
 
 

@@ -168,3 +168,61 @@ def test_dtype_mapping():
     assert tl_hip.as_dtype("bf16") is tl_hip.bfloat16
     with pytest.raises(TypeError):
         tl_hip.as_dtype(np.complex64)
+
+
+SAN_LIB = os.path.join(PKG, "csrc", "_build", "san", "libtl_san.so")
+
+
+def _asan_runtime():
+    r = subprocess.run(["/opt/rocm/bin/hipcc", "-print-file-name=libclang_rt.asan-x86_64.so"],
+                       capture_output=True, text=True)
+    path = r.stdout.strip()
+    return path if r.returncode == 0 and os.path.isabs(path) and os.path.exists(path) else None
+
+
+def test_abi_host_paths_under_address_and_ub_sanitizers():
+    """Every exported entry point, called the way a binding could get it wrong (null context,
+    null pointers, zero sizes) and through the no-device path, in a host build instrumented
+    with ASan and UBSan: each returns a status with a message and no sanitizer reports."""
+    if not os.path.exists(SAN_LIB):
+        r = subprocess.run(["make", "-C", os.path.join(PKG, "csrc"), "san", "-j8"],
+                           capture_output=True, text=True, timeout=600)
+        if r.returncode != 0:
+            pytest.skip("sanitizer build unavailable: " + r.stderr[-500:])
+    rt = _asan_runtime()
+    if rt is None:
+        pytest.skip("clang ASan runtime not found")
+    code = (
+        "import ctypes, sys; sys.path.insert(0, %r)\n"
+        "import tl_hip\n"
+        "lib = tl_hip.load_library()\n"
+        "assert lib.tl_version() >= 1\n"
+        "n = ctypes.c_int(-1)\n"
+        "rc = lib.tl_device_count(ctypes.byref(n)); print('count', rc, n.value)\n"
+        "h = ctypes.c_void_p()\n"
+        "rc = lib.tl_init(0, ctypes.byref(h)); print('init', rc, lib.tl_last_error())\n"
+        "assert rc != 0 and lib.tl_last_error()\n"
+        "for name, argtypes in tl_hip.SIGNATURES.items():\n"
+        "    if name in ('tl_version', 'tl_last_error'):\n"
+        "        continue\n"
+        "    args = []\n"
+        "    for t in argtypes:\n"
+        "        if t is ctypes.c_void_p or hasattr(t, '_type_') and not isinstance(t._type_, str):\n"
+        "            args.append(None)\n"
+        "        elif t in (ctypes.c_float, ctypes.c_double):\n"
+        "            args.append(0.0)\n"
+        "        else:\n"
+        "            args.append(0)\n"
+        "    rc = getattr(lib, name)(*args)\n"
+        "    assert 0 <= rc <= 6, (name, rc)\n"
+        "    if name != 'tl_event_destroy':\n"
+        "        assert rc != 0 and lib.tl_last_error(), name\n"
+        "print('SAN_OK')\n" % PKG)
+    env = dict(os.environ, TL_LIBRARY=SAN_LIB, LD_PRELOAD=rt,
+               ASAN_OPTIONS="detect_leaks=0:abort_on_error=1",
+               UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                       env=env)
+    out = r.stdout + r.stderr
+    assert r.returncode == 0 and "SAN_OK" in r.stdout, out[-3000:]
+    assert "AddressSanitizer" not in out and "runtime error" not in out, out[-3000:]

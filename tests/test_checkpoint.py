@@ -88,3 +88,72 @@ def test_files_that_need_unpickling_or_lack_a_layout_are_refused(tmp_path):
     np.savez(bare, x=np.zeros(3, np.float32))
     with pytest.raises(ValueError, match="not a"):
         checkpoint.load_weights(FakeModel(0), bare)
+
+
+def test_array_mismatch_behind_a_matching_layout_is_refused_before_any_write(tmp_path):
+    """The JSON layout matches the model but the last array does not: nothing is written."""
+    path = str(tmp_path / "w.npz")
+    checkpoint.save_weights(FakeModel(0), path)
+    with np.load(path, allow_pickle=False) as z:
+        arrays = {k: z[k] for k in z.files}
+    for bad in (arrays["L0002.P01"].astype(np.float64), arrays["L0002.P01"][:-1]):
+        arrays["L0002.P01"] = bad
+        np.savez(path, **arrays)
+        other = FakeModel(1)
+        before = [p.copy() for p in params(other)]
+        with pytest.raises(ValueError, match="L2.P1"):
+            checkpoint.load_weights(other, path)
+        for x, y in zip(before, params(other)):
+            assert np.array_equal(x, y)
+
+
+def _notebook_save(model, path, protocol):
+    """What the notebook's save_weights writes (reference demo.ipynb cell 17): a pickled
+    list of {"name", "parameters"} records holding host arrays."""
+    import pickle
+    lst = [{"name": type(layer).__name__, "parameters": [p.get() for p in layer.parameters]}
+           for layer in model.layers]
+    with open(path, "wb") as f:
+        pickle.dump(lst, f, protocol=protocol)
+
+
+@pytest.mark.parametrize("protocol", [2, 4, 5])
+def test_notebook_pickle_is_read_in_layer_order(tmp_path, protocol):
+    a, b = FakeModel(0), FakeModel(1)
+    path = str(tmp_path / "nb.pkl")
+    _notebook_save(a, path, protocol)
+    assert checkpoint.load_notebook_weights(b, path) is b
+    for x, y in zip(params(a), params(b)):
+        assert np.array_equal(x, y)
+
+
+def test_notebook_pickle_naming_other_globals_is_refused(tmp_path):
+    """A pickle that would call anything but NumPy's array reconstruction stops at the
+    lookup, before the call (the payload here is a harmless print)."""
+    import pickle
+
+    class Payload:
+        def __reduce__(self):
+            return (print, ("called",))
+
+    path = str(tmp_path / "evil.pkl")
+    with open(path, "wb") as f:
+        pickle.dump([{"name": "Dense", "parameters": [Payload()]}], f)
+    with pytest.raises(pickle.UnpicklingError, match="builtins.print"):
+        checkpoint.read_notebook_weights(path)
+    obj = str(tmp_path / "obj.pkl")
+    with open(obj, "wb") as f:
+        pickle.dump([{"name": "Dense", "parameters": [np.array([1, "a"], dtype=object)]}], f)
+    with pytest.raises((pickle.UnpicklingError, ValueError)):
+        checkpoint.load_notebook_weights(FakeModel(0), obj)
+
+
+def test_notebook_pickle_with_wrong_layout_is_refused_before_any_write(tmp_path):
+    path = str(tmp_path / "nb.pkl")
+    _notebook_save(FakeModel(0, widths=(8, 12)), path, 4)
+    other = FakeModel(1)
+    before = [p.copy() for p in params(other)]
+    with pytest.raises(ValueError, match="shape"):
+        checkpoint.load_notebook_weights(other, path)
+    for x, y in zip(before, params(other)):
+        assert np.array_equal(x, y)

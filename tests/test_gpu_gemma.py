@@ -303,18 +303,40 @@ def test_gemma_full_width_one_layer_bf16(tl):
     assert np.array_equal(tl["xp"].argmax(model.back.output).get(), np.argmax(got, -1))
 
 
+def test_gemma_full_width_four_layers_prefill_and_decode_bf16(tl):
+    """Config 5 widths with four layers, device-seeded N(0, 0.02) weights: the prefill's last
+    row and three cached greedy decode steps (skinny GEMMs, split-KV decode attention, RoPE
+    at positions past the prompt) against the oracle recomputing the window on the same
+    tokens."""
+    g = tl["gemma"]
+    cfg = dict(g.GEMMA_2B, layers=4)
+    model = g.build_gemma(cfg, "bf16")
+    g.seed_gemma(model, 25, 0.02, device=True)
+    ids = np.random.default_rng(26).integers(0, cfg["vocab"], (2, 64))
+    new, rows = model.generate_greedy(ids, 4, return_logits=True)
+    assert np.array_equal(new, np.argmax(rows, -1).T)
+    P = _device_params(model, cfg)
+    seq = np.concatenate([ids, new], axis=1)
+    full = ref.gemma_forward(seq[:, :-1], P, cfg, bf16=True)  # [2, 67, V]
+    want_rows = full[:, 63:, :].transpose(1, 0, 2)  # step t reads position 63 + t
+    for t in range(4):
+        assert ref.max_rel(rows[t], want_rows[t]) <= 2e-2, t
+
+
 def test_gemma_config5_full_shape_decode_bf16(tl):
     """BASELINE config 5 at full size: 18 layers, 2.5B device-seeded bf16 weights, prefill
-    B=4, T=2048 into the KV cache, then greedy steps. Every cached step's logits equal the
-    last row of a fresh prefill over the same tokens, and the ids are the device argmax of
-    those rows. (The whole model is beyond the CPU oracle; its layers are pinned above.)"""
+    B=4, T=2048 into the KV cache, then all 128 greedy steps (cache positions 2048-2174).
+    The cached logits of steps 32, 64 and 127 equal the last row of a fresh prefill over the
+    same tokens, and the ids are the device argmax of every step's row. (The whole model is
+    beyond the CPU oracle; four full-width layers are checked against it above.)"""
     g = tl["gemma"]
     model = g.build_gemma(g.GEMMA_2B, "bf16")
     g.seed_gemma(model, 23, 0.02, device=True)
     ids = np.random.default_rng(24).integers(0, 256000, (4, 2048))
-    new, rows = model.generate_greedy(ids, 4, return_logits=True)
-    assert new.shape == (4, 4) and np.array_equal(new, np.argmax(rows, -1).T)
+    new, rows = model.generate_greedy(ids, 128, return_logits=True)
+    assert new.shape == (4, 128) and np.array_equal(new, np.argmax(rows, -1).T)
     assert np.all(np.isfinite(rows))
     seq = np.concatenate([ids, new], axis=1)
-    fresh = model.last_rows(model.forward(seq[:, :2051])).get()
-    assert ref.max_rel(rows[3], fresh) <= 2e-2
+    for t in (32, 64, 127):
+        fresh = model.last_rows(model.forward(seq[:, :2048 + t])).get()
+        assert ref.max_rel(rows[t], fresh) <= 2e-2, t

@@ -202,6 +202,43 @@ def test_softmax_many_rows(xp, dt, rows, cols, causal, period, offset):
     assert np.all(y[~keep] == 0)
 
 
+def _row_rel(got, want):
+    """Largest per-row max |diff| / max |ref| (each row against its own scale)."""
+    got = got.reshape(-1, got.shape[-1]).astype(np.float64)
+    want = want.reshape(-1, want.shape[-1]).astype(np.float64)
+    den = np.maximum(np.max(np.abs(want), axis=1), 1e-30)
+    return float(np.max(np.max(np.abs(got - want), axis=1) / den))
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_config2_norms_exact_shape(xp, dt):
+    """BASELINE config 2's norm tensors exactly: [16384, 4096], inputs N(0,1) from a seed,
+    gamma and beta N(0,1); every row checked against the oracle on its own scale."""
+    rng = np.random.default_rng(16384)
+    x = rnd(dt, rng.standard_normal((16384, 4096), dtype=F32))
+    g = rnd(dt, rng.standard_normal(4096, dtype=F32))
+    b = rnd(dt, rng.standard_normal(4096, dtype=F32))
+    xd = up(xp, x, dt)
+    y = xp.layernorm(xd, up(xp, g, dt), up(xp, b, dt), F32(1e-5)).get()
+    assert _row_rel(y, rnd(dt, ref.layernorm(x, g, b))) <= TOL[dt], dt
+    del y
+    y = xp.rmsnorm(xd, up(xp, g, dt), F32(1e-6), 0.0).get()
+    assert _row_rel(y, rnd(dt, ref.rmsnorm(x, g, F32(1e-6), 0.0))) <= TOL[dt], dt
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_config2_causal_softmax_exact_shape(xp, dt):
+    """BASELINE config 2's attention scores exactly: [8, 12, 1024, 1024], N(0,1) from a seed,
+    causal; every row checked against the oracle on its own scale, every masked entry 0."""
+    T = 1024
+    s = rnd(dt, np.random.default_rng(1024).standard_normal((8, 12, T, T), dtype=F32))
+    y = xp.softmax(up(xp, s, dt), causal=True, period=T, offset=0).get()
+    want = ref.softmax(s + ref.causal_mask(T))
+    assert _row_rel(y, rnd(dt, want)) <= TOL[dt], dt
+    iu = np.triu_indices(T, 1)
+    assert np.all(y[..., iu[0], iu[1]] == 0)
+
+
 def test_softmax_causal_golden(xp):
     import os
     z = np.load(os.path.join(os.path.dirname(__file__), "golden", "softmax_causal_small.npz"))

@@ -140,6 +140,31 @@ def test_dense_and_vit_head(tl, dt):
     assert ref.max_rel(yv, ref.vit_head(xv, w, b)) <= tol
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_weight_written_through_a_view_is_repacked(tl, dt):
+    """The GEMM reads a packed [N, K] copy of a weight for large products (fp32 with >= 128
+    tiles of 128x128, bf16 always). Writing the weight through another view of its buffer,
+    or as a kernel's output operand, must make the next forward use the new values."""
+    xp = tl["xp"]
+    tl["backend"].set_float_type(dt)
+    rnd = ref.round_bf16 if dt == "bf16" else (lambda a: a)
+    tol = 1e-5 if dt == "fp32" else 2e-2
+    d = tl["layers"].Dense(256, 512)
+    rng = np.random.default_rng(77)
+    d.bias.set(np.zeros(512, F32))
+    x = rnd(rng.standard_normal((4096, 256)).astype(F32))
+    xd = xp.array(x, dtype=dt)
+    w0 = rnd(rng.standard_normal((256, 512)).astype(F32) * F32(0.1))
+    d.weights.set(w0)
+    assert ref.max_rel(d.forward(xd).get(), x @ w0) <= tol
+    w1 = rnd(rng.standard_normal((256, 512)).astype(F32) * F32(0.1))
+    d.weights.reshape(-1).set(w1.reshape(-1))  # a different DeviceTensor over the same buffer
+    assert ref.max_rel(d.forward(xd).get(), x @ w1) <= tol
+    w2t = rnd(rng.standard_normal((512, 256)).astype(F32) * F32(0.1))
+    xp.transpose2d(xp.array(w2t, dtype=dt), out=d.weights, out_offset=0, ldy=512)
+    assert ref.max_rel(d.forward(xd).get(), x @ w2t.T) <= tol
+
+
 def test_gpt2_small_shape_bf16_short(tl):
     """BASELINE config 3 model (vocab 50257, 12 layers, d 768, 12 heads) at B=2, T=128."""
     cfg = dict(vocab=50257, ctx=1024, layers=12, d=768, heads=12, act="gelu")
@@ -155,8 +180,9 @@ def test_gpt2_small_shape_bf16_short(tl):
 
 def test_gpt2_small_full_shape_bf16(tl):
     """BASELINE config 3 at its full size, B=8, T=1024: size-independent properties over the
-    whole batch, oracle parity on sequence 0 (causal rows of one sequence depend only on
-    that sequence), and batch independence of sequence 0."""
+    whole batch, oracle parity on sequences 0 and 7 (causal rows of one sequence depend only
+    on that sequence, so the first and last batch entries pin the batch strides), and every
+    sequence run alone equals its row of the batched run."""
     cfg = dict(vocab=50257, ctx=1024, layers=12, d=768, heads=12, act="gelu")
     ids = np.random.default_rng(6).integers(0, 50257, (8, 1024))
     net, probs, logits = run_gpt(tl, cfg, ids, "bf16", seed=1)
@@ -168,13 +194,38 @@ def test_gpt2_small_full_shape_bf16(tl):
     # softmax is monotone: the most likely token is the largest logit (up to bf16 ties)
     agree = np.mean(ids_logits == ids_probs)
     assert agree > 0.99, agree
-    l0 = logits.get()[0]
-    want_p, want_l = ref.gpt_forward(ids[:1], ref.gpt_params(cfg, 1, bf16=True), cfg, bf16=True,
-                                     return_logits=True)
-    assert ref.max_rel(l0, want_l[0]) <= 2e-2
-    probs1 = net.predict(ids[:1])
-    l1 = net.layers[-2].output.get()[0]
-    assert ref.max_rel(l1, l0) <= 1e-6
+    full = logits.get()
+    want_p, want_l = ref.gpt_forward(ids[[0, 7]], ref.gpt_params(cfg, 1, bf16=True), cfg,
+                                     bf16=True, return_logits=True)
+    assert ref.max_rel(full[0], want_l[0]) <= 2e-2
+    assert ref.max_rel(full[7], want_l[1]) <= 2e-2
+    for b in range(8):
+        net.predict(ids[b:b + 1])
+        alone = net.layers[-2].output.get()[0]
+        assert ref.max_rel(alone, full[b]) <= 1e-6, b
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_embed_front_sinusoidal_positions(tl, dt):
+    """GPTEmbedFront's sinusoidal branch (reference transformer_adapters.py:128-135, 148-153):
+    table[ids] + the closed-form position table, one rounding of the sum in bf16, bit-exact."""
+    tl["backend"].set_float_type(dt)
+    V, ctx, C = 37, 50, 24
+    table = tl["ta"].GPTEmbeddingTable(V, C)
+    front = tl["ta"].GPTEmbedFront(table, ctx, positional_embedding="sinusoidal")
+    assert front.parameters == [table.table]  # no trainable positions in this branch
+    rng = np.random.default_rng(31)
+    tab = rng.standard_normal((V, C)).astype(F32)
+    tab = ref.round_bf16(tab) if dt == "bf16" else tab
+    table.table.set(tab)
+    ids = rng.integers(0, V, (3, 41))
+    got = front.forward(ids).get()
+    pos = ref.sinusoidal_positions(ctx, C)
+    if dt == "bf16":
+        want = ref.round_bf16(ref.embed_front(ids, tab, ref.round_bf16(pos)))
+    else:
+        want = ref.embed_front(ids, tab, pos)
+    assert np.array_equal(got, want)
 
 
 def test_sequence_longer_than_context_is_rejected(tl):

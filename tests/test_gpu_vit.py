@@ -116,6 +116,30 @@ def test_tiny_notebook_vit_fp32(tl):
     assert np.array_equal(tl["xp"].argmax(probs).get(), np.argmax(got, -1))
 
 
+def test_vit_golden_fixture_fp32(tl):
+    """The notebook ViT composition against tests/golden/vit_tiny.npz (brute-force float64
+    loops, independent of the oracle): non-square patches of a non-square image, a register
+    token, SiLU blocks, a hidden SiLU head. Head output, class scores and probabilities."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vit_tiny.npz"))
+    cfg = {k[4:]: z[k] for k in z.files if k.startswith("cfg_")}
+    cfg = {k: (tuple(int(a) for a in v) if v.ndim else (str(v) if v.dtype.kind == "U" else int(v)))
+           for k, v in cfg.items()}
+    net = tl["vit"].build_vit(cfg, "fp32")
+    params = [p for layer in net.layers for p in layer.parameters]
+    names = [str(n) for n in z["param_order"]]
+    assert len(params) == len(names)
+    for p, n in zip(params, names):
+        p.set(z["p_" + n])
+    probs = net.predict(z["images"])
+    head = net.layers[-5].output.get()   # VitMLPHead
+    logits = net.layers[-2].output.get()  # Dense
+    assert ref.max_rel(head, z["head"]) <= 1e-5
+    assert ref.max_rel(logits, z["logits"]) <= 1e-5
+    assert ref.max_rel(probs.get(), z["probs"]) <= 1e-5
+    assert np.array_equal(tl["xp"].argmax(probs).get(), np.argmax(z["probs"], -1))
+
+
 def _cifar_like(rng, n):
     """Pixels uniform in [0, 1], normalised per channel as (x - 0.5) / sqrt(1/12)."""
     x = rng.random((n, 3, 32, 32), dtype=F32)
@@ -125,7 +149,9 @@ def _cifar_like(rng, n):
 def test_vit_config4_full_shape_bf16(tl):
     """BASELINE config 4 at its full size (B=512, 65 tokens, d 384, 6 heads, 8 layers,
     10 classes, bf16): rows are probability vectors, images are independent of the rest of
-    the batch, and sampled images match the oracle."""
+    the batch, and sampled images (first, middle and last) match the oracle on the head's
+    class scores (before the softmax, which would compress their error) and on the
+    probabilities."""
     cfg = tl["vit"].VIT_S4
     net = tl["vit"].build_vit(cfg, "bf16")
     tl["vit"].seed_vit(net, 5, 0.02)
@@ -133,12 +159,15 @@ def test_vit_config4_full_shape_bf16(tl):
     xp = tl["xp"]
     probs_dev = net.predict(xp.array(x, dtype="bf16"))
     probs = probs_dev.get()
-    assert probs.shape == (512, 10)
+    scores = net.layers[-2].output.get()  # VitMLPHead output, [512, 10]
+    assert probs.shape == (512, 10) and scores.shape == (512, 10)
     assert np.array_equal(xp.argmax(probs_dev).get(), np.argmax(probs, -1))
     np.testing.assert_allclose(probs.astype(np.float64).sum(-1), 1.0, rtol=2e-2)
     P = ref.vit_params(cfg, 5, 0.02, bf16=True)
-    idx = [0, 1, 255, 511]
-    want = ref.vit_forward(x[idx], P, cfg, bf16=True)
-    assert ref.max_rel(probs[idx], want) <= 2e-2
+    idx = [0, 1, 255, 510, 511]
+    want_p, want_s = ref.vit_forward(x[idx], P, cfg, bf16=True, return_logits=True)
+    assert ref.max_rel(scores[idx], want_s) <= 2e-2
+    assert ref.max_rel(probs[idx], want_p) <= 2e-2
     sub = net.predict(xp.array(x[idx], dtype="bf16")).get()
-    assert ref.max_rel(sub, probs[idx]) <= 1e-2  # other tile shapes at 4 images
+    assert ref.max_rel(sub, probs[idx]) <= 1e-2  # other tile shapes at 5 images
+    assert ref.max_rel(net.layers[-2].output.get(), scores[idx]) <= 2e-2

@@ -422,3 +422,34 @@ def test_vit_forward_images_are_independent():
     assert ref.max_rel(ref.vit_forward(x[1:2], P, cfg), full[1:2]) < 1e-5
     names = [n for n, _ in ref.vit_param_shapes(cfg)]
     assert names[:3] == ["proj", "cls", "pos"] and names[-4:] == ["head.w", "head.b", "dense.w", "dense.b"]
+
+
+def test_dense_brute_force():
+    """reference layers.py:206-209: y = x @ W + b over the last axis of any leading shape."""
+    rng = np.random.default_rng(43)
+    x = rng.standard_normal((2, 3, 5)).astype(F32)
+    w = rng.standard_normal((5, 4)).astype(F32)
+    b = rng.standard_normal(4).astype(F32) * 3  # a bias large enough that dropping it fails
+    got = ref.dense(x, w, b)
+    assert got.shape == (2, 3, 4)
+    for i in range(2):
+        for j in range(3):
+            for o in range(4):
+                want = sum(float(x[i, j, k]) * float(w[k, o]) for k in range(5)) + float(b[o])
+                assert abs(float(got[i, j, o]) - want) < 1e-5 * (1 + abs(want))
+
+
+def test_vit_head_brute_force():
+    """reference transformer_adapters.py:89-95: the class token (token 0) @ W + b."""
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((3, 4, 5)).astype(F32)
+    w = rng.standard_normal((5, 2)).astype(F32)
+    b = rng.standard_normal(2).astype(F32) * 3
+    got = ref.vit_head(x, w, b)
+    assert got.shape == (3, 2)
+    for n in range(3):
+        for o in range(2):
+            want = sum(float(x[n, 0, k]) * float(w[k, o]) for k in range(5)) + float(b[o])
+            assert abs(float(got[n, o]) - want) < 1e-5 * (1 + abs(want))
+            other = sum(float(x[n, 1, k]) * float(w[k, o]) for k in range(5)) + float(b[o])
+            assert abs(float(got[n, o]) - other) > 1e-3  # a wrong token index would fail

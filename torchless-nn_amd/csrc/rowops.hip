@@ -747,7 +747,7 @@ __global__ __launch_bounds__(256) void act_kernel(const T* __restrict__ x, T* __
 }
 
 // ------------------------------------------------------------------------------------
-// argmax (reference network.py:315, 338: xp.argmax(axis=-1), first index on ties)
+// argmax (reference network.py:135, 158: xp.argmax(axis=-1), first index on ties)
 // ------------------------------------------------------------------------------------
 // True when (va, ia) should win over (vb, ib): NaN beats everything (NumPy returns the
 // first NaN), then larger value, then smaller index.

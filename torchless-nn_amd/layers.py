@@ -10,9 +10,12 @@ reference; every forward is a handful of libtl kernel launches on one HIP stream
                                the causal softmax row kernel and the batched P.V GEMM
   LayerNorm / RMSNorm       -> one row kernel each
 
-bf16 weights are used by the MFMA GEMM in a K-contiguous copy ([out, in]) that is packed
-on the device the first time a weight is used and again whenever it is modified; fp32
-weights are read in place by the fp32 GEMM.
+The MFMA GEMMs read a weight in a K-contiguous copy ([out, in]) that is packed on the
+device the first time the weight is used and again after its buffer has been written (by
+`set`, `fill` or any kernel writing into any view of it). bf16 weights always take that copy;
+fp32 weights take it for products the fp32 matrix-core kernel runs (K % 4 == 0 and at least
+128 output tiles of 128x128), which doubles their HBM use, and are read in place by the fp32
+VALU GEMM otherwise.
 """
 import numpy as np
 

@@ -1,4 +1,4 @@
-"""Inference driver (reference network.py:208-219, 325-340)."""
+"""Inference driver (reference network.py:28-49: Network, predict/_forward, set_eval)."""
 import tl_hip as xp
 from utils import Layer
 
@@ -24,7 +24,7 @@ class Network:
 
     def predict_ids(self, input):
         """argmax over the last axis of predict(input), as int64 on the device (the
-        reference's `xp.argmax(y_hat, axis=-1)`, network.py:315, 338)."""
+        reference's `xp.argmax(y_hat, axis=-1)`, network.py:135, 158)."""
         return xp.argmax(self.predict(input), axis=-1)
 
     def train(self, *args, **kwargs):

@@ -268,13 +268,15 @@ def synchronize():
 
 # ---- device memory --------------------------------------------------------------------
 class DeviceBuffer:
-    __slots__ = ("ptr", "nbytes", "_ctx", "__weakref__")
+    """One tl_malloc allocation. `version` counts the writes made into it through this
+    module (by any view of it), so data derived from its contents can tell it is stale."""
+    __slots__ = ("ptr", "nbytes", "_ctx", "version", "__weakref__")
 
     def __init__(self, nbytes: int):
         c = ctx()
         p = ctypes.c_void_p()
         check(c.lib.tl_malloc(c.handle, int(nbytes), ctypes.byref(p)))
-        self.ptr, self.nbytes, self._ctx = p.value, int(nbytes), c
+        self.ptr, self.nbytes, self._ctx, self.version = p.value, int(nbytes), c, 0
 
     def __del__(self):
         try:
@@ -303,7 +305,7 @@ class DeviceTensor:
     rows of the last dimension. Rows are padded only where a kernel benefits (e.g. the
     50257-wide logits use a pitch that keeps every row 16-byte aligned)."""
 
-    __slots__ = ("shape", "dtype", "pitch", "buf", "offset", "_version", "_aux", "__weakref__")
+    __slots__ = ("shape", "dtype", "pitch", "buf", "offset", "_aux", "__weakref__")
 
     def __init__(self, shape, dtype, pitch=None, buf=None, offset=0):
         self.shape = _norm_shape(shape)
@@ -320,8 +322,18 @@ class DeviceTensor:
             if int(offset) < 0 or end > buf.nbytes:
                 raise ValueError(f"view of {end - int(offset)} bytes at offset {int(offset)} "
                                  f"exceeds its {buf.nbytes}-byte buffer")
-        self.buf, self.offset, self._version = buf, int(offset), 0
+        self.buf, self.offset = buf, int(offset)
         self._aux = None  # device-side derived data (e.g. a packed weight), by _version
+
+    @property
+    def _version(self) -> int:
+        """Write count of the underlying buffer: it changes whenever any view of the buffer
+        is written through this module (set, fill, or a kernel's out= / C= operand)."""
+        return self.buf.version
+
+    @_version.setter
+    def _version(self, value):
+        self.buf.version = int(value)
 
     # -- geometry
     @property
@@ -442,6 +454,13 @@ class DeviceTensor:
         return out
 
 
+def _wrote(*tensors):
+    """Record a write into each given tensor's buffer (None entries are skipped)."""
+    for t in tensors:
+        if t is not None:
+            t.buf.version += 1
+
+
 def _to_host_raw(host: np.ndarray, dtype: DType) -> np.ndarray:
     if dtype is bfloat16:
         return f32_to_bf16_bits(np.asarray(host, dtype=np.float32))
@@ -480,7 +499,7 @@ def asnumpy(t) -> np.ndarray:
 
 
 def argmax(t: DeviceTensor, axis=-1) -> DeviceTensor:
-    """First index of the maximum along the last axis, int64 (reference network.py:315)."""
+    """First index of the maximum along the last axis, int64 (reference network.py:135, 158)."""
     if axis not in (-1, t.ndim - 1):
         raise NotImplementedError("argmax is implemented over the last axis")
     out = DeviceTensor(t.shape[:-1] if t.ndim > 1 else (1,), int64)
@@ -555,6 +574,10 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
                   KFAMILY[family], GEMM_TILES[tile])
     lib_, h = _c()
     check(lib_.tl_gemm(h, ctypes.byref(d)))
+    if qkv is not None:
+        _wrote(qkv[0], qkv[1], qkv[2])
+    else:
+        _wrote(C)
 
 
 def layernorm(x: DeviceTensor, gamma, beta, eps, out=None):
@@ -562,6 +585,7 @@ def layernorm(x: DeviceTensor, gamma, beta, eps, out=None):
     lib_, h = _c()
     check(lib_.tl_layernorm_fwd(h, x.ptr, gamma.ptr, beta.ptr, out.ptr, x.nrows, x.ncols,
                                 x.pitch, out.pitch, float(eps), x.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -570,6 +594,7 @@ def rmsnorm(x: DeviceTensor, gamma, eps, gamma_offset=0.0, out=None):
     lib_, h = _c()
     check(lib_.tl_rmsnorm_fwd(h, x.ptr, gamma.ptr, out.ptr, x.nrows, x.ncols, x.pitch,
                               out.pitch, float(eps), float(gamma_offset), x.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -579,6 +604,7 @@ def softmax(x: DeviceTensor, temperature=1.0, causal=False, period=1, offset=0, 
     check(lib_.tl_softmax_fwd(h, x.ptr, out.ptr, x.nrows, x.ncols, x.pitch, out.pitch,
                               float(temperature), int(bool(causal)), int(period), int(offset),
                               x.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -609,6 +635,7 @@ def rope(x: DeviceTensor, table: DeviceTensor, out=None, seq_len=None, n_seq=Non
                                  f"the end of its buffer")
     lib_, h = _c()
     check(lib_.tl_rope_fwd(h, x.ptr, out.ptr, table.ptr, n, T, D, stride, x.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -639,8 +666,7 @@ def rope2(x1: DeviceTensor, x2: DeviceTensor, table: DeviceTensor, seq_len, n_se
     lib_, h = _c()
     check(lib_.tl_rope2_fwd(h, x1.ptr, x1.ptr, n1, st1, x2.ptr, x2.ptr, n2, st2, table.ptr, T, D,
                             x1.dtype.code))
-    x1._version += 1
-    x2._version += 1
+    _wrote(x1, x2)
     return x1, x2
 
 
@@ -650,6 +676,7 @@ def activation(x: DeviceTensor, act: int, out=None):
     out = out if out is not None else DeviceTensor(x.shape, x.dtype)
     lib_, h = _c()
     check(lib_.tl_act_fwd(h, x.ptr, out.ptr, x.size, int(act), x.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -667,6 +694,7 @@ def embed(ids: DeviceTensor, table: DeviceTensor, pos, seq_len, pos0=0, out_shap
     check(lib_.tl_embed_fwd(h, ids.ptr, ids.dtype.code, table.ptr,
                             pos.ptr if pos is not None else None, out.ptr, ids.size, seq_len,
                             pos0, V, C, ld_out, float(scale), table.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -696,6 +724,7 @@ def attention(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTen
     check(lib_.tl_attention_fwd(h, q.ptr, k.ptr, vt.ptr, out.ptr, B, n_heads_q, n_heads_kv, Tq,
                                 Tk, D, out.pitch, int(offset), float(divisor), int(bool(causal)),
                                 Lk, q.dtype.code))
+    _wrote(out)
     return out
 
 
@@ -717,6 +746,7 @@ def transpose2d(x: DeviceTensor, out=None, out_offset=0, ldy=None) -> DeviceTens
         ptr, ld = out.ptr + out_offset * x.dtype.itemsize, ldy
     lib_, h = _c()
     check(lib_.tl_transpose2d(h, x.ptr, ptr, r, c_, x.pitch, ld, x.dtype.code))
+    _wrote(out)
     return out
 
 
