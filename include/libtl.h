@@ -261,6 +261,19 @@ int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, 
                      int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                      int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
                      float divisor, int32_t causal, int64_t kv_capacity, int32_t dtype);
+/* tl_attention_fwd that allocates nothing: the same arguments, kernels and results, with the
+ * decode path's partial results (at most 16 query rows per kv head) kept in a static device
+ * array of 16 MiB instead of the context's grow-only workspace, and the launch kept out of the
+ * event profiler. No counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). A
+ * call whose partials need more than 16 MiB (batch x kv heads x key blocks of 64 keys, each
+ * 16 x (head_dim + 2) floats) fails with TL_ERR_INVALID. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (two contexts or two host threads) race. */
+int tl_attention_fwd_noalloc(tl_ctx* ctx, const void* q, const void* k, const void* vt,
+                             void* out, int64_t batch, int64_t n_heads_q, int64_t n_heads_kv,
+                             int64_t seq_q, int64_t seq_k, int64_t head_dim, int64_t ld_out,
+                             int64_t offset, float divisor, int32_t causal,
+                             int64_t kv_capacity, int32_t dtype);
 
 #ifdef __cplusplus
 }

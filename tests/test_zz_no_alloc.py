@@ -1,0 +1,88 @@
+"""tl_attention_fwd_noalloc (the allocation-free variant of tl_attention_fwd) through the C
+ABI: on the decode path its results equal tl_attention_fwd's bit for bit on two calls in a
+row, the second smaller (the static scratch keeps the first call's contents); the prefill
+path agrees too; a call whose partials exceed the static scratch is refused."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def xp():
+    import tl_hip
+    tl_hip.ctx()
+    return tl_hip
+
+
+def _operands(xp, rng, B, Hq, Hkv, Tq, Tk, L, D):
+    def dev(shape, scale):
+        return xp.array(ref.round_bf16(rng.standard_normal(shape).astype(np.float32) * scale),
+                        dtype="bf16")
+    q = dev((B, Hq, Tq, D), 1.0)
+    k = dev((B, Hkv, L, D), 1.0)
+    vt = dev((B, Hkv, D, L), 1.0)
+    return q, k, vt
+
+
+def _run(xp, fn, q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, offset):
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    out.fill(7.0)
+    c = xp.ctx()
+    rc = getattr(c.lib, fn)(c.handle, q.ptr, k.ptr, vt.ptr, out.ptr, B, Hq, Hkv, Tq, Tk, D,
+                            out.pitch, offset, float(np.float32(D ** 0.5)), 1, L,
+                            xp.bfloat16.code)
+    assert rc == 0, (fn, rc, xp.last_error())
+    return out.get_raw()
+
+
+# (B, Hq, Hkv, Tq, Tk, L, D): the config-5 decode step first, then a smaller call
+CASES = [(4, 8, 1, 1, 2176, 2176, 256), (2, 4, 1, 1, 300, 304, 128)]
+
+
+def test_noalloc_decode_matches_allocating_entry_point_twice(xp):
+    rng = np.random.default_rng(2024)
+    for B, Hq, Hkv, Tq, Tk, L, D in CASES:
+        print(f"noalloc decode case B={B} Hq={Hq} Hkv={Hkv} Tq={Tq} Tk={Tk} L={L} D={D}", flush=True)
+        q, k, vt = _operands(xp, rng, B, Hq, Hkv, Tq, Tk, L, D)
+        off = Tk - Tq
+        want = _run(xp, "tl_attention_fwd", q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, off)
+        got = _run(xp, "tl_attention_fwd_noalloc", q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, off)
+        assert np.array_equal(got, want)
+        # and both agree with the float64 definition
+        qf, kf, vf = (xp.bf16_bits_to_f32(t.get_raw()).reshape(t.shape) for t in (q, k, vt))
+        s = np.einsum("bhtd,bkd->bhtk", qf.astype(np.float64), kf[:, 0, :Tk].astype(np.float64))
+        s /= np.sqrt(D)
+        p = np.exp(s - s.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+        o = np.einsum("bhtk,bdk->bthd", p, vf[:, 0, :, :Tk].astype(np.float64)).reshape(B, Tq, Hq * D)
+        assert ref.max_rel(xp.bf16_bits_to_f32(got).reshape(o.shape), o) <= 2e-2
+    xp.synchronize()
+
+
+def test_noalloc_prefill_matches(xp):
+    B, Hq, Hkv, Tq, Tk, L, D = 2, 4, 2, 130, 130, 136, 64
+    rng = np.random.default_rng(7)
+    q, k, vt = _operands(xp, rng, B, Hq, Hkv, Tq, Tk, L, D)
+    want = _run(xp, "tl_attention_fwd", q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, 0)
+    got = _run(xp, "tl_attention_fwd_noalloc", q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, 0)
+    assert np.array_equal(got, want)
+
+
+def test_noalloc_rejects_partials_beyond_its_scratch(xp):
+    # 64 x 1 kv heads x 34 blocks of 64 keys x 16 x (256 + 2) floats > 16 MiB
+    B, Hq, Hkv, Tq, Tk, L, D = 64, 8, 1, 1, 2176, 2176, 256
+    q = xp.empty((B, Hq, Tq, D), "bf16")
+    k = xp.empty((B, Hkv, L, D), "bf16")
+    vt = xp.empty((B, Hkv, D, L), "bf16")
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    c = xp.ctx()
+    rc = c.lib.tl_attention_fwd_noalloc(c.handle, q.ptr, k.ptr, vt.ptr, out.ptr, B, Hq, Hkv, Tq,
+                                        Tk, D, out.pitch, Tk - 1, 16.0, 1, L, xp.bfloat16.code)
+    assert rc == xp.TL_ERR_INVALID
+    assert "allocation-free" in xp.last_error()
+    xp.synchronize()

@@ -16,6 +16,8 @@
 //                (two 4-key runs) are its B operand as they stand, and the V^T fragment is
 //                read with the same key permutation, so no data moves between lanes.
 // The final O / l is written as 4 consecutive head-dim values per lane.
+#include <mutex>
+
 #include "tl_internal.hpp"
 
 namespace tl {
@@ -496,6 +498,31 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(Attn
   p.out[((int64_t)b * p.Tq + t) * p.ld_out + (int64_t)h * D + d] = f2bf(o / stats[1]);
 }
 
+// Scratch of tl_attention_fwd_noalloc (the decode partials): a file-scope array that every
+// GPU the library runs on holds until the process ends. In host code `scratch` names a
+// host-side stand-in, not a device address; its address on each device comes from
+// hipGetSymbolAddress (attention_scratch_setup) and only that address reaches kernels.
+constexpr size_t kNoallocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+int attention_scratch_setup(tl_ctx* ctx) {
+  static std::mutex mu;
+  static void* by_device[256] = {};
+  if (ctx->device < 0 || ctx->device >= 256)
+    return fail(TL_ERR_NO_DEVICE, "device index %d out of range for the scratch table", ctx->device);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!by_device[ctx->device]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(TL_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                  hipGetErrorString(e));
+    by_device[ctx->device] = ptr;
+  }
+  ctx->noalloc_scratch = by_device[ctx->device];
+  return TL_OK;
+}
+
 template <int D>
 static void launch_decode(int nw, int jt, dim3 g1, dim3 g2, hipStream_t st, const AttnParams& p,
                           const DecodeWs& w) {
@@ -512,11 +539,14 @@ static void launch_decode(int nw, int jt, dim3 g1, dim3 g2, hipStream_t st, cons
 
 using namespace tl;
 
-extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt,
-                                void* out, int64_t batch, int64_t n_heads_q, int64_t n_heads_kv,
-                                int64_t seq_q, int64_t seq_k, int64_t head_dim, int64_t ld_out,
-                                int64_t offset, float divisor, int32_t causal,
-                                int64_t kv_capacity, int32_t dtype) {
+// Both entry points. With noalloc the decode partials go to the static scratch array (its
+// size is the limit) and the launch is kept out of the event profiler, so the call makes no
+// allocation of any kind; otherwise they go to the context's grow-only workspace.
+static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, void* out,
+                         int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
+                         int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
+                         float divisor, int32_t causal, int64_t kv_capacity, int32_t dtype,
+                         bool noalloc) {
   int rc = enter(ctx);
   if (rc) return rc;
   TL_REQUIRE(q && k && vt && out, "null pointer");
@@ -550,7 +580,7 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
   const double bh = (double)batch * n_heads_q;
   const double flops = bh * kept * 4.0 * head_dim;
   const double bytes = 2.0 * (bh * seq_q * head_dim * 2 + (double)batch * n_heads_kv * seq_k * head_dim * 2);
-  LaunchScope ls(ctx, TL_KF_ATTENTION, flops, bytes);
+  LaunchScope ls(ctx, noalloc ? -1 : TL_KF_ATTENTION, flops, bytes);
   const int64_t rows_per_kv = (n_heads_q / n_heads_kv) * seq_q;
   if (rows_per_kv <= 16) {  // decode: split the keys over many small workgroups
     DecodeWs w;
@@ -567,8 +597,18 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
     TL_REQUIRE(batch * n_heads_kv <= 65535, "batch * kv heads exceeds 65535");
     void* ws;
     const size_t obytes = (size_t)slots * 16 * head_dim * sizeof(float);
-    rc = workspace(ctx, obytes + (size_t)slots * 16 * 2 * sizeof(float), &ws);
-    if (rc) return rc;
+    const size_t need = obytes + (size_t)slots * 16 * 2 * sizeof(float);
+    if (noalloc) {
+      if (need > kNoallocScratchBytes)
+        return fail(TL_ERR_INVALID, "decode attention needs %zu bytes of partials; the "
+                    "allocation-free entry point has %zu (tl_attention_fwd has no such limit)",
+                    need, kNoallocScratchBytes);
+      if (!ctx->noalloc_scratch) return fail(TL_ERR_HIP, "static scratch was not set up");
+      ws = ctx->noalloc_scratch;
+    } else {
+      rc = workspace(ctx, need, &ws);
+      if (rc) return rc;
+    }
     w.o = (float*)ws;
     w.ml = (float*)((char*)ws + obytes);
     const dim3 g1((unsigned)w.nblk, (unsigned)(batch * n_heads_kv));
@@ -590,4 +630,23 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
     default: attention_fwd_kernel<256><<<grid, 256, 0, ctx->stream>>>(p); break;
   }
   return ls.finish("attention_fwd");
+}
+
+extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt,
+                                void* out, int64_t batch, int64_t n_heads_q, int64_t n_heads_kv,
+                                int64_t seq_q, int64_t seq_k, int64_t head_dim, int64_t ld_out,
+                                int64_t offset, float divisor, int32_t causal,
+                                int64_t kv_capacity, int32_t dtype) {
+  return attention_fwd(ctx, q, k, vt, out, batch, n_heads_q, n_heads_kv, seq_q, seq_k, head_dim,
+                       ld_out, offset, divisor, causal, kv_capacity, dtype, false);
+}
+
+extern "C" int tl_attention_fwd_noalloc(tl_ctx* ctx, const void* q, const void* k,
+                                        const void* vt, void* out, int64_t batch,
+                                        int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
+                                        int64_t seq_k, int64_t head_dim, int64_t ld_out,
+                                        int64_t offset, float divisor, int32_t causal,
+                                        int64_t kv_capacity, int32_t dtype) {
+  return attention_fwd(ctx, q, k, vt, out, batch, n_heads_q, n_heads_kv, seq_q, seq_k, head_dim,
+                       ld_out, offset, divisor, causal, kv_capacity, dtype, true);
 }

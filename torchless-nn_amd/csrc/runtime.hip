@@ -56,7 +56,7 @@ static hipEvent_t pool_event(tl_ctx* ctx) {
 
 LaunchScope::LaunchScope(tl_ctx* c, int fam, double fl, double by)
     : ctx(c), family(fam), flops(fl), bytes(by) {
-  if (ctx->kprof_mask & (1u << family)) {
+  if (family >= 0 && (ctx->kprof_mask & (1u << family))) {
     start = pool_event(ctx);
     if (start) (void)hipEventRecord(start, ctx->stream);
   }
@@ -185,6 +185,13 @@ int tl_init(int device, tl_ctx** out) {
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return fail(TL_ERR_HIP, "status word allocation: %s", hipGetErrorString(e));
+  }
+  const int src = attention_scratch_setup(ctx);
+  if (src != TL_OK) {
+    (void)hipFree(ctx->status);
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return src;
   }
   *out = ctx;
   return TL_OK;

@@ -68,6 +68,9 @@ struct tl_ctx {
   // attention); used in stream order, so one buffer serves every call on this context
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  // device address, on this context's device, of the static scratch array behind
+  // tl_attention_fwd_noalloc (set by tl_init)
+  void* noalloc_scratch = nullptr;
 };
 
 namespace tl {
@@ -89,7 +92,12 @@ int enter(tl_ctx* ctx);
 // Returns the context's scratch buffer, grown to at least `bytes` (256-byte aligned).
 int workspace(tl_ctx* ctx, size_t bytes, void** ptr);
 
-// Brackets one kernel launch with profiler events when its family is enabled.
+// Looks up, once per device and with that device current, the address of the static scratch
+// array behind tl_attention_fwd_noalloc, and stores it in ctx->noalloc_scratch.
+int attention_scratch_setup(tl_ctx* ctx);
+
+// Brackets one kernel launch with profiler events when its family is enabled (a negative
+// family never is: such a launch creates no events).
 struct LaunchScope {
   tl_ctx* ctx;
   int family;

@@ -179,6 +179,8 @@ SIGNATURES = {
     "tl_gemm": [_P, ctypes.POINTER(_GemmDesc)],
     "tl_attention_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                          _F32, _I32, _I64, _I32],
+    "tl_attention_fwd_noalloc": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                                 _I64, _F32, _I32, _I64, _I32],
 }
 _RESTYPES = {"tl_last_error": ctypes.c_char_p}
 
