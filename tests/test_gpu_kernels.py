@@ -795,6 +795,41 @@ def test_attention_fused_grouped_heads_and_offset(xp, heads):
     assert ref.max_rel(out.get(), want) <= 2e-2
 
 
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("case", [
+    # B, Hq, Hkv, Tq, Tk, Lk, causal, offset: sequences of 256 and more take the wide kernel
+    (2, 3, 3, 256, 256, 256, True, 0),      # exactly two 128-row blocks
+    (1, 4, 2, 300, 300, 304, True, 0),      # ragged last block and chunk, NaN capacity pad
+    (2, 4, 1, 330, 400, 408, True, 70),     # grouped kv heads, queries at an offset
+    (1, 2, 2, 257, 390, 392, False, 0),     # unmasked, one row in the last block
+    (8, 12, 12, 1024, 1024, 1024, True, 0),  # the GPT-2-small shape
+])
+def test_attention_wide_long_sequences(xp, D, case):
+    """The wide prefill kernel (32 query rows per wave, 128-row blocks, heaviest causal block
+    first) against the float64 definition, with NaN in the key/value capacity padding."""
+    B, Hq, Hkv, Tq, Tk, Lk, causal, offset = case
+    rng = np.random.default_rng(Tq + Tk + D)
+    q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, Hkv, Lk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
+    k[:, :, Tk:] = np.nan
+    vt[:, :, :, Tk:] = np.nan
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=divisor, causal=causal, offset=offset, seq_k=Tk)
+    got = out.get()
+    assert np.all(np.isfinite(got)), case
+    if B * Hq * Tq > 20000:  # the GPT-2 shape: first and last batch entries against float64
+        sel = [0, B - 1]
+        want = attention_ref(q[sel], k[sel][:, :, :Tk], vt[sel][:, :, :, :Tk], Hq, Hkv, divisor,
+                             causal, offset)
+        assert ref.max_rel(got[sel], want) <= 2e-2, case
+        return
+    want = attention_ref(q, k[:, :, :Tk], vt[:, :, :, :Tk], Hq, Hkv, divisor, causal, offset)
+    assert ref.max_rel(got, want) <= 2e-2, case
+
+
 @pytest.mark.parametrize("case", [
     # B, Hq, Hkv, Tq, Tk, Lk, D, causal, offset
     (4, 8, 1, 1, 2049, 2056, 256, True, 2048),

@@ -271,6 +271,231 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   }
 }
 
+// Wide variant for long sequences (D 32 or 64): each wave owns 32 query rows as two 16-row
+// MFMA groups, so every K and V fragment read from LDS feeds two MFMAs, and a workgroup of 4
+// waves covers 128 query rows, so every 64-key chunk moved into LDS serves twice the rows.
+// The per-wave chain (S^T = K Q^T, online softmax with lazy rescaling, O^T += V^T P^T, the
+// same lane layouts and key permutation) is attention_fwd_kernel's, per group. Grid:
+// (batch x heads, 128-row blocks); block y = 0 is the last (under a causal mask the
+// heaviest) block of every head, so the heaviest blocks of all heads start first.
+template <int D>
+__global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
+  constexpr int BKV = 64, G = 2, RB = 128;
+  constexpr int KCH = D / 8;
+  constexpr int KSW = KCH >= 8 ? 7 : KCH - 1;
+  constexpr int DT = D / 16;
+  constexpr int KS = D / 32;
+  constexpr int K_LOADS = BKV * KCH / 256;
+  constexpr int V_LOADS = D * 8 / 256;
+  static_assert(K_LOADS >= 1 && V_LOADS >= 1, "head_dim too small");
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[2][BKV * D];
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[2][D * BKV];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int nqb = (p.Tq + RB - 1) / RB;
+  const int qb = nqb - 1 - (int)blockIdx.y;
+  const int w0 = qb * RB + wave * 32;  // first row of this wave; group g starts at w0 + 16 g
+  const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
+  const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
+  const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
+
+  bf16x8 qf[G][KS];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int qi = min(w0 + 16 * g + fr, p.Tq - 1);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qf[g][s] = *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * D + 32 * s + 8 * fg);
+  }
+  const int q_last = min(qb * RB + RB - 1, p.Tq - 1);
+  int kv_end = p.Tk;
+  if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q_last + p.offset + 1);
+  const int nchunks = (kv_end + BKV - 1) / BKV;
+
+  uint4 rk[K_LOADS], rv[V_LOADS];
+  uint32_t k_off[K_LOADS], v_off[V_LOADS];
+#pragma unroll
+  for (int i = 0; i < K_LOADS; ++i) {
+    const int idx = i * 256 + tid;
+    k_off[i] = (uint32_t)((idx / KCH) * D + (idx % KCH) * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < V_LOADS; ++i) {
+    const int idx = i * 256 + tid;
+    v_off[i] = (uint32_t)((idx >> 3) * p.Lk + (idx & 7) * 8);
+  }
+  auto load_chunk_regs = [&](int kv0) {
+    const bf16_t* kc = kh + (int64_t)kv0 * D;
+    const bf16_t* vc = vh + kv0;
+    if (kv0 + BKV <= p.Tk) {
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) rk[i] = *reinterpret_cast<const uint4*>(kc + k_off[i]);
+#pragma unroll
+      for (int i = 0; i < V_LOADS; ++i) rv[i] = *reinterpret_cast<const uint4*>(vc + v_off[i]);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int kv = kv0 + (i * 256 + tid) / KCH;
+      rk[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(kc + k_off[i]) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < V_LOADS; ++i) {
+      const int kv = kv0 + ((i * 256 + tid) & 7) * 8;
+      rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vc + v_off[i]) : make_uint4(0, 0, 0, 0);
+      if (kv < p.Tk && kv + 8 > p.Tk) rv[i] = keep_first(rv[i], p.Tk - kv);
+    }
+  };
+  auto store_chunk_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
+      *reinterpret_cast<uint4*>(&Ks[buf][r * D + ((c ^ (r & KSW)) << 3)]) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < V_LOADS; ++i) {
+      const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
+      *reinterpret_cast<uint4*>(&Vs[buf][r * BKV + ((c ^ (r & 7)) << 3)]) = rv[i];
+    }
+  };
+
+  f32x4 o[G][DT];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[g][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[G], l_part[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_part[g] = 0.f;
+  }
+
+  load_chunk_regs(0);
+  store_chunk_lds(0);
+  __syncthreads();
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int cur = ch & 1;
+    const int kv0 = ch * BKV;
+    if (ch + 1 < nchunks) load_chunk_regs(kv0 + BKV);
+
+    // S^T for 4 key tiles of 16, both row groups from each K fragment
+    f32x4 s[G][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[g][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int r = j * 16 + fr;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = ks * 4 + fg;
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[cur][r * D + ((c ^ (r & KSW)) << 3)]);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          s[g][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[g][ks], s[g][j], 0, 0, 0);
+      }
+    }
+    bf16x8 pf[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int q0 = w0 + 16 * g, qpos = q0 + fr;
+      float mx = -INFINITY;
+      const bool full = kv0 + BKV <= p.Tk &&
+                        (!p.causal || (int64_t)(kv0 + BKV - 1) <= (int64_t)q0 + p.offset);
+      if (full) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[g][j][v]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kv = kv0 + j * 16 + 4 * fg + v;
+            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
+            s[g][j][v] = ok ? s[g][j][v] : -INFINITY;
+            mx = fmaxf(mx, s[g][j][v]);
+          }
+      }
+      // lazy rescaling, as in attention_fwd_kernel
+      if (__any(mx * p.scale_log2 > m_run[g] + 8.0f)) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mxs = mx * p.scale_log2;
+        const bool grow = mxs > m_run[g] + 8.0f;
+        const float m_new = grow ? mxs : m_run[g];
+        const float alpha = __builtin_amdgcn_exp2f(m_run[g] - m_new);
+        l_part[g] *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o[g][t][v] *= alpha;
+        m_run[g] = m_new;
+      }
+      const float m_ref = m_run[g] == -INFINITY ? 0.f : m_run[g];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][j][v], p.scale_log2, -m_ref));
+          s[g][j][v] = e;
+          l_part[g] += e;
+        }
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          pf[g][c2][v] = (__bf16)s[g][2 * c2][v];
+          pf[g][c2][4 + v] = (__bf16)s[g][2 * c2 + 1][v];
+        }
+    }
+
+    // O^T += V^T P^T over two 32-key halves, both row groups from each V fragment
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2) {
+      const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int r = t * 16 + fr;
+        const bf16_t* row = &Vs[cur][r * BKV];
+        const int ca = ka >> 3, cb = kb >> 3;
+        const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 7)) << 3) + (ka & 7));
+        const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 7)) << 3) + (kb & 7));
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[g][c2], o[g][t], 0, 0, 0);
+      }
+    }
+
+    if (ch + 1 < nchunks) store_chunk_lds(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float l_run = l_part[g] + __shfl_xor(l_part[g], 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    const int qpos = w0 + 16 * g + fr;
+    if (qpos < p.Tq) {
+      const float inv = 1.0f / l_run;
+      bf16_t* orow = p.out + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        uint2 w;
+        w.x = (uint32_t)f2bf(o[g][t][0] * inv) | ((uint32_t)f2bf(o[g][t][1] * inv) << 16);
+        w.y = (uint32_t)f2bf(o[g][t][2] * inv) | ((uint32_t)f2bf(o[g][t][3] * inv) << 16);
+        *reinterpret_cast<uint2*>(orow + t * 16 + 4 * fg) = w;
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Decode (split-KV) attention for a few query rows per kv head: the query rows that share a
 // kv head (Hq / Hkv heads x Tq positions, at most 16) form one MFMA column block, so every
@@ -620,6 +845,15 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
       default: launch_decode<256>(nw, jt, g1, g2, ctx->stream, p, w); break;
     }
     return ls.finish("attention_decode");
+  }
+  // long sequences at head dim 32 / 64: the wide kernel (128-row blocks, 32 rows per wave)
+  if (seq_q >= 256 && head_dim <= 64) {
+    const int64_t nqb = (seq_q + 127) / 128;
+    TL_REQUIRE(nqb <= 65535, "too many 128-row query blocks");
+    const dim3 grid((unsigned)(batch * n_heads_q), (unsigned)nqb);
+    if (head_dim == 32) attention_fwd_wide_kernel<32><<<grid, 256, 0, ctx->stream>>>(p);
+    else attention_fwd_wide_kernel<64><<<grid, 256, 0, ctx->stream>>>(p);
+    return ls.finish("attention_fwd_wide");
   }
   const int64_t nqb = (seq_q + 63) / 64;
   dim3 grid((unsigned)(causal ? (nqb + 1) / 2 : nqb), (unsigned)(batch * n_heads_q));
