@@ -248,6 +248,31 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
     xp.synchronize()
     wall = (time.perf_counter() - t0) / decode_steps * 1e3
     decode_ms = e0.elapsed_ms(e1) / decode_steps
+    # the same steps as one captured HIP graph each: the position lives on the device, so
+    # one capture replays at every position (same kernels and results as the loop above)
+    import layers
+    tok = xp.empty((B,), xp.int64)
+    xp.argmax(model.last_rows(logits), out=tok)
+    dpos = layers.DevicePosition(T, 1, D, cfg["rope_base"])
+
+    def gstep():
+        model.decode_step(tok, cache, dpos)
+        dpos.advance(1)
+
+    gstep()  # eager at the device position: everything the capture needs exists after it
+    with xp.capture() as g:
+        gstep()
+    dpos.pos.set(np.array([T], np.int64))
+    xp.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for t in range(decode_steps):
+        g.launch()
+    e1.record()
+    xp.synchronize()
+    gwall = (time.perf_counter() - t0) / decode_steps * 1e3
+    graph_ms = e0.elapsed_ms(e1) / decode_steps
+    g.destroy()
     # per-family kernel time of the decode steps (HIP events around every launch)
     xp.kprof_reset()
     xp.kprof_enable(list(xp.KFAMILY))
@@ -278,6 +303,10 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
         "decode_bytes_per_step": w_bytes + kv_bytes,
         "decode_hbm_gbs": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9, 1),
         "decode_hbm_frac": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "decode_graph_ms_per_step": round(graph_ms, 4),
+        "decode_graph_wall_ms_per_step": round(gwall, 4),
+        "decode_graph_tokens_per_s": round(B / (graph_ms * 1e-3), 1),
+        "decode_graph_hbm_frac": round((w_bytes + kv_bytes) / (graph_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         "decode_kernel_breakdown": decode_breakdown,
     }
     log(f"gemma config 5: {json.dumps(out)}")

@@ -29,6 +29,7 @@ extern "C" {
 #endif
 
 typedef struct tl_ctx tl_ctx;
+typedef struct tl_graph tl_graph;
 
 /* Element types. Floating-point data is fp32 or bf16 (bf16 stored as raw uint16). */
 enum tl_dtype { TL_F32 = 0, TL_BF16 = 1, TL_I32 = 2, TL_I64 = 3, TL_U8 = 4 };
@@ -136,6 +137,10 @@ typedef struct tl_gemm_desc {
   int32_t family;                       /* enum tl_kfamily used by the profiler */
   int32_t tile;                         /* MFMA tile hint: 0 = choose automatically, else
                                            enum tl_gemm_tile */
+  const void* kv_pos0_dev;              /* TL_EPI_QKV_SPLIT: when not NULL, an int64 in device
+                                           memory read at run time in place of kv_pos0 (a
+                                           captured graph writes the cache at the current
+                                           position); rows past kv_len are not written */
 } tl_gemm_desc;
 
 /* ---- runtime ------------------------------------------------------------------------ */
@@ -153,7 +158,9 @@ int tl_free(tl_ctx* ctx, void* ptr);
 int tl_empty_cache(tl_ctx* ctx);
 int tl_mem_stats(tl_ctx* ctx, size_t* bytes_in_use, size_t* bytes_cached);
 /* Host<->device copies. Replace `xp.array(host)` (reference network.py:117-118, 152-153) and
- * `.get()` (reference demo.ipynb:1535). h2d returns once the host buffer may be reused. */
+ * `.get()` (reference demo.ipynb:1535). h2d returns once the host buffer may be reused: up to
+ * 64 MiB it is copied into a pinned staging buffer and the device copy is queued behind the
+ * work already on the stream, without waiting for it; larger copies wait for the stream. */
 int tl_memcpy_h2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
 int tl_memcpy_d2h(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
 int tl_memcpy_d2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes);
@@ -163,6 +170,20 @@ int tl_memcpy2d_d2h(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
                     size_t width_bytes, size_t rows);
 /* Waits for the stream, then reports any latched kernel data error. */
 int tl_sync(tl_ctx* ctx);
+/* HIP graphs of the context stream, for replaying a whole step (a decode step, a short
+ * forward) with one launch instead of one host call per kernel. No reference counterpart
+ * (the reference dispatches every op from Python, network.py:36-39).
+ * tl_graph_begin starts capturing: the calls that follow are recorded, not run, until
+ * tl_graph_end, which instantiates them. While a capture is open, calls that wait for the
+ * stream (tl_sync, host copies) fail with TL_ERR_INVALID, the kernel profiler records
+ * nothing, and a workspace that would have to grow fails the call (run the step once
+ * before capturing it). Device blocks that tl_malloc hands out during the capture belong to
+ * the graph until tl_graph_destroy: replays write them, so they are kept from reuse even
+ * after the caller frees them. tl_graph_launch replays the graph on the context stream. */
+int tl_graph_begin(tl_ctx* ctx);
+int tl_graph_end(tl_ctx* ctx, tl_graph** out);
+int tl_graph_launch(tl_ctx* ctx, tl_graph* graph);
+int tl_graph_destroy(tl_ctx* ctx, tl_graph* graph);
 /* Events on the context stream, for timing. */
 int tl_event_create(tl_ctx* ctx, void** ev);
 int tl_event_record(tl_ctx* ctx, void* ev);
@@ -229,6 +250,24 @@ int tl_softmax_fwd(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
  * evaluated in fp64. No reference counterpart (positions are absolute there). */
 int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
                   int64_t pos0);
+/* tl_rope_table for positions *pos0 .. *pos0 + seq_len - 1, with *pos0 an int64 read from
+ * device memory when the kernel runs (a graph replays it at the current position). */
+int tl_rope_table_dev(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
+                      const int64_t* pos0);
+/* In-place tl_rope2_fwd whose second set starts at row *pos of each sequence: x2 points at
+ * row 0 of n_seq2 sequences of rows_cap2 rows, seq_stride2 elements apart (a KV cache), and
+ * rows *pos .. *pos + seq_len - 1 of each are rotated by the table's seq_len positions
+ * (rows at or past rows_cap2 are skipped). *pos is an int64 read from device memory when
+ * the kernel runs. */
+int tl_rope2_dev(tl_ctx* ctx, void* x1, int64_t n_seq1, int64_t seq_stride1, void* x2,
+                 int64_t n_seq2, int64_t seq_stride2, int64_t rows_cap2, const void* table,
+                 int64_t seq_len, int64_t head_dim, const int64_t* pos, int32_t dtype);
+/* *x += delta on the device (advances a device position inside a graph). */
+int tl_i64_add(tl_ctx* ctx, int64_t* x, int64_t delta);
+/* hist[r * ld_hist + (*pos - pos_base)] = ids[r] for r < rows, when that column lies in
+ * [0, cols): records a decode step's token ids at a device position. */
+int tl_ids_append(tl_ctx* ctx, const int64_t* ids, int64_t* hist, int64_t rows, int64_t ld_hist,
+                  int64_t cols, const int64_t* pos, int64_t pos_base);
 /* Rotate-half RoPE over x [n_seq][seq_stride] holding T rows of D (row pitch D) per
  * sequence (seq_stride = T*D when packed; a cache slice uses its capacity * D): for i < D/2,
  * y[i] = x[i] cos - x[i+D/2] sin, y[i+D/2] = x[i+D/2] cos + x[i] sin. In place is allowed. */
@@ -261,6 +300,16 @@ int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, 
                      int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                      int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
                      float divisor, int32_t causal, int64_t kv_capacity, int32_t dtype);
+/* Causal decode attention (at most 16 query rows per kv head) at a device position: query t
+ * sits at position *pos + t and keys 0 .. *pos + seq_q - 1 of the cache (capacity
+ * kv_capacity, at most that many) are attended to, with *pos an int64 read from device
+ * memory when the kernels run, so a captured decode step replays at the current position.
+ * Otherwise as tl_attention_fwd. No reference counterpart (the reference recomputes the
+ * window every step, demo.ipynb:1526-1533). */
+int tl_attention_decode_dev(tl_ctx* ctx, const void* q, const void* k, const void* vt, void* out,
+                            int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
+                            int64_t head_dim, int64_t ld_out, float divisor, int64_t kv_capacity,
+                            const int64_t* pos, int32_t dtype);
 /* tl_attention_fwd that allocates nothing: the same arguments, kernels and results, with the
  * decode path's partial results (at most 16 query rows per kv head) kept in a static device
  * array of 16 MiB instead of the context's grow-only workspace, and the launch kept out of the

@@ -51,6 +51,7 @@ struct GemmParams {
   void* vt;
   int T, Hq, Hkv, Dh;
   int L, pos0;  // key/value cache capacity and write position (QKV split)
+  const int64_t* pos0_dev;  // when set: the write position, read from device memory
   int geglu;    // gated epilogue: C[m, n/2] = act(acc[m, n]) * acc[m, n+1]
   int tiles_m, tiles_n, group_m;
   FastDiv div_T, div_Dh;
@@ -139,6 +140,7 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
     // Dh % 4 == 0 (checked on the host), so the 4 columns share one head of one part.
     const int mi = (int)m, ni = (int)n0;
     const int b = mi / p.T, t = mi - b * p.T;
+    const int pos0 = p.pos0_dev ? (int)*p.pos0_dev : p.pos0;
     const int qw = p.Hq * p.Dh, kw = p.Hkv * p.Dh;
     TO* dst;
     int64_t step;
@@ -147,12 +149,14 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
       dst = (TO*)p.q + ((int64_t)(b * p.Hq + h) * p.T + t) * p.Dh + d;
       step = 1;
     } else if (ni < qw + kw) {
+      if (t + pos0 >= p.L) return;  // a device position past the cache: nothing written
       const int nn = ni - qw, h = nn / p.Dh, d = nn - h * p.Dh;
-      dst = (TO*)p.k + ((int64_t)(b * p.Hkv + h) * p.L + t + p.pos0) * p.Dh + d;
+      dst = (TO*)p.k + ((int64_t)(b * p.Hkv + h) * p.L + t + pos0) * p.Dh + d;
       step = 1;
     } else {
+      if (t + pos0 >= p.L) return;
       const int nn = ni - qw - kw, h = nn / p.Dh, d = nn - h * p.Dh;
-      dst = (TO*)p.vt + ((int64_t)(b * p.Hkv + h) * p.Dh + d) * p.L + t + p.pos0;
+      dst = (TO*)p.vt + ((int64_t)(b * p.Hkv + h) * p.Dh + d) * p.L + t + pos0;
       step = p.L;
     }
     if (step == 1 && sizeof(TO) == 2) {
@@ -242,14 +246,17 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
       const int64_t m = mb + 16 * i;
       if (m >= e.M) continue;
       const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
+      const int pos0 = e.pos0_dev ? (int)*e.pos0_dev : e.pos0;
+      const bool in_cache = t + pos0 < e.L;  // a device position past the cache: no K/V rows
       const int64_t rq = ((int64_t)b * e.Hq * e.T + t) * e.Dh;
-      const int64_t rk = ((int64_t)b * e.Hkv * e.L + t + e.pos0) * e.Dh;
-      const int64_t rv = (int64_t)b * e.Hkv * e.Dh * e.L + t + e.pos0;
+      const int64_t rk = ((int64_t)b * e.Hkv * e.L + t + pos0) * e.Dh;
+      const int64_t rv = (int64_t)b * e.Hkv * e.Dh * e.L + t + pos0;
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         if (cnt[j] == 0) continue;
         float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
         finish(v, j);
+        if (part[j] > 0 && !in_cache) continue;
         if (part[j] < 2) {
           TO* dst = cbase[j] + (part[j] == 0 ? rq : rk);
           if (sizeof(TO) == 2) {
@@ -1569,6 +1576,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     const int64_t L = d->kv_len > 0 ? d->kv_len : d->seq_len;
     TL_REQUIRE(d->kv_pos0 >= 0 && d->kv_pos0 + d->seq_len <= L && L < (1LL << 31),
                "cache write [kv_pos0, kv_pos0 + seq_len) exceeds kv_len");
+    TL_REQUIRE(!d->kv_pos0_dev || ((uintptr_t)d->kv_pos0_dev % 8 == 0 && d->kv_pos0 == 0),
+               "kv_pos0_dev must be an aligned int64 and kv_pos0 0");
   } else {
     TL_REQUIRE(d->C, "null output");
     TL_REQUIRE(d->ldc >= (geglu ? d->N / 2 : d->N), "ldc too small");
@@ -1587,6 +1596,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.T = (int)d->seq_len; p.Hq = (int)d->n_heads_q; p.Hkv = (int)d->n_heads_kv; p.Dh = (int)d->head_dim;
   p.L = (int)(d->kv_len > 0 ? d->kv_len : d->seq_len);
   p.pos0 = (int)d->kv_pos0;
+  p.pos0_dev = qkv ? (const int64_t*)d->kv_pos0_dev : nullptr;
   p.geglu = geglu;
   const size_t eo = dtype_size(d->dtype_out);
   p.vec_store = !qkv && d->ldc % 4 == 0 && ((uintptr_t)d->C % (4 * eo)) == 0 &&
@@ -1610,7 +1620,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     else if (b && r && d->act == TL_ACT_NONE) p.epi = EPI_BIAS_RES;
     else if (!b && r && d->act == TL_ACT_NONE) p.epi = EPI_RES;
   }
-  if (qkv && eo == 2 && d->divisor == 1.0f && d->act == TL_ACT_NONE && !d->residual &&
+  if (qkv && !d->kv_pos0_dev && eo == 2 && d->divisor == 1.0f && d->act == TL_ACT_NONE && !d->residual &&
       d->head_dim % 8 == 0 && d->seq_len % 8 == 0 && p.L % 8 == 0 && p.pos0 % 8 == 0 &&
       ((uintptr_t)d->q % 16) == 0 && ((uintptr_t)d->k % 16) == 0 && ((uintptr_t)d->vt % 16) == 0)
     p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;

@@ -639,11 +639,15 @@ __global__ void rope_table_kernel(float* table, int64_t seq_len, int64_t head_di
 }
 
 // One sequence set of a RoPE launch: n_seq sequences of seq_len rows, seq_stride elements
-// apart (x == y allowed).
+// apart (x == y allowed). With row0 set, the rows start at row *row0 of each sequence (an
+// int64 in device memory: a cache slice at a position known only when the kernel runs), and
+// rows at or past rows_cap are left alone.
 struct RopeSet {
   const void* x;
   void* y;
   int64_t n_seq, seq_stride;
+  const int64_t* row0;
+  int64_t rows_cap;
 };
 
 // One thread per (row, chunk of the first half): it loads that chunk and the matching chunk
@@ -665,8 +669,13 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeSet s0, RopeSet s1,
   const int64_t total = total0 + s1.n_seq * seq_len * per_row;
   const int64_t tsz = seq_len * half;
   auto item = [&](const RopeSet& st, int64_t i, int64_t sq, int64_t t) {
-    const T* xr = (const T*)st.x + sq * st.seq_stride + t * head_dim;
-    T* yr = (T*)st.y + sq * st.seq_stride + t * head_dim;
+    int64_t r = t;
+    if (st.row0) {
+      r += *st.row0;
+      if (r < t || r >= st.rows_cap) return;
+    }
+    const T* xr = (const T*)st.x + sq * st.seq_stride + r * head_dim;
+    T* yr = (T*)st.y + sq * st.seq_stride + r * head_dim;
     const float* cs = table + t * half + i;
     const float* sn = table + tsz + t * half + i;
     float a[VW], b[VW], c[VW], s[VW], o1[VW], o2[VW];
@@ -1276,6 +1285,34 @@ int tl_softmax_fwd(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
   return ls.finish("softmax_fwd");
 }
 
+// Positions read from an int64 in device memory, so a captured graph replays with the
+// current position rather than the one it was captured at.
+__global__ void rope_table_dev_kernel(float* table, int64_t seq_len, int64_t head_dim, double base,
+                                      const int64_t* pos0) {
+  const int64_t half = head_dim / 2;
+  const int64_t n = seq_len * half;
+  const int64_t p0 = *pos0;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = idx / half, i = idx % half;
+    const double inv_freq = pow(base, -(double)(2 * i) / (double)head_dim);
+    const double ang = (double)(p0 + t) * inv_freq;
+    table[idx] = (float)cos(ang);
+    table[n + idx] = (float)sin(ang);
+  }
+}
+// x[0] += delta, by lane 0 of one wave (a vector store)
+__global__ void i64_add_kernel(int64_t* x, int64_t delta) {
+  if (threadIdx.x == 0) x[0] = x[0] + delta;
+}
+// hist[r * ld + (*pos - base)] = ids[r] for r < rows when 0 <= *pos - base < cols
+__global__ void ids_append_kernel(const int64_t* ids, int64_t* hist, int64_t rows, int64_t ld,
+                                  int64_t cols, const int64_t* pos, int64_t base) {
+  const int64_t c = *pos - base;
+  if (c < 0 || c >= cols) return;
+  for (int64_t r = threadIdx.x; r < rows; r += blockDim.x) hist[r * ld + c] = ids[r];
+}
+
 int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
                   int64_t pos0) {
   int rc = enter(ctx);
@@ -1289,6 +1326,40 @@ int tl_rope_table(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, d
   return ls.finish("rope_table");
 }
 
+int tl_rope_table_dev(tl_ctx* ctx, void* table, int64_t seq_len, int64_t head_dim, double base,
+                      const int64_t* pos0) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(table && pos0, "null pointer");
+  TL_REQUIRE(seq_len > 0 && head_dim > 0 && head_dim % 2 == 0, "head_dim must be even and positive");
+  TL_REQUIRE(base > 0 && (uintptr_t)pos0 % 8 == 0, "bad base or unaligned position");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 4.0 * seq_len * head_dim);
+  rope_table_dev_kernel<<<grid_for(ctx, seq_len * head_dim / 2, 256), 256, 0, ctx->stream>>>(
+      (float*)table, seq_len, head_dim, base, pos0);
+  return ls.finish("rope_table_dev");
+}
+
+int tl_i64_add(tl_ctx* ctx, int64_t* x, int64_t delta) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(x && (uintptr_t)x % 8 == 0, "null or unaligned pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 16.0);
+  i64_add_kernel<<<1, 64, 0, ctx->stream>>>(x, delta);
+  return ls.finish("i64_add");
+}
+
+int tl_ids_append(tl_ctx* ctx, const int64_t* ids, int64_t* hist, int64_t rows, int64_t ld_hist,
+                  int64_t cols, const int64_t* pos, int64_t pos_base) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(ids && hist && pos, "null pointer");
+  TL_REQUIRE(rows > 0 && cols > 0 && ld_hist >= cols, "bad history shape");
+  TL_REQUIRE(((uintptr_t)ids | (uintptr_t)hist | (uintptr_t)pos) % 8 == 0, "unaligned int64 operand");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, 16.0 * rows);
+  ids_append_kernel<<<1, 256, 0, ctx->stream>>>(ids, hist, rows, ld_hist, cols, pos, pos_base);
+  return ls.finish("ids_append");
+}
+
 int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t n_seq,
                 int64_t seq_len, int64_t head_dim, int64_t seq_stride, int32_t dtype) {
   int rc = enter(ctx);
@@ -1300,7 +1371,7 @@ int tl_rope_fwd(tl_ctx* ctx, const void* x, void* y, const void* table, int64_t 
   TL_REQUIRE(x && y && table, "null pointer");
   const double es = (double)dtype_size(dtype);
   LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * n_seq * seq_len * head_dim);
-  const RopeSet s0{x, y, n_seq, seq_stride}, s1{nullptr, nullptr, 0, 0};
+  const RopeSet s0{x, y, n_seq, seq_stride, nullptr, 0}, s1{nullptr, nullptr, 0, 0, nullptr, 0};
   if (dtype == TL_F32) launch_rope<float>(ctx, s0, s1, table, seq_len, head_dim);
   else launch_rope<bf16_t>(ctx, s0, s1, table, seq_len, head_dim);
   return ls.finish("rope_fwd");
@@ -1321,10 +1392,34 @@ int tl_rope2_fwd(tl_ctx* ctx, const void* x1, void* y1, int64_t n_seq1, int64_t 
   TL_REQUIRE(table && (n_seq1 == 0 || (x1 && y1)) && (n_seq2 == 0 || (x2 && y2)), "null pointer");
   const double es = (double)dtype_size(dtype);
   LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * (n_seq1 + n_seq2) * seq_len * head_dim);
-  const RopeSet s0{x1, y1, n_seq1, seq_stride1}, s1{x2, y2, n_seq2, seq_stride2};
+  const RopeSet s0{x1, y1, n_seq1, seq_stride1, nullptr, 0},
+      s1{x2, y2, n_seq2, seq_stride2, nullptr, 0};
   if (dtype == TL_F32) launch_rope<float>(ctx, s0, s1, table, seq_len, head_dim);
   else launch_rope<bf16_t>(ctx, s0, s1, table, seq_len, head_dim);
   return ls.finish("rope2_fwd");
+}
+
+int tl_rope2_dev(tl_ctx* ctx, void* x1, int64_t n_seq1, int64_t seq_stride1, void* x2,
+                 int64_t n_seq2, int64_t seq_stride2, int64_t rows_cap2, const void* table,
+                 int64_t seq_len, int64_t head_dim, const int64_t* pos, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(n_seq1 >= 0 && n_seq2 >= 0 && seq_len > 0 && head_dim > 0 && head_dim % 2 == 0,
+             "bad sizes");
+  TL_REQUIRE((n_seq1 == 0 || seq_stride1 >= seq_len * head_dim) &&
+                 (n_seq2 == 0 || (rows_cap2 >= seq_len && seq_stride2 >= rows_cap2 * head_dim)),
+             "seq_stride1 < seq_len * head_dim or seq_stride2 < rows_cap2 * head_dim");
+  if (n_seq1 + n_seq2 == 0) return TL_OK;
+  TL_REQUIRE(table && pos && (n_seq1 == 0 || x1) && (n_seq2 == 0 || x2), "null pointer");
+  TL_REQUIRE((uintptr_t)pos % 8 == 0, "unaligned position");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_ROPE, 0, 2.0 * es * (n_seq1 + n_seq2) * seq_len * head_dim);
+  const RopeSet s0{x1, x1, n_seq1, seq_stride1, nullptr, 0},
+      s1{x2, x2, n_seq2, seq_stride2, pos, rows_cap2};
+  if (dtype == TL_F32) launch_rope<float>(ctx, s0, s1, table, seq_len, head_dim);
+  else launch_rope<bf16_t>(ctx, s0, s1, table, seq_len, head_dim);
+  return ls.finish("rope2_dev");
 }
 
 int tl_act_fwd(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t act, int32_t dtype) {

@@ -1,5 +1,6 @@
 // libtl runtime: context, errors, caching allocator, copies, events and the per-launch
 // event profiler. One in-order HIP stream per context; every op is enqueued on it.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdlib>
 #include <cstring>
@@ -22,9 +23,16 @@ void clear_error() { g_err[0] = 0; }
 
 int workspace(tl_ctx* ctx, size_t bytes, void** ptr) {
   if (bytes > ctx->ws_bytes) {
-    // the old buffer may still be read by queued kernels: wait for them before freeing
+    if (ctx->capturing)
+      return fail(TL_ERR_INVALID, "the workspace would grow to %zu bytes during a graph capture: "
+                  "run the captured calls once before capturing them", bytes);
+    // the old buffer may still be read by queued kernels: wait for them before freeing; a
+    // live graph may still replay kernels that use it, so it is kept until no graph is left
     TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
-    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ws) {
+      if (ctx->graphs.empty()) (void)hipFree(ctx->ws);
+      else ctx->ws_retired.push_back(ctx->ws);
+    }
     ctx->ws = nullptr;
     ctx->ws_bytes = 0;
     const size_t size = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
@@ -56,7 +64,7 @@ static hipEvent_t pool_event(tl_ctx* ctx) {
 
 LaunchScope::LaunchScope(tl_ctx* c, int fam, double fl, double by)
     : ctx(c), family(fam), flops(fl), bytes(by) {
-  if (family >= 0 && (ctx->kprof_mask & (1u << family))) {
+  if (family >= 0 && !ctx->capturing && (ctx->kprof_mask & (1u << family))) {
     start = pool_event(ctx);
     if (start) (void)hipEventRecord(start, ctx->stream);
   }
@@ -95,6 +103,7 @@ static int kprof_drain(tl_ctx* ctx) {
 
 static int release_cache(tl_ctx* ctx) {
   if (ctx->free_blocks.empty()) return TL_OK;
+  if (ctx->capturing) return fail(TL_ERR_INVALID, "cannot release cached blocks during a graph capture");
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
   for (auto& kv : ctx->free_blocks) (void)hipFree(kv.second);
   ctx->free_blocks.clear();
@@ -200,7 +209,25 @@ int tl_init(int device, tl_ctx** out) {
 int tl_destroy(tl_ctx* ctx) {
   int rc = enter(ctx);
   if (rc) return rc;
+  if (ctx->capturing) {
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();
+  }
   (void)hipStreamSynchronize(ctx->stream);
+  for (tl_graph* g : ctx->graphs) {
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+  }
+  for (auto& kv : ctx->graph_block_size)
+    if (ctx->graph_released.count(kv.first)) (void)hipFree(kv.first);
+  for (void* w : ctx->ws_retired) (void)hipFree(w);
+  for (auto& st : ctx->staging) {
+    if (st.host) (void)hipHostFree(st.host);
+    if (st.done) (void)hipEventDestroy(st.done);
+  }
   for (auto& r : ctx->kprof_pending) {
     (void)hipEventDestroy(r.start);
     (void)hipEventDestroy(r.stop);
@@ -225,6 +252,18 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr) {
   size_t size = bytes == 0 ? 512 : bytes;
   size_t gran = size < (1u << 20) ? 512 : (64u << 10);
   size = (size + gran - 1) / gran * gran;
+  if (ctx->capturing) {
+    // a block this capture already handed out and got back is reused first (the captured
+    // kernels run in stream order, as eager ones do)
+    auto ct = ctx->capture_free.lower_bound(size);
+    if (ct != ctx->capture_free.end() && ct->first <= size + size / 4) {
+      void* p = ct->second;
+      ctx->live[p] = ct->first;
+      ctx->capture_free.erase(ct);
+      *ptr = p;
+      return TL_OK;
+    }
+  }
   auto it = ctx->free_blocks.lower_bound(size);
   if (it != ctx->free_blocks.end() && it->first <= size + size / 4) {
     size_t got = it->first;
@@ -233,6 +272,7 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr) {
     ctx->bytes_cached -= got;
     ctx->live[p] = got;
     ctx->bytes_in_use += got;
+    if (ctx->capturing) ctx->capture_blocks.push_back(p);
     *ptr = p;
     return TL_OK;
   }
@@ -240,6 +280,8 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr) {
   hipError_t e = hipMalloc(&p, size);
   if (e != hipSuccess) {
     (void)hipGetLastError();
+    if (ctx->capturing)
+      return fail(TL_ERR_OOM, "hipMalloc(%zu bytes) failed during a graph capture", size);
     rc = release_cache(ctx);
     if (rc) return rc;
     e = hipMalloc(&p, size);
@@ -250,6 +292,7 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr) {
   }
   ctx->live[p] = size;
   ctx->bytes_in_use += size;
+  if (ctx->capturing) ctx->capture_blocks.push_back(p);
   *ptr = p;
   return TL_OK;
 }
@@ -260,6 +303,19 @@ int tl_free(tl_ctx* ctx, void* ptr) {
   if (!ptr) return TL_OK;
   auto it = ctx->live.find(ptr);
   if (it == ctx->live.end()) return fail(TL_ERR_INVALID, "tl_free: %p was not allocated by tl_malloc", ptr);
+  if (ctx->graph_block_size.count(ptr)) {
+    // a live graph still writes it on every replay: held until tl_graph_destroy
+    ctx->graph_released.insert(ptr);
+    ctx->live.erase(it);
+    return TL_OK;
+  }
+  if (ctx->capturing &&
+      std::find(ctx->capture_blocks.begin(), ctx->capture_blocks.end(), ptr) != ctx->capture_blocks.end()) {
+    // handed out by the open capture: reusable by the rest of it, then held by its graph
+    ctx->capture_free.emplace(it->second, ptr);
+    ctx->live.erase(it);
+    return TL_OK;
+  }
   // Stream order makes reuse safe: the next user's kernels run after this block's last
   // reader on the same stream.
   ctx->free_blocks.emplace(it->second, ptr);
@@ -283,11 +339,47 @@ int tl_mem_stats(tl_ctx* ctx, size_t* in_use, size_t* cached) {
   return TL_OK;
 }
 
+// A pinned staging buffer of at least `bytes` whose previous copy has completed (waiting
+// only for that copy), or null when the copy is too large to stage.
+static constexpr size_t kStageMax = (size_t)64 << 20;
+static int stage_for(tl_ctx* ctx, size_t bytes, tl_ctx::Staging** out) {
+  *out = nullptr;
+  if (bytes > kStageMax) return TL_OK;
+  tl_ctx::Staging& st = ctx->staging[ctx->staging_next];
+  ctx->staging_next = (ctx->staging_next + 1) % 4;
+  if (st.pending) {
+    TL_CHECK_HIP(hipEventSynchronize(st.done));
+    st.pending = false;
+  }
+  if (!st.done) TL_CHECK_HIP(hipEventCreateWithFlags(&st.done, hipEventDisableTiming));
+  if (st.bytes < bytes) {
+    if (st.host) TL_CHECK_HIP(hipHostFree(st.host));
+    st.host = nullptr;
+    st.bytes = 0;
+    const size_t sz = std::max(bytes, (size_t)1 << 20);
+    TL_CHECK_HIP(hipHostMalloc(&st.host, sz, hipHostMallocDefault));
+    st.bytes = sz;
+  }
+  *out = &st;
+  return TL_OK;
+}
+
 int tl_memcpy_h2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes) {
   int rc = enter(ctx);
   if (rc) return rc;
   if (bytes == 0) return TL_OK;
   TL_REQUIRE(dst && src, "null pointer");
+  TL_REQUIRE(!ctx->capturing, "host copies cannot be captured in a graph");
+  tl_ctx::Staging* st;
+  rc = stage_for(ctx, bytes, &st);
+  if (rc) return rc;
+  if (st) {
+    std::memcpy(st->host, src, bytes);
+    TL_CHECK_HIP(hipMemcpyAsync(dst, st->host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    TL_CHECK_HIP(hipEventRecord(st->done, ctx->stream));
+    st->pending = true;
+    return TL_OK;
+  }
   TL_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
   return TL_OK;
@@ -298,6 +390,7 @@ int tl_memcpy_d2h(tl_ctx* ctx, void* dst, const void* src, size_t bytes) {
   if (rc) return rc;
   if (bytes == 0) return TL_OK;
   TL_REQUIRE(dst && src, "null pointer");
+  TL_REQUIRE(!ctx->capturing, "host copies cannot be captured in a graph");
   TL_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
   return check_status_word(ctx);
@@ -319,6 +412,19 @@ int tl_memcpy2d_h2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
   if (width == 0 || rows == 0) return TL_OK;
   TL_REQUIRE(dst && src, "null pointer");
   TL_REQUIRE(width <= dpitch && width <= spitch, "width exceeds pitch");
+  TL_REQUIRE(!ctx->capturing, "host copies cannot be captured in a graph");
+  tl_ctx::Staging* st;
+  rc = stage_for(ctx, width * rows, &st);
+  if (rc) return rc;
+  if (st) {  // rows packed into the staging buffer, then one 2D copy out of it
+    for (size_t r = 0; r < rows; ++r)
+      std::memcpy((char*)st->host + r * width, (const char*)src + r * spitch, width);
+    TL_CHECK_HIP(hipMemcpy2DAsync(dst, dpitch, st->host, width, width, rows, hipMemcpyHostToDevice,
+                                  ctx->stream));
+    TL_CHECK_HIP(hipEventRecord(st->done, ctx->stream));
+    st->pending = true;
+    return TL_OK;
+  }
   TL_CHECK_HIP(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyHostToDevice, ctx->stream));
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
   return TL_OK;
@@ -331,6 +437,7 @@ int tl_memcpy2d_d2h(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
   if (width == 0 || rows == 0) return TL_OK;
   TL_REQUIRE(dst && src, "null pointer");
   TL_REQUIRE(width <= dpitch && width <= spitch, "width exceeds pitch");
+  TL_REQUIRE(!ctx->capturing, "host copies cannot be captured in a graph");
   TL_CHECK_HIP(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToHost, ctx->stream));
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
   return check_status_word(ctx);
@@ -339,7 +446,111 @@ int tl_memcpy2d_d2h(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
 int tl_sync(tl_ctx* ctx) {
   int rc = enter(ctx);
   if (rc) return rc;
+  TL_REQUIRE(!ctx->capturing, "tl_sync during a graph capture");
   TL_CHECK_HIP(hipStreamSynchronize(ctx->stream));
+  return check_status_word(ctx);
+}
+
+int tl_graph_begin(tl_ctx* ctx) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(!ctx->capturing, "a graph capture is already open on this context");
+  TL_CHECK_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+  ctx->capturing = true;
+  ctx->capture_blocks.clear();
+  ctx->capture_free.clear();
+  return TL_OK;
+}
+
+// Ends the open capture; the blocks it handed out become held by `g` (or, when the capture
+// failed, go back to the cache: the caller's, once freed, and those freed during it).
+static void settle_capture_blocks(tl_ctx* ctx, tl_graph* g) {
+  std::unordered_set<void*> freed;
+  for (auto& kv : ctx->capture_free) freed.insert(kv.second);
+  for (void* b : ctx->capture_blocks) {
+    size_t sz = 0;
+    auto lv = ctx->live.find(b);
+    if (lv != ctx->live.end()) sz = lv->second;
+    for (auto& kv : ctx->capture_free)
+      if (kv.second == b) sz = kv.first;
+    if (g) {
+      g->blocks.push_back(b);
+      ctx->graph_block_size[b] = sz;
+      if (freed.count(b)) ctx->graph_released.insert(b);
+    } else if (freed.count(b)) {
+      ctx->free_blocks.emplace(sz, b);
+      ctx->bytes_cached += sz;
+      ctx->bytes_in_use -= sz;
+    }
+  }
+  ctx->capture_blocks.clear();
+  ctx->capture_free.clear();
+}
+
+int tl_graph_end(tl_ctx* ctx, tl_graph** out) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(out, "null output pointer");
+  *out = nullptr;
+  TL_REQUIRE(ctx->capturing, "no graph capture is open on this context");
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+  ctx->capturing = false;
+  hipGraphExec_t exec = nullptr;
+  if (e == hipSuccess && graph) e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess || !graph) {
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    settle_capture_blocks(ctx, nullptr);
+    return fail(TL_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+  }
+  tl_graph* g = new tl_graph();
+  g->graph = graph;
+  g->exec = exec;
+  settle_capture_blocks(ctx, g);
+  ctx->graphs.push_back(g);
+  *out = g;
+  return TL_OK;
+}
+
+int tl_graph_launch(tl_ctx* ctx, tl_graph* g) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(g && std::find(ctx->graphs.begin(), ctx->graphs.end(), g) != ctx->graphs.end(),
+             "not a live graph of this context");
+  TL_REQUIRE(!ctx->capturing, "graph launch during a graph capture");
+  TL_CHECK_HIP(hipGraphLaunch(g->exec, ctx->stream));
+  return TL_OK;
+}
+
+int tl_graph_destroy(tl_ctx* ctx, tl_graph* g) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (!g) return TL_OK;
+  auto it = std::find(ctx->graphs.begin(), ctx->graphs.end(), g);
+  TL_REQUIRE(it != ctx->graphs.end(), "not a live graph of this context");
+  ctx->graphs.erase(it);
+  // replays still queued finish before the executable goes
+  const hipError_t se = hipStreamSynchronize(ctx->stream);
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  // blocks the caller has freed return to the cache (stream order: later users run after
+  // the graph's last queued replay); blocks the caller still holds stay its own
+  for (void* b : g->blocks) {
+    const size_t sz = ctx->graph_block_size[b];
+    ctx->graph_block_size.erase(b);
+    if (ctx->graph_released.erase(b)) {
+      ctx->free_blocks.emplace(sz, b);
+      ctx->bytes_cached += sz;
+      ctx->bytes_in_use -= sz;
+    }
+  }
+  delete g;
+  if (ctx->graphs.empty() && !ctx->ws_retired.empty()) {
+    for (void* w : ctx->ws_retired) (void)hipFree(w);
+    ctx->ws_retired.clear();
+  }
+  if (se != hipSuccess) return fail(TL_ERR_HIP, "stream synchronize: %s", hipGetErrorString(se));
   return check_status_word(ctx);
 }
 

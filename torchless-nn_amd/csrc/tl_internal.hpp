@@ -9,6 +9,7 @@
 #include <map>
 #include <string>
 #include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "libtl.h"
@@ -71,6 +72,33 @@ struct tl_ctx {
   // device address, on this context's device, of the static scratch array behind
   // tl_attention_fwd_noalloc (set by tl_init)
   void* noalloc_scratch = nullptr;
+  // HIP graph capture of the context stream (tl_graph_*). Blocks handed out by tl_malloc
+  // while a capture is open belong to the graph it produces for as long as the graph lives:
+  // its replays write them, so they are not reused even after the caller frees them.
+  bool capturing = false;
+  std::vector<void*> capture_blocks;             // handed out during the open capture
+  std::multimap<size_t, void*> capture_free;     // freed during it (reusable by it only)
+  std::unordered_map<void*, size_t> graph_block_size;  // every block a live graph holds
+  std::unordered_set<void*> graph_released;      // ... that the caller has already freed
+  std::vector<tl_graph*> graphs;                 // live graphs
+  std::vector<void*> ws_retired;                 // workspaces replaced while graphs held them
+  // stream-ordered host -> device copies: pinned staging buffers used round-robin, each
+  // reusable once the copy out of it (an event) has completed
+  struct Staging {
+    void* host = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+  };
+  Staging staging[4];
+  int staging_next = 0;
+};
+
+// A captured graph and the device blocks it holds.
+struct tl_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<void*> blocks;
 };
 
 namespace tl {

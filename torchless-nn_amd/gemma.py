@@ -10,7 +10,7 @@ import numpy as np
 
 import backend
 import tl_hip as xp
-from layers import GemmaBlock, KVCache, RMSNorm
+from layers import DevicePosition, GemmaBlock, KVCache, RMSNorm
 from transformer_adapters import GPTEmbeddingTable, GPTEmbedBack, ScaledEmbedFront
 
 __all__ = ["GEMMA_2B", "GemmaDecoder", "build_gemma", "seed_gemma"]
@@ -59,16 +59,38 @@ class GemmaDecoder:
         return xp.DeviceTensor((B, V), logits.dtype, pitch=T * logits.pitch, buf=logits.buf,
                                offset=logits.offset + (T - 1) * logits.pitch * es)
 
-    def generate_greedy(self, ids, n_new, cache=None, return_logits=False):
+    def decode_step(self, tok, cache, dpos):
+        """One greedy step at the device position dpos: the tokens tok [B] (int64, on the
+        device) sit at position *dpos.pos; their keys and values go into the cache there and
+        tok is overwritten with the argmax of the next-token logits, which are returned
+        [B, 1, V]. Makes no host round trip, so it can be captured in a graph."""
+        B = tok.size
+        dpos.refresh()
+        x = self.front.forward(tok.reshape(B, 1))
+        for i, blk in enumerate(self.blocks):
+            x = blk.forward(x, cache, i, dpos)
+        logits = self.back.forward(self.final_norm.forward(x))
+        xp.argmax(self.last_rows(logits), out=tok)
+        return logits
+
+    def generate_greedy(self, ids, n_new, cache=None, return_logits=False, graph=True):
         """Prefill `ids` [B, T] into a KV cache, then take `n_new` greedy steps, each feeding
         the device argmax of the last logits row back as the next token. Returns the new
         token ids [B, n_new] as a host int64 array (and, if asked, the per-step last-row
-        logits [n_new, B, V] as float32: step 0 from the prefill)."""
+        logits [n_new, B, V] as float32: step 0 from the prefill).
+
+        With graph=True (no logits asked for, and a model the fused attention kernel takes:
+        bf16) the first decode step runs eagerly at a device position, the next is captured
+        as one HIP graph (position advance and token record included) and replayed for the
+        rest, so each step is one host call; the ids are the same as without."""
         if not isinstance(ids, xp.DeviceTensor):
             ids = xp.array(np.asarray(ids))
         B, T = ids.shape
         if cache is None:
             cache = self.new_cache(B, T + n_new)
+        if (graph and not return_logits and n_new >= 2
+                and xp.attention_supported(self.dtype, self.cfg["head_dim"], cache.capacity)):
+            return self._generate_graph(ids, n_new, cache)
         logits = self.forward(ids, cache, 0)
         steps, kept = [], []
         for t in range(n_new):
@@ -81,6 +103,36 @@ class GemmaDecoder:
                 logits = self.forward(nxt.reshape(B, 1), cache, T + t)
         out = np.stack([s.get() for s in steps], axis=1) if steps else np.zeros((B, 0), np.int64)
         return (out, np.stack(kept)) if return_logits else out
+
+    def _generate_graph(self, ids, n_new, cache):
+        B, T = ids.shape
+        if T + n_new - 1 > cache.capacity:
+            raise ValueError("KV cache too small")
+        c = self.cfg
+        logits = self.forward(ids, cache, 0)
+        tok = xp.empty((B,), xp.int64)
+        xp.argmax(self.last_rows(logits), out=tok)
+        del logits
+        hist = xp.empty((B, n_new), xp.int64)  # column j: the token at position T + j
+        dpos = DevicePosition(T, 1, c["head_dim"], c.get("rope_base", 10000.0))
+        xp.ids_append(tok, hist, dpos.pos, T)
+
+        def step():
+            self.decode_step(tok, cache, dpos)
+            dpos.advance(1)
+            xp.ids_append(tok, hist, dpos.pos, T)
+
+        step()  # eager: creates what later steps reuse (packed weights, workspace)
+        if n_new > 2:
+            with xp.capture() as g:
+                step()
+            try:
+                for _ in range(n_new - 2):
+                    g.launch()
+            finally:
+                g.destroy()
+        cache.length = T + n_new - 1
+        return hist.get()
 
 
 def build_gemma(cfg, dtype=None):

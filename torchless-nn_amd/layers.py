@@ -26,7 +26,7 @@ from activations import act_code_of
 
 __all__ = ["Dense", "Dropout", "MultiHeadAttention", "TransformerFeedForward", "LayerNorm",
            "RMSNorm", "TransformerBlock", "linear", "KVCache", "MultiQueryAttention",
-           "GeGLUFeedForward", "GemmaBlock"]
+           "GeGLUFeedForward", "GemmaBlock", "DevicePosition"]
 
 
 def _round_up(n, m):
@@ -337,6 +337,27 @@ def _rope_table(T, D, base, pos0):
     return t
 
 
+class DevicePosition:
+    """The position of a decode step kept in device memory (one int64) together with the
+    RoPE table of the step's T positions, so a step captured in a graph replays at the
+    current position: `refresh()` recomputes the table from the device value and
+    `advance(n)` adds n on the device, both stream-ordered."""
+
+    def __init__(self, start, T, head_dim, base=10000.0):
+        self.pos = xp.array(np.array([start], np.int64))
+        self.T, self.head_dim, self.base = int(T), int(head_dim), float(base)
+        self.table = xp.empty((2, self.T, self.head_dim // 2), xp.float32)
+
+    def refresh(self):
+        xp.rope_table_dev(self.table, self.pos, self.base)
+
+    def advance(self, n=1):
+        xp.i64_add(self.pos, n)
+
+    def get(self):
+        return int(self.pos.get()[0])
+
+
 class KVCache:
     """Per-layer keys [B, Hkv, L, D] and transposed values [B, Hkv, D, L] in HBM, L a
     multiple of 8; positions at or past the valid length are never read as values."""
@@ -378,6 +399,8 @@ class MultiQueryAttention(Layer):
         return self._forward(input, None, cache, layer, pos0)
 
     def _forward(self, input, residual, cache=None, layer=0, pos0=0):
+        if isinstance(pos0, DevicePosition):
+            return self._forward_dev(input, residual, cache, layer, pos0)
         self.input = input
         B, T, C = input.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.heads_dim
@@ -407,6 +430,33 @@ class MultiQueryAttention(Layer):
                          causal=True, offset=pos0, seq_k=Tk)
         else:
             self._unfused(q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt, divisor, pos0)
+        out = linear(heads.reshape(B * T, Hq * D), self.out_weights,
+                     residual=(residual.reshape(B * T, C) if residual is not None else None))
+        self.output = out.reshape(B, T, C)
+        return self.output
+
+    def _forward_dev(self, input, residual, cache, layer, dpos):
+        """Decode at a device position (what a captured step replays): the same kernels and
+        arithmetic as the host-position call, with the cache row, the RoPE positions and the
+        attended key count read from dpos.pos on the device. The caller keeps the position
+        below the cache capacity (rows past it are neither written nor read)."""
+        self.input = input
+        B, T, C = input.shape
+        Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.heads_dim
+        if cache is None:
+            raise ValueError("decoding at a device position needs a KV cache")
+        if dpos.T != T or dpos.head_dim != D or dpos.base != self.rope_base:
+            raise ValueError("the device position's RoPE table does not match this call")
+        dt = input.dtype
+        if not (self.fused and xp.attention_supported(dt, D, cache.capacity)):
+            raise ValueError("decoding at a device position needs the fused attention kernel")
+        q = xp.empty((B, Hq, T, D), dt)
+        k, vt, L = cache.k[layer], cache.vt[layer], cache.capacity
+        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, dpos.pos))
+        xp.rope2_dev(q, k, dpos.table, dpos.pos)
+        heads = xp.empty((B, T, Hq * D), dt)
+        xp.attention_decode_dev(q, k, vt, heads, dpos.pos, n_heads_q=Hq, n_heads_kv=Hkv,
+                                divisor=float(np.float32(D ** 0.5)))
         out = linear(heads.reshape(B * T, Hq * D), self.out_weights,
                      residual=(residual.reshape(B * T, C) if residual is not None else None))
         self.output = out.reshape(B, T, C)

@@ -131,6 +131,7 @@ class _GemmDesc(ctypes.Structure):
         ("n_heads_kv", ctypes.c_int64), ("head_dim", ctypes.c_int64),
         ("kv_len", ctypes.c_int64), ("kv_pos0", ctypes.c_int64),
         ("family", ctypes.c_int32), ("tile", ctypes.c_int32),
+        ("kv_pos0_dev", ctypes.c_void_p),
     ]
 
 
@@ -181,6 +182,16 @@ SIGNATURES = {
                          _F32, _I32, _I64, _I32],
     "tl_attention_fwd_noalloc": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                  _I64, _F32, _I32, _I64, _I32],
+    "tl_attention_decode_dev": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32,
+                                _I64, _P, _I32],
+    "tl_graph_begin": [_P],
+    "tl_graph_end": [_P, ctypes.POINTER(_P)],
+    "tl_graph_launch": [_P, _P],
+    "tl_graph_destroy": [_P, _P],
+    "tl_rope_table_dev": [_P, _P, _I64, _I64, _F64, _P],
+    "tl_rope2_dev": [_P, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I32],
+    "tl_i64_add": [_P, _P, _I64],
+    "tl_ids_append": [_P, _P, _P, _I64, _I64, _I64, _P, _I64],
 }
 _RESTYPES = {"tl_last_error": ctypes.c_char_p}
 
@@ -500,13 +511,18 @@ def asnumpy(t) -> np.ndarray:
     return t.get() if isinstance(t, DeviceTensor) else np.asarray(t)
 
 
-def argmax(t: DeviceTensor, axis=-1) -> DeviceTensor:
-    """First index of the maximum along the last axis, int64 (reference network.py:135, 158)."""
+def argmax(t: DeviceTensor, axis=-1, out=None) -> DeviceTensor:
+    """First index of the maximum along the last axis, int64 (reference network.py:135, 158).
+    `out`, if given, is a contiguous int64 tensor with one element per row."""
     if axis not in (-1, t.ndim - 1):
         raise NotImplementedError("argmax is implemented over the last axis")
-    out = DeviceTensor(t.shape[:-1] if t.ndim > 1 else (1,), int64)
+    if out is None:
+        out = DeviceTensor(t.shape[:-1] if t.ndim > 1 else (1,), int64)
+    elif out.dtype is not int64 or out.size != t.nrows or not out.contiguous:
+        raise ValueError("argmax out must be a contiguous int64 tensor, one element per row")
     c = ctx()
     check(c.lib.tl_argmax(c.handle, t.ptr, t.nrows, t.ncols, t.pitch, t.dtype.code, out.ptr))
+    _wrote(out)
     return out
 
 
@@ -556,9 +572,15 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
          out_dtype=None, batch=1, batch_inner=1, sa=(0, 0), sb=(0, 0), sc=(0, 0), bias=None,
          residual=None, ldr=0, sr=(0, 0), act=TL_ACT_NONE, divisor=1.0, qkv=None,
          family="gemm_mfma", tile="auto", geglu=False):
+    """One tl_gemm call. qkv = (q, k, vt, T, Hq, Hkv, D[, kv_len, kv_pos0]) selects the
+    split epilogue; kv_pos0 may be a one-element int64 DeviceTensor (the cache position
+    read on the device when the kernel runs)."""
+    pos_dev = None
     if qkv is not None:
         q, k, vt, T, Hq, Hkv, Dh = qkv[:7]
         kv_len, kv_pos0 = (qkv[7], qkv[8]) if len(qkv) > 7 else (0, 0)
+        if isinstance(kv_pos0, DeviceTensor):
+            pos_dev, kv_pos0 = _position_ptr(kv_pos0), 0
         epi, qp, kp, vp = TL_EPI_QKV_SPLIT, q.ptr, k.ptr, vt.ptr
     else:
         epi = TL_EPI_GEGLU if geglu else TL_EPI_STORE
@@ -573,7 +595,7 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
                   bias.ptr if bias is not None else None,
                   residual.ptr if residual is not None else None, ldr, sr[0], sr[1],
                   act, float(divisor), epi, qp, kp, vp, T, Hq, Hkv, Dh, kv_len, kv_pos0,
-                  KFAMILY[family], GEMM_TILES[tile])
+                  KFAMILY[family], GEMM_TILES[tile], pos_dev)
     lib_, h = _c()
     check(lib_.tl_gemm(h, ctypes.byref(d)))
     if qkv is not None:
@@ -728,6 +750,122 @@ def attention(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTen
                                 Lk, q.dtype.code))
     _wrote(out)
     return out
+
+
+def _position_ptr(pos: DeviceTensor):
+    if pos.dtype is not int64 or pos.size != 1:
+        raise ValueError("a device position is a one-element int64 tensor")
+    return pos.ptr
+
+
+def attention_decode_dev(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTensor,
+                         pos: DeviceTensor, *, n_heads_q, n_heads_kv, divisor):
+    """Causal decode attention at a device position: q [B, Hq, Tq, D] at positions
+    *pos .. *pos + Tq - 1 over the cache k [B, Hkv, L, D] / vt [B, Hkv, D, L]."""
+    B, Hq, Tq, D = q.shape
+    lib_, h = _c()
+    check(lib_.tl_attention_decode_dev(h, q.ptr, k.ptr, vt.ptr, out.ptr, B, n_heads_q,
+                                       n_heads_kv, Tq, D, out.pitch, float(divisor), k.shape[2],
+                                       _position_ptr(pos), q.dtype.code))
+    _wrote(out)
+    return out
+
+
+def rope_table_dev(table: DeviceTensor, pos: DeviceTensor, base=10000.0) -> DeviceTensor:
+    """Fill `table` [2, T, D/2] (float32) with cos/sin of positions *pos .. *pos + T - 1."""
+    _, T, half = table.shape
+    lib_, h = _c()
+    check(lib_.tl_rope_table_dev(h, table.ptr, T, 2 * half, float(base), _position_ptr(pos)))
+    _wrote(table)
+    return table
+
+
+def rope2_dev(x1: DeviceTensor, cache: DeviceTensor, table: DeviceTensor, pos: DeviceTensor):
+    """In place: rotate x1 [.., T, D] by the table's T positions, and the same T rows of
+    every sequence of `cache` [.., L, D] starting at row *pos."""
+    if x1.dtype is not cache.dtype or not (x1.contiguous and cache.contiguous):
+        raise ValueError("rope2_dev needs contiguous operands of one dtype")
+    T, D = x1.shape[-2], x1.shape[-1]
+    L = cache.shape[-2]
+    if cache.shape[-1] != D or table.shape[1] != T:
+        raise ValueError("rope2_dev operands disagree on T or D")
+    lib_, h = _c()
+    check(lib_.tl_rope2_dev(h, x1.ptr, x1.size // (T * D), T * D, cache.ptr,
+                            cache.size // (L * D), L * D, L, table.ptr, T, D,
+                            _position_ptr(pos), x1.dtype.code))
+    _wrote(x1, cache)
+    return x1
+
+
+def i64_add(x: DeviceTensor, delta: int):
+    """x[0] += delta on the device (stream-ordered)."""
+    lib_, h = _c()
+    check(lib_.tl_i64_add(h, _position_ptr(x), int(delta)))
+    _wrote(x)
+
+
+def ids_append(ids: DeviceTensor, hist: DeviceTensor, pos: DeviceTensor, pos_base: int):
+    """hist[r, *pos - pos_base] = ids[r] when that column is inside hist [rows, cols]."""
+    rows, cols = hist.shape
+    if ids.dtype is not int64 or hist.dtype is not int64 or ids.size != rows:
+        raise ValueError("ids_append takes int64 ids [rows] and history [rows, cols]")
+    lib_, h = _c()
+    check(lib_.tl_ids_append(h, ids.ptr, hist.ptr, rows, hist.pitch, cols, _position_ptr(pos),
+                             int(pos_base)))
+    _wrote(hist)
+
+
+class Graph:
+    """A captured sequence of this module's calls on the context stream, replayed with one
+    launch. Use as `with xp.capture() as g: <calls>`, then `g.launch()`. The calls in the
+    block are recorded, not run; tensors allocated inside are written on every replay."""
+
+    def __init__(self, handle):
+        self._handle, self._ctx = handle, ctx()
+
+    def launch(self):
+        if not self._handle:
+            raise TLError(TL_ERR_INVALID, "graph was destroyed")
+        check(self._ctx.lib.tl_graph_launch(self._ctx.handle, self._handle))
+
+    def destroy(self):
+        if self._handle:
+            h, self._handle = self._handle, None
+            check(self._ctx.lib.tl_graph_destroy(self._ctx.handle, h))
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class capture:  # noqa: N801  (used as a context manager, like torch.cuda.graph)
+    """with capture() as g: ... -- records the calls of the block into a Graph `g.graph`."""
+
+    def __enter__(self):
+        c = ctx()
+        check(c.lib.tl_graph_begin(c.handle))
+        self.graph = None
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        c = ctx()
+        h = ctypes.c_void_p()
+        rc = c.lib.tl_graph_end(c.handle, ctypes.byref(h))
+        if exc_type is None:
+            check(rc)
+            self.graph = Graph(h.value)
+        elif rc == TL_OK:
+            c.lib.tl_graph_destroy(c.handle, h.value)
+        return False
+
+    def launch(self):
+        self.graph.launch()
+
+    def destroy(self):
+        if self.graph is not None:
+            self.graph.destroy()
 
 
 def attention_supported(dtype, head_dim, kv_capacity) -> bool:
