@@ -377,7 +377,7 @@ def decode_sweep(xp, reps=50):
     x, h = dev((B, C), 1.0), dev((B, F), 1.0)
     res = dev((B, C), 1.0)
     w = {"qkv": dev((10 * D, C)), "out": dev((C, C)), "geglu": dev((2 * F, C)),
-         "down": dev((C, F)), "head": dev((V, C))}
+         "down": dev((C, F)), "head": dev((V, C)), "down_pad": dev((C, F + 64))}
     q, k, vt = (xp.empty((B, Hq, 1, D), "bf16"), dev((B, 1, L, D), 1.0), dev((B, 1, D, L), 1.0))
     outc, outf = xp.empty((B, C), "bf16"), xp.empty((B, F), "bf16")
     logits = xp.empty((B, V), "bf16", pitch=V)
@@ -395,6 +395,20 @@ def decode_sweep(xp, reps=50):
                                  C=outc, ldc=C, residual=res, ldr=C), 2 * C * F),
         "head": (lambda: xp.gemm(x, w["head"], M=B, N=V, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
                                  C=logits, ldc=V), 2 * V * C),
+        # the same products with the RMSNorm's row scaling folded in, and the down projection with its
+        # weight rows padded off the 32 KiB pitch
+        "qkv_norm": (lambda: xp.gemm(x, w["qkv"], M=B, N=10 * D, K=C, lda=C, ldb=C,
+                                     b_layout=xp.TL_B_NK, qkv=(q, k, vt, 1, Hq, 1, D, L, 2100),
+                                     norm_eps=1e-6), 2 * 10 * D * C),
+        "geglu_norm": (lambda: xp.gemm(x, w["geglu"], M=B, N=2 * F, K=C, lda=C, ldb=C,
+                                       b_layout=xp.TL_B_NK, C=outf, ldc=F, act=xp.TL_ACT_GELU,
+                                       geglu=True, norm_eps=1e-6), 2 * 2 * F * C),
+        "head_norm": (lambda: xp.gemm(x, w["head"], M=B, N=V, K=C, lda=C, ldb=C,
+                                      b_layout=xp.TL_B_NK, C=logits, ldc=V,
+                                      norm_eps=1e-6), 2 * V * C),
+        "down_pad": (lambda: xp.gemm(h, w["down_pad"], M=B, N=C, K=F, lda=F, ldb=F + 64,
+                                     b_layout=xp.TL_B_NK, C=outc, ldc=C, residual=res, ldr=C),
+                     2 * C * F),
         "rmsnorm_4x2048": (lambda: xp.rmsnorm(x, gam, np.float32(1e-6), 1.0, out=xn), 2 * 2 * B * C),
         "attention": (lambda: xp.attention(q, k, vt, heads, n_heads_q=Hq, n_heads_kv=1,
                                            divisor=16.0, causal=True, offset=Tk - 1, seq_k=Tk),

@@ -141,6 +141,12 @@ typedef struct tl_gemm_desc {
                                            memory read at run time in place of kv_pos0 (a
                                            captured graph writes the cache at the current
                                            position); rows past kv_len are not written */
+  int32_t norm_rows;                    /* nonzero: row m of the product is multiplied by
+                                           1 / sqrt(mean_k A[m, k]^2 + norm_eps) before the
+                                           epilogue; with an RMSNorm's gain folded into B's
+                                           K index that is RMSNorm(A) @ B (unbatched bf16,
+                                           M <= 16, B as [N, K] only) */
+  float norm_eps;
 } tl_gemm_desc;
 
 /* ---- runtime ------------------------------------------------------------------------ */
@@ -211,6 +217,12 @@ int tl_random_normal(tl_ctx* ctx, void* y, int64_t n, uint64_t seed, uint64_t st
 /* y[c*ldy + r] = x[r*ldx + c]: weight pre-packing into the K-contiguous GEMM layout. */
 int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t ldy, int32_t dtype);
+/* y[c, r] = x[r, c] * (gain_offset + gain[r]) (float types; gain has `rows` elements): the
+ * transpose that packs a [K, N] weight as [N, K] with an RMSNorm's gain folded into K, for
+ * products that take the norm as row scaling (tl_gemm_desc.norm_rows). */
+int tl_transpose2d_gain(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                        int64_t ldx, int64_t ldy, const void* gain, float gain_offset,
+                        int32_t dtype);
 /* ViT patch extraction, reference transformer_adapters.py:39-47 (VitProjector.forward's
  * reshape / transpose(0,2,4,3,5,1) / reshape): x [B, C, H, W] -> y [B, (H/ph)(W/pw),
  * ph*pw*C], token i*(W/pw) + j, features ordered (row in patch, column in patch, channel).
@@ -304,12 +316,15 @@ int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* vt, 
  * sits at position *pos + t and keys 0 .. *pos + seq_q - 1 of the cache (capacity
  * kv_capacity, at most that many) are attended to, with *pos an int64 read from device
  * memory when the kernels run, so a captured decode step replays at the current position.
- * Otherwise as tl_attention_fwd. No reference counterpart (the reference recomputes the
- * window every step, demo.ipynb:1526-1533). */
-int tl_attention_decode_dev(tl_ctx* ctx, const void* q, const void* k, const void* vt, void* out,
+ * Otherwise as tl_attention_fwd. With rope_table (float [2, seq_q, head_dim/2]: cos then
+ * sin of positions *pos ..; head_dim >= 64), q and the cache keys at positions *pos ..
+ * *pos + seq_q - 1 are taken unrotated: the kernel applies rotate-half RoPE to both and
+ * writes the rotated keys back into k. No reference counterpart (the reference recomputes
+ * the window every step, demo.ipynb:1526-1533). */
+int tl_attention_decode_dev(tl_ctx* ctx, const void* q, void* k, const void* vt, void* out,
                             int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                             int64_t head_dim, int64_t ld_out, float divisor, int64_t kv_capacity,
-                            const int64_t* pos, int32_t dtype);
+                            const int64_t* pos, const void* rope_table, int32_t dtype);
 /* tl_attention_fwd that allocates nothing: the same arguments, kernels and results, with the
  * decode path's partial results (at most 16 query rows per kv head) kept in a static device
  * array of 16 MiB instead of the context's grow-only workspace, and the launch kept out of the

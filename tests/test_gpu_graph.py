@@ -68,6 +68,57 @@ def test_attention_decode_dev_matches_host_offset(tl, cfg):
         assert np.array_equal(_bits(got), _bits(want)), (cfg, pos)
 
 
+def _attn64(q, k, v, Hq, Hkv, pos):
+    """float64 causal attention of q [B, Hq, Tq, D] at positions pos .. over keys k
+    [B, Hkv, >= pos + Tq, D] and values v [B, Hkv, D, >= pos + Tq] -> [B, Tq, Hq * D]."""
+    B, _, Tq, D = q.shape
+    g = Hq // Hkv
+    out = np.zeros((B, Tq, Hq * D))
+    for b in range(B):
+        for h in range(Hq):
+            kk = k[b, h // g].astype(np.float64)
+            vv = v[b, h // g].astype(np.float64)
+            for t in range(Tq):
+                n = pos + t + 1
+                sc = kk[:n] @ q[b, h, t].astype(np.float64) / np.sqrt(D)
+                e = np.exp(sc - sc.max())
+                out[b, t, h * D:(h + 1) * D] = vv[:, :n] @ (e / e.sum())
+    return out
+
+
+@pytest.mark.parametrize("cfg", [(4, 8, 1, 256, 2176, 1), (2, 4, 2, 64, 264, 2),
+                                 (1, 8, 1, 128, 1024, 2), (3, 4, 4, 64, 40, 1)])
+def test_attention_decode_fused_rope(tl, cfg):
+    """Decode attention taking unrotated queries and new cache keys with the RoPE table: the
+    new keys are rotated in the cache (within rounding of the oracle's RoPE; no other row
+    touched) and the output matches float64 attention over the oracle-rotated operands."""
+    from oracle import numpy_ref as ref
+    xp = tl["xp"]
+    B, Hq, Hkv, D, L, Tq = cfg
+    rng = np.random.default_rng(B * 7 + D + Tq)
+    qh = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
+    kh = ref.round_bf16(rng.standard_normal((B, Hkv, L, D)).astype(F32))
+    vh = ref.round_bf16(rng.standard_normal((B, Hkv, D, L)).astype(F32))
+    for pos in (0, 63, L - Tq):
+        q = xp.array(qh, dtype="bf16")
+        k = xp.array(kh, dtype="bf16")
+        vt = xp.array(vh, dtype="bf16")
+        out = xp.empty((B, Tq, Hq * D), xp.bfloat16)
+        table = xp.rope_table(Tq, D, 10000.0, pos)
+        xp.attention_decode_dev(q, k, vt, out, _pos(xp, pos), n_heads_q=Hq, n_heads_kv=Hkv,
+                                divisor=float(np.float32(D ** 0.5)), rope=table)
+        c, s = ref.rope_table(Tq, D, 10000.0, pos)
+        knew = ref.round_bf16(ref.rope(kh[:, :, pos:pos + Tq], c, s))
+        got_k = k.get()
+        assert ref.max_rel(got_k[:, :, pos:pos + Tq], knew) <= 1e-2, pos
+        assert np.array_equal(got_k[:, :, :pos], kh[:, :, :pos])
+        assert np.array_equal(got_k[:, :, pos + Tq:], kh[:, :, pos + Tq:])
+        kr = kh.copy()
+        kr[:, :, pos:pos + Tq] = knew
+        want = _attn64(ref.round_bf16(ref.rope(qh, c, s)), kr, vh, Hq, Hkv, pos)
+        assert ref.max_rel(out.get(), want) <= 2e-2, pos
+
+
 def test_attention_decode_dev_refuses_prefill_shapes(tl):
     xp = tl["xp"]
     q = xp.zeros((1, 8, 4, 64), xp.bfloat16)  # 8 heads x 4 rows share one kv head: 32 rows

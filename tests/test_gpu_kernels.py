@@ -709,6 +709,52 @@ def test_gemm_gated_staged(xp, tile, mnk):
         assert np.all(got[:, F:] == 7.0), (tile, mnk, act)
 
 
+@pytest.mark.parametrize("mnk", [(4, 2560, 2048), (3, 300, 776), (16, 1000, 64), (1, 8, 8)])
+def test_gemm_skinny_rms_row_scaling(xp, mnk):
+    """An RMSNorm folded into a decode product: the gain packed into the weight with
+    tl_transpose2d_gain and the product's rows scaled by 1 / rms(a). act(RMSNorm(a) @ w +
+    bias) + residual for gain offsets 1 (Gemma's (1 + gamma)) and 0, the gated and QKV
+    epilogues, against the oracle's norm then product; a tall product refuses it."""
+    M, N, K = mnk
+    rng = np.random.default_rng(M + N + K + 5)
+    a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32) * 3)
+    w = ref.round_bf16(rng.standard_normal((K, N)).astype(F32) / np.sqrt(K))
+    g = ref.round_bf16(rng.standard_normal(K).astype(F32) * 0.5)
+    bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+    res = ref.round_bf16(rng.standard_normal((M, N)).astype(F32))
+    dw, dg = up(xp, w, "bf16"), up(xp, g, "bf16")
+    for off in (1.0, 0.0):
+        packed = xp.transpose2d_gain(dw, dg, off)
+        assert np.array_equal(packed.get(), ref.round_bf16(w.T * (F32(off) + g)[None, :])), off
+        out = xp.empty((M, N), "bf16")
+        xp.gemm(up(xp, a, "bf16"), packed, M=M, N=N, K=K, lda=K, ldb=K,
+                b_layout=xp.TL_B_NK, C=out, ldc=N, bias=up(xp, bias, "bf16"),
+                act=xp.TL_ACT_SILU, residual=up(xp, res, "bf16"), ldr=N, norm_eps=1e-6)
+        want = gemm_ref(ref.rmsnorm(a, g, F32(1e-6), off), w, bias, "silu", res)
+        assert ref.max_rel(out.get(), want) <= 2e-2, (mnk, off)
+    packed = xp.transpose2d_gain(dw, dg, 1.0)
+    t = gemm_ref(ref.rmsnorm(a, g, F32(1e-6), 1.0), w)
+    if N % 2 == 0:
+        h = xp.empty((M, N // 2), "bf16")
+        xp.gemm(up(xp, a, "bf16"), packed, M=M, N=N, K=K, lda=K, ldb=K,
+                b_layout=xp.TL_B_NK, C=h, ldc=N // 2, act=xp.TL_ACT_GELU, geglu=True,
+                norm_eps=1e-6)
+        assert ref.max_rel(h.get(), ref.gelu(t[:, 0::2]) * t[:, 1::2]) <= 2e-2, mnk
+    if N % 40 == 0:  # (Hq + 2 Hkv) D with D = N / 10: 8 query heads, one kv head
+        D, L, pos = N // 10, 24, 5
+        q = xp.empty((M, 8, 1, D), "bf16")
+        k, vt = xp.zeros((M, 1, L, D), "bf16"), xp.zeros((M, 1, D, L), "bf16")
+        xp.gemm(up(xp, a, "bf16"), packed, M=M, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK,
+                qkv=(q, k, vt, 1, 8, 1, D, L, pos), norm_eps=1e-6)
+        assert ref.max_rel(q.get()[:, :, 0].reshape(M, 8 * D), t[:, :8 * D]) <= 2e-2
+        assert ref.max_rel(k.get()[:, 0, pos], t[:, 8 * D:9 * D]) <= 2e-2
+        assert ref.max_rel(vt.get()[:, 0, :, pos], t[:, 9 * D:]) <= 2e-2
+    tall = xp.zeros((17, K), "bf16")
+    with pytest.raises(xp.TLError):
+        xp.gemm(tall, packed, M=17, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK,
+                C=xp.empty((17, N), "bf16"), ldc=N, norm_eps=1e-6)
+
+
 def test_gemm_skinny_rejects_tall(xp):
     a = xp.zeros((17, 64), "bf16")
     w = xp.zeros((32, 64), "bf16")

@@ -51,7 +51,27 @@ struct AttnParams {
   // decode with a device position: when set, query t sits at *pos_dev + t and keys
   // 0 .. *pos_dev + Tq - 1 (at most Lk) are valid; Tk and offset are read from it at run time
   const int64_t* pos_dev;
+  // decode only: the rotate-half RoPE table [2, Tq, D/2] (cos, sin) of positions offset ..
+  // offset + Tq - 1. When set, the decode kernel rotates the queries and this call's new
+  // cache keys (positions offset ..) itself and writes the rotated keys back to the cache.
+  const float* rope;
 };
+
+// Rotate-half RoPE of 8 consecutive elements a (index d < D/2) and their partners b
+// (index d + D/2) with cos c and sin s, in fp32 and rounded to bf16 as a separate RoPE pass
+// would store them.
+__device__ __forceinline__ void rope8(bf16x8& a, bf16x8& b, const float* c, const float* s) {
+  const float4 c0 = *reinterpret_cast<const float4*>(c), c1 = *reinterpret_cast<const float4*>(c + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(s), s1 = *reinterpret_cast<const float4*>(s + 4);
+  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float fa = (float)a[e], fb = (float)b[e];
+    a[e] = (__bf16)(fa * cv[e] - fb * sv[e]);
+    b[e] = (__bf16)(fb * cv[e] + fa * sv[e]);
+  }
+}
 
 template <int D>
 __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
@@ -546,6 +566,17 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
     for (int ks = 0; ks < KS; ++ks)
       qf[ks] = rowok ? *reinterpret_cast<const bf16x8*>(qrow + 32 * ks) : zero;
   }
+  // fused RoPE (D >= 64): element d = 32 ks + 8 grp + e of qf[ks] has its partner d + D/2 in
+  // qf[ks + KS/2] of the same lane
+  constexpr int KH = KS / 2;
+  if constexpr (KH > 0) {
+    if (p.rope && rowok) {
+      const float* cs = p.rope + (int64_t)t * (D / 2) + 8 * grp;
+      const float* sn = cs + (int64_t)p.Tq * (D / 2);
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) rope8(qf[ks], qf[ks + KH], cs + 32 * ks, sn + 32 * ks);
+    }
+  }
   const bf16_t* kh = p.k + (int64_t)bh * p.Lk * D;
   const bf16_t* vh = p.vt + (int64_t)bh * D * p.Lk;
   const int kc0 = (blockIdx.x * NW + wave) * KPW;
@@ -578,6 +609,28 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
       if (inb && kb + 4 > p.Tk) vb = keep_first4(vb, p.Tk - kb);
       vfa[hp][dt] = va;
       vfb[hp][dt] = vb;
+    }
+  }
+  // fused RoPE of this call's new keys (positions offset .. offset + Tq - 1): the one lane
+  // group holding such a key rotates it and writes it back to the cache for later steps
+  if constexpr (KH > 0) {
+    if (p.rope) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int key = kc0 + 16 * j + col;
+        const int64_t tn = (int64_t)key - p.offset;
+        if (key < p.Tk && tn >= 0 && tn < p.Tq) {
+          const float* cs = p.rope + tn * (D / 2) + 8 * grp;
+          const float* sn = cs + (int64_t)p.Tq * (D / 2);
+          bf16_t* krow = const_cast<bf16_t*>(kh) + (int64_t)key * D + 8 * grp;
+#pragma unroll
+          for (int ks = 0; ks < KH; ++ks) {
+            rope8(kf[j][ks], kf[j][ks + KH], cs + 32 * ks, sn + 32 * ks);
+            *reinterpret_cast<bf16x8*>(krow + 32 * ks) = kf[j][ks];
+            *reinterpret_cast<bf16x8*>(krow + 32 * (ks + KH)) = kf[j][ks + KH];
+          }
+        }
+      }
     }
   }
 
@@ -782,7 +835,8 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
                          int64_t batch, int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                          int64_t seq_k, int64_t head_dim, int64_t ld_out, int64_t offset,
                          float divisor, int32_t causal, int64_t kv_capacity, int32_t dtype,
-                         bool noalloc, const int64_t* pos_dev = nullptr) {
+                         bool noalloc, const int64_t* pos_dev = nullptr,
+                         const float* rope = nullptr) {
   int rc = enter(ctx);
   if (rc) return rc;
   TL_REQUIRE(q && k && vt && out, "null pointer");
@@ -810,6 +864,11 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
   p.ld_out = ld_out; p.offset = offset; p.causal = causal ? 1 : 0;
   p.scale_log2 = 1.4426950408889634f / divisor;
   p.pos_dev = pos_dev;
+  p.rope = rope;
+  if (rope) {
+    TL_REQUIRE(head_dim >= 64 && (n_heads_q / n_heads_kv) * seq_q <= 16 && causal && ((uintptr_t)rope & 15u) == 0,
+               "fused RoPE is implemented for causal decode at head_dim >= 64 (16-byte aligned table)");
+  }
   if (pos_dev) {
     TL_REQUIRE((uintptr_t)pos_dev % 8 == 0 && causal, "device positions need causal decode");
     if ((n_heads_q / n_heads_kv) * seq_q > 16)
@@ -898,17 +957,19 @@ extern "C" int tl_attention_fwd(tl_ctx* ctx, const void* q, const void* k, const
                        ld_out, offset, divisor, causal, kv_capacity, dtype, false);
 }
 
-extern "C" int tl_attention_decode_dev(tl_ctx* ctx, const void* q, const void* k,
+extern "C" int tl_attention_decode_dev(tl_ctx* ctx, const void* q, void* k,
                                        const void* vt, void* out, int64_t batch,
                                        int64_t n_heads_q, int64_t n_heads_kv, int64_t seq_q,
                                        int64_t head_dim, int64_t ld_out, float divisor,
-                                       int64_t kv_capacity, const int64_t* pos, int32_t dtype) {
+                                       int64_t kv_capacity, const int64_t* pos,
+                                       const void* rope_table, int32_t dtype) {
   if (!pos) {
     (void)enter(ctx);
     return fail(TL_ERR_INVALID, "null position");
   }
   return attention_fwd(ctx, q, k, vt, out, batch, n_heads_q, n_heads_kv, seq_q, kv_capacity,
-                       head_dim, ld_out, 0, divisor, 1, kv_capacity, dtype, false, pos);
+                       head_dim, ld_out, 0, divisor, 1, kv_capacity, dtype, false, pos,
+                       (const float*)rope_table);
 }
 
 extern "C" int tl_attention_fwd_noalloc(tl_ctx* ctx, const void* q, const void* k,

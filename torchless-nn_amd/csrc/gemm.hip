@@ -55,6 +55,11 @@ struct GemmParams {
   int geglu;    // gated epilogue: C[m, n/2] = act(acc[m, n]) * acc[m, n+1]
   int tiles_m, tiles_n, group_m;
   FastDiv div_T, div_Dh;
+  // RMS row scaling (skinny kernel): the product of row m is multiplied by
+  // 1 / sqrt(sum_k A[m, k]^2 / K + norm_eps) before the epilogue, which with the norm's gain
+  // folded into B makes it RMSNorm(A) @ B
+  int norm_rows;
+  float norm_eps;
 };
 
 // Global-memory access through an address-space-1 pointer. The epilogue's pointers come
@@ -1216,12 +1221,25 @@ void gemm_dma_persistent_kernel(GemmParams p) {
 // first operand: lane holds out[m = lane % 16][n0 + 4 (lane / 16) + 0..3]. U steps are in
 // flight per wave. The NW partial sums meet in LDS and the first wave runs the same
 // epilogue as the fp32 kernel (bias, activation, residual, QKV scatter, gated pairs).
+//
+// With norm_rows set (NORM), each step also multiplies the A fragment by itself on the
+// matrix cores (X X^T, one more MFMA per 32-wide step, no vector ALU work): its diagonal is
+// each row's sum of squares, and the reduced sums are scaled by 1 / sqrt(mean + eps). With
+// the norm's gain folded into B, that is RMSNorm(A) @ B without a separate pass over A.
+// (Scaling the A fragments by the gain on the vector ALUs instead cost more than the norm's
+// own launch: every workgroup repeats that work, 2048 times for the GeGLU product.)
+//
 // When there are too few 16-row blocks to fill the GPU, K is also split over gridDim.y
 // workgroups: each writes its partial block (64 lanes x 4 floats) to `part`, and
 // gemm_skinny_reduce_kernel, the next launch on the stream, sums them and runs the epilogue.
-template <typename TO, int NW, int U>
+// (Letting the last-arriving workgroup reduce instead costs more than the launch it saves:
+// publishing the partials across XCDs takes an agent-scope release and acquire, which on
+// gfx950 write back and invalidate the whole L2 of the XCD, and the down projection of a
+// config-5 decode step went from 18 to 31 us.)
+template <typename TO, int NW, int U, bool NORM>
 __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p, float* part) {
   __shared__ f32x4 red[NW][64];
+  __shared__ float ssq[NW][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int64_t z = blockIdx.z;
@@ -1240,6 +1258,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p, floa
   const int64_t s0 = g0 + wave * per, s1 = min(g1, s0 + per);
   const bf16x8 zero = {};
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 sq = {0.f, 0.f, 0.f, 0.f};  // NORM: X X^T, lane (m, g) holds rows 4 g .. 4 g + 3 of column m
   for (int64_t s = s0; s < s1; s += U) {
     bf16x8 w[U], x[U];
 #pragma unroll
@@ -1250,20 +1269,33 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p, floa
       x[u] = in && xrow ? *reinterpret_cast<const bf16x8*>(X + k) : zero;
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], x[u], acc, 0, 0, 0);
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], x[u], acc, 0, 0, 0);
+      if constexpr (NORM) sq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[u], x[u], sq, 0, 0, 0);
+    }
   }
   red[wave][lane] = acc;
+  if constexpr (NORM) {
+    if (g == (r >> 2)) ssq[wave][r] = sq[r & 3];  // the diagonal element (r, r)
+  }
   __syncthreads();
   if (S == 1) {
     if (wave == 0 && xrow) {
       f32x4 t = red[0][lane];
 #pragma unroll
       for (int w = 1; w < NW; ++w) t += red[w][lane];
+      if constexpr (NORM) {
+        float q = ssq[0][r];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) q += ssq[w][r];
+        t *= 1.0f / sqrtf(q / (float)p.K + p.norm_eps);
+      }
       float v[4] = {t[0], t[1], t[2], t[3]};
       epilogue4<bf16_t, TO>(p, zo, zi, r, n0 + 4 * g, v);
     }
     return;
   }
+  // split K (no norm: the host keeps normed products unsplit)
   if (wave == 0) {
     const int64_t tile = (int64_t)blockIdx.z * gridDim.x + blockIdx.x;
     f32x4 t = red[0][lane];
@@ -1482,14 +1514,18 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
 
 template <typename TO>
 static void launch_skinny(int cfg, dim3 grid, hipStream_t st, const GemmParams& p, float* part) {
+  if (p.norm_rows) {  // the row-scaled form exists for the default shape only
+    gemm_skinny_kernel<TO, 4, 16, true><<<grid, 256, 0, st>>>(p, part);
+    return;
+  }
   switch (cfg) {
-    case 1: gemm_skinny_kernel<TO, 4, 8><<<grid, 256, 0, st>>>(p, part); break;
-    case 2: gemm_skinny_kernel<TO, 8, 16><<<grid, 512, 0, st>>>(p, part); break;
-    case 3: gemm_skinny_kernel<TO, 8, 8><<<grid, 512, 0, st>>>(p, part); break;
-    case 4: gemm_skinny_kernel<TO, 16, 4><<<grid, 1024, 0, st>>>(p, part); break;
-    case 5: gemm_skinny_kernel<TO, 8, 4><<<grid, 512, 0, st>>>(p, part); break;
-    case 6: gemm_skinny_kernel<TO, 16, 8><<<grid, 1024, 0, st>>>(p, part); break;
-    default: gemm_skinny_kernel<TO, 4, 16><<<grid, 256, 0, st>>>(p, part); break;
+    case 1: gemm_skinny_kernel<TO, 4, 8, false><<<grid, 256, 0, st>>>(p, part); break;
+    case 2: gemm_skinny_kernel<TO, 8, 16, false><<<grid, 512, 0, st>>>(p, part); break;
+    case 3: gemm_skinny_kernel<TO, 8, 8, false><<<grid, 512, 0, st>>>(p, part); break;
+    case 4: gemm_skinny_kernel<TO, 16, 4, false><<<grid, 1024, 0, st>>>(p, part); break;
+    case 5: gemm_skinny_kernel<TO, 8, 4, false><<<grid, 512, 0, st>>>(p, part); break;
+    case 6: gemm_skinny_kernel<TO, 16, 8, false><<<grid, 1024, 0, st>>>(p, part); break;
+    default: gemm_skinny_kernel<TO, 4, 16, false><<<grid, 256, 0, st>>>(p, part); break;
   }
   if (grid.y > 1)
     gemm_skinny_reduce_kernel<TO><<<dim3(grid.x, 1, grid.z), 64, 0, st>>>(p, part, (int)grid.y);
@@ -1630,6 +1666,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
+  p.norm_rows = d->norm_rows != 0;
+  p.norm_eps = d->norm_eps;
 
   // The MFMA kernel streams 16-byte rows of A and Bt: K-contiguous, 8-element aligned.
   const bool mfma = d->dtype_in == TL_BF16 && d->b_layout == TL_B_NK && d->K % 8 == 0 &&
@@ -1652,6 +1690,12 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
   const bool f32out = d->dtype_out == TL_F32;
   const bool skinny = mfma && (d->tile == TL_TILE_SKINNY || (d->tile == TL_TILE_AUTO && d->M <= 16));
+  if (d->norm_rows) {
+    if (!skinny || batch != 1)
+      return fail(TL_ERR_UNSUPPORTED, "RMS row scaling is implemented for unbatched bf16 "
+                  "products with M <= 16 and B as [N, K]");
+    TL_REQUIRE(d->norm_eps >= 0.f, "norm_eps must be >= 0");
+  }
   if (skinny) {
     TL_REQUIRE(d->M <= 16, "the skinny GEMM takes M <= 16");
     const int cfg = ctx->skinny_cfg >= 1 && ctx->skinny_cfg <= 6 ? ctx->skinny_cfg : 0;
@@ -1662,8 +1706,8 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     // per CU while every part keeps >= 4096 of K (down projection K = 16384: 4 parts,
     // 23.6 -> 18.0 us; K = 2048 shapes lose more to the extra launch than they gain).
     int64_t split = 1;
-    while (split < std::min(16, ctx->skinny_max_split) && tiles * split < 2 * cus &&
-           nsteps / (split * 2) >= 128)
+    while (!d->norm_rows && split < std::min(16, ctx->skinny_max_split) &&
+           tiles * split < 2 * cus && nsteps / (split * 2) >= 128)
       split *= 2;
     dim3 grid((unsigned)((d->N + 15) / 16), (unsigned)split, (unsigned)batch);
     float* part = nullptr;

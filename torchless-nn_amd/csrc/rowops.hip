@@ -103,6 +103,31 @@ __global__ __launch_bounds__(256) void transpose_kernel(const U* x, U* y, int64_
   }
 }
 
+// The same transpose with source row r multiplied by (offset + gain[r]) on the way (an
+// RMSNorm's gain folded into the K index of a packed [N, K] weight).
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_gain_kernel(const T* x, T* y, int64_t rows,
+                                                             int64_t cols, int64_t ldx,
+                                                             int64_t ldy, const T* gain,
+                                                             float offset) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int r = ty + 4 * i;
+    if (r0 + r < rows && c0 + tx < cols)
+      tile[r][tx] = Elem<T>::load(x + (r0 + r) * ldx + c0 + tx) *
+                    (offset + Elem<T>::load(gain + r0 + r));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    int c = ty + 4 * i;
+    if (c0 + c < cols && r0 + tx < rows) Elem<T>::store(y + (c0 + c) * ldy + r0 + tx, tile[tx][c]);
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // ViT patch extraction (reference transformer_adapters.py:39-47): image [B, C, H, W] ->
 // tokens [B, (H/p0)(W/p1), p0 p1 C] with token index i (W/p1) + j and feature order
@@ -1210,6 +1235,29 @@ int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
   else
     transpose_kernel<uint32_t><<<grid, 256, 0, ctx->stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols, ldx, ldy);
   return ls.finish("transpose2d");
+}
+
+int tl_transpose2d_gain(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
+                        int64_t ldx, int64_t ldy, const void* gain, float gain_offset,
+                        int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE_FLOAT(dtype);
+  TL_REQUIRE(rows >= 0 && cols >= 0, "negative size");
+  if (rows == 0 || cols == 0) return TL_OK;
+  TL_REQUIRE(x && y && gain && x != y, "null or aliased pointer");
+  TL_REQUIRE(ldx >= cols && ldy >= rows, "leading dimension too small");
+  TL_REQUIRE((cols + 63) / 64 <= 0x7fffffff && (rows + 63) / 64 <= 65535, "matrix too large");
+  const double es = (double)dtype_size(dtype);
+  LaunchScope ls(ctx, TL_KF_MISC, 0, es * (2.0 * rows * cols + rows));
+  dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (dtype == TL_F32)
+    transpose_gain_kernel<float><<<grid, 256, 0, ctx->stream>>>(
+        (const float*)x, (float*)y, rows, cols, ldx, ldy, (const float*)gain, gain_offset);
+  else
+    transpose_gain_kernel<bf16_t><<<grid, 256, 0, ctx->stream>>>(
+        (const bf16_t*)x, (bf16_t*)y, rows, cols, ldx, ldy, (const bf16_t*)gain, gain_offset);
+  return ls.finish("transpose2d_gain");
 }
 
 int tl_embed_fwd(tl_ctx* ctx, const void* ids, int32_t ids_dtype, const void* table,

@@ -33,34 +33,73 @@ def _round_up(n, m):
     return (n + m - 1) // m * m
 
 
-def _packed_nk(w):
+def _packed_nk(w, prenorm=None):
     """[K, N] weight -> [N, K] (K-contiguous) copy for the MFMA GEMM, cached on the
-    weight until its contents change."""
-    if w._aux is not None and w._aux[0] == w._version:
+    weight until its contents change. With `prenorm` (the RMSNorm layer that feeds the
+    product) its gain is folded in: B[n, k] = w[k, n] * (gamma_offset + gamma[k])."""
+    key = ((w._version,) if prenorm is None else
+           (w._version, prenorm.gamma._version, prenorm.gamma_offset))
+    if w._aux is not None and w._aux[0] == key:
         return w._aux[1]
-    packed = xp.transpose2d(w)
-    w._aux = (w._version, packed)
+    if prenorm is None:
+        packed = xp.transpose2d(w)
+    else:
+        packed = xp.transpose2d_gain(w, prenorm.gamma, prenorm.gamma_offset)
+    w._aux = (key, packed)
     return packed
 
 
+_UNIT_GAIN = {}
+
+
+def _folds_gain(prenorm, w_dtype):
+    """bf16 products fed by an RMSNorm carry its gain in their packed weight."""
+    return prenorm is not None and w_dtype is xp.bfloat16 and prenorm.gamma.dtype is xp.bfloat16
+
+
+def _prenorm(x2d, prenorm, w_dtype):
+    """(A operand, norm_eps) of a product that starts with the RMSNorm layer `prenorm`.
+    When the weight carries the gain (bf16), a decode step's few rows go in unnormalised and
+    the product scales each row by its 1 / rms (no separate launch); more rows are
+    normalised first with a unit gain. Otherwise the norm layer runs as it is."""
+    if prenorm is None:
+        return x2d, None
+    if not _folds_gain(prenorm, w_dtype):
+        return prenorm.forward(x2d), None
+    M, K = x2d.shape
+    prenorm.input = x2d
+    if M <= 16 and K % 8 == 0 and x2d.pitch % 8 == 0 and x2d.ptr % 16 == 0:
+        prenorm.output = None
+        return x2d, float(prenorm.eps)
+    key = (K, x2d.dtype.name)
+    if key not in _UNIT_GAIN:
+        _UNIT_GAIN[key] = xp.zeros((K,), x2d.dtype)
+    prenorm.output = xp.rmsnorm(x2d, _UNIT_GAIN[key], prenorm.eps, 1.0)
+    return prenorm.output, None
+
+
 def linear(x2d, w, bias=None, act=xp.TL_ACT_NONE, residual=None, out=None, qkv=None,
-           family="gemm_mfma"):
-    """y = act(x2d @ w + bias) (+ residual), x2d [M, K], w [K, N] (reference `x @ W + b`)."""
+           family="gemm_mfma", prenorm=None):
+    """y = act(x2d @ w + bias) (+ residual), x2d [M, K], w [K, N] (reference `x @ W + b`).
+    With `prenorm` (an RMSNorm layer) the product is RMSNorm(x2d) @ w."""
     M, K = x2d.shape
     Kw, N = w.shape
     if Kw != K:
         raise ValueError(f"matmul shape mismatch: {x2d.shape} @ {w.shape}")
+    fold = prenorm if _folds_gain(prenorm, w.dtype) else None
+    x2d, norm_eps = _prenorm(x2d, prenorm, w.dtype)
     if qkv is None and out is None:
         out = xp.empty((M, N), x2d.dtype)
     # bf16 always, fp32 when the product is large enough for the fp32 matrix-core kernel
     # (at least 128 output tiles of 128x128, K % 4 == 0): both read B as [N, K]
     if w.dtype is xp.bfloat16 or (K % 4 == 0 and -(-M // 128) * -(-N // 128) >= 128):
-        B, ldb, layout = _packed_nk(w), K, xp.TL_B_NK
+        B, ldb, layout = _packed_nk(w, fold), K, xp.TL_B_NK
     else:
         B, ldb, layout = w, w.pitch, xp.TL_B_KN
     xp.gemm(x2d, B, M=M, N=N, K=K, lda=x2d.pitch, ldb=ldb, b_layout=layout, C=out,
             ldc=(out.pitch if out is not None else 0), bias=bias, act=act, residual=residual,
-            ldr=(residual.pitch if residual is not None else 0), qkv=qkv, family=family)
+            ldr=(residual.pitch if residual is not None else 0), qkv=qkv, family=family,
+            norm_eps=norm_eps)
     return out
 
 
@@ -343,10 +382,16 @@ class DevicePosition:
     current position: `refresh()` recomputes the table from the device value and
     `advance(n)` adds n on the device, both stream-ordered."""
 
-    def __init__(self, start, T, head_dim, base=10000.0):
+    def __init__(self, start, T, head_dim, base=10000.0, table=None):
         self.pos = xp.array(np.array([start], np.int64))
         self.T, self.head_dim, self.base = int(T), int(head_dim), float(base)
-        self.table = xp.empty((2, self.T, self.head_dim // 2), xp.float32)
+        self.table = table if table is not None else xp.empty((2, self.T, self.head_dim // 2),
+                                                              xp.float32)
+
+    @classmethod
+    def at(cls, pos0, T, head_dim, base):
+        """A fixed host position pos0 (its table from the shared host-position tables)."""
+        return cls(pos0, T, head_dim, base, table=_rope_table(T, head_dim, base, pos0))
 
     def refresh(self):
         xp.rope_table_dev(self.table, self.pos, self.base)
@@ -398,12 +443,20 @@ class MultiQueryAttention(Layer):
     def forward(self, input, cache=None, layer=0, pos0=0):
         return self._forward(input, None, cache, layer, pos0)
 
-    def _forward(self, input, residual, cache=None, layer=0, pos0=0):
+    def _forward(self, input, residual, cache=None, layer=0, pos0=0, prenorm=None):
+        """`prenorm` (an RMSNorm layer) normalises `input` first (folded into the QKV
+        product for a decode step's few rows)."""
         if isinstance(pos0, DevicePosition):
-            return self._forward_dev(input, residual, cache, layer, pos0)
-        self.input = input
+            return self._forward_dev(input, residual, cache, layer, pos0, prenorm)
         B, T, C = input.shape
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.heads_dim
+        if (cache is not None and self.fused and (Hq // Hkv) * T <= 16 and
+                pos0 + T <= min(cache.capacity, self.context_length) and
+                xp.attention_supported(input.dtype, D, cache.capacity)):
+            # a decode step: the same kernels as a replayed one (position in device memory)
+            dpos = DevicePosition.at(pos0, T, D, self.rope_base)
+            return self._forward_dev(input, residual, cache, layer, dpos, prenorm)
+        self.input = input
         if pos0 + T > self.context_length:
             raise ValueError(f"positions up to {pos0 + T} exceed the context length "
                              f"{self.context_length}")
@@ -416,7 +469,8 @@ class MultiQueryAttention(Layer):
         else:
             L = _round_up(T, 8)
             k, vt = xp.empty((B, Hkv, L, D), dt), xp.empty((B, Hkv, D, L), dt)
-        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0))
+        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, pos0),
+               prenorm=prenorm)
         table = _rope_table(T, D, self.rope_base, pos0)
         # queries and this call's cache keys rotated in one launch
         kslice = xp.DeviceTensor((B * Hkv, T, D), dt, buf=k.buf,
@@ -435,7 +489,7 @@ class MultiQueryAttention(Layer):
         self.output = out.reshape(B, T, C)
         return self.output
 
-    def _forward_dev(self, input, residual, cache, layer, dpos):
+    def _forward_dev(self, input, residual, cache, layer, dpos, prenorm=None):
         """Decode at a device position (what a captured step replays): the same kernels and
         arithmetic as the host-position call, with the cache row, the RoPE positions and the
         attended key count read from dpos.pos on the device. The caller keeps the position
@@ -452,11 +506,17 @@ class MultiQueryAttention(Layer):
             raise ValueError("decoding at a device position needs the fused attention kernel")
         q = xp.empty((B, Hq, T, D), dt)
         k, vt, L = cache.k[layer], cache.vt[layer], cache.capacity
-        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, dpos.pos))
-        xp.rope2_dev(q, k, dpos.table, dpos.pos)
+        linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, dpos.pos),
+               prenorm=prenorm)
         heads = xp.empty((B, T, Hq * D), dt)
-        xp.attention_decode_dev(q, k, vt, heads, dpos.pos, n_heads_q=Hq, n_heads_kv=Hkv,
-                                divisor=float(np.float32(D ** 0.5)))
+        div = float(np.float32(D ** 0.5))
+        if D >= 64:  # RoPE of the queries and new keys inside the attention kernel
+            xp.attention_decode_dev(q, k, vt, heads, dpos.pos, n_heads_q=Hq, n_heads_kv=Hkv,
+                                    divisor=div, rope=dpos.table)
+        else:
+            xp.rope2_dev(q, k, dpos.table, dpos.pos)
+            xp.attention_decode_dev(q, k, vt, heads, dpos.pos, n_heads_q=Hq, n_heads_kv=Hkv,
+                                    divisor=div)
         out = linear(heads.reshape(B * T, Hq * D), self.out_weights,
                      residual=(residual.reshape(B * T, C) if residual is not None else None))
         self.output = out.reshape(B, T, C)
@@ -507,29 +567,38 @@ class GeGLUFeedForward(Layer):
             self.register_param(w)
         self._pack = None
 
-    def _packed(self):
+    def _packed(self, prenorm=None):
+        """Gate and up weights interleaved as [2F, C] rows (gate f, up f), with the gain of
+        `prenorm` (the RMSNorm feeding the FFN) folded in when given."""
         g, u = self.gate_weights, self.up_weights
-        key = (g._version, u._version)
+        key = ((g._version, u._version) if prenorm is None else
+               (g._version, u._version, prenorm.gamma._version, prenorm.gamma_offset))
         if self._pack is None or self._pack[0] != key:
             C, F = g.shape
             packed = xp.empty((2 * F, C), g.dtype)
-            xp.transpose2d(g, out=packed, out_offset=0, ldy=2 * C)
-            xp.transpose2d(u, out=packed, out_offset=C, ldy=2 * C)
+            for w, at in ((g, 0), (u, C)):
+                if prenorm is None:
+                    xp.transpose2d(w, out=packed, out_offset=at, ldy=2 * C)
+                else:
+                    xp.transpose2d_gain(w, prenorm.gamma, prenorm.gamma_offset, out=packed,
+                                        out_offset=at, ldy=2 * C)
             self._pack = (key, packed)
         return self._pack[1]
 
     def forward(self, input):
         return self._forward(input, None)
 
-    def _forward(self, input, residual):
+    def _forward(self, input, residual, prenorm=None):
         self.input = input
         shape = input.shape
         C, F = shape[-1], self.hidden
-        x2 = input.reshape(-1, C)
+        wdt = self.gate_weights.dtype
+        x2, norm_eps = _prenorm(input.reshape(-1, C), prenorm, wdt)
         M = x2.shape[0]
         h = xp.empty((M, F), input.dtype)
-        xp.gemm(x2, self._packed(), M=M, N=2 * F, K=C, lda=x2.pitch, ldb=C, b_layout=xp.TL_B_NK,
-                C=h, ldc=F, act=self.act_code, geglu=True)
+        pack = self._packed(prenorm if _folds_gain(prenorm, wdt) else None)
+        xp.gemm(x2, pack, M=M, N=2 * F, K=C, lda=x2.pitch, ldb=C, b_layout=xp.TL_B_NK,
+                C=h, ldc=F, act=self.act_code, geglu=True, norm_eps=norm_eps)
         self.hidden_output = h
         y = linear(h, self.down_weights,
                    residual=(residual.reshape(-1, C) if residual is not None else None))
@@ -555,6 +624,6 @@ class GemmaBlock(Layer):
 
     def forward(self, input, cache=None, layer=0, pos0=0):
         self.input = input
-        y = self.attn_block._forward(self.pre_attn_norm.forward(input), input, cache, layer, pos0)
-        self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), y)
+        y = self.attn_block._forward(input, input, cache, layer, pos0, prenorm=self.pre_attn_norm)
+        self.output = self.ffn._forward(y, y, prenorm=self.pre_ffn_norm)
         return self.output

@@ -132,6 +132,7 @@ class _GemmDesc(ctypes.Structure):
         ("kv_len", ctypes.c_int64), ("kv_pos0", ctypes.c_int64),
         ("family", ctypes.c_int32), ("tile", ctypes.c_int32),
         ("kv_pos0_dev", ctypes.c_void_p),
+        ("norm_rows", ctypes.c_int32), ("norm_eps", ctypes.c_float),
     ]
 
 
@@ -167,6 +168,7 @@ SIGNATURES = {
     "tl_random_normal": [_P, _P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F32, _F32, _I32],
     "tl_transpose2d": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
+    "tl_transpose2d_gain": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _F32, _I32],
     "tl_patchify": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32],
     "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_layernorm_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32],
@@ -183,7 +185,7 @@ SIGNATURES = {
     "tl_attention_fwd_noalloc": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                                  _I64, _F32, _I32, _I64, _I32],
     "tl_attention_decode_dev": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32,
-                                _I64, _P, _I32],
+                                _I64, _P, _P, _I32],
     "tl_graph_begin": [_P],
     "tl_graph_end": [_P, ctypes.POINTER(_P)],
     "tl_graph_launch": [_P, _P],
@@ -571,10 +573,12 @@ def _c():
 def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=None, ldc=0,
          out_dtype=None, batch=1, batch_inner=1, sa=(0, 0), sb=(0, 0), sc=(0, 0), bias=None,
          residual=None, ldr=0, sr=(0, 0), act=TL_ACT_NONE, divisor=1.0, qkv=None,
-         family="gemm_mfma", tile="auto", geglu=False):
+         family="gemm_mfma", tile="auto", geglu=False, norm_eps=None):
     """One tl_gemm call. qkv = (q, k, vt, T, Hq, Hkv, D[, kv_len, kv_pos0]) selects the
     split epilogue; kv_pos0 may be a one-element int64 DeviceTensor (the cache position
-    read on the device when the kernel runs)."""
+    read on the device when the kernel runs). norm_eps (M <= 16) scales each row of the
+    product by 1 / sqrt(mean(A_row^2) + norm_eps): RMSNorm(A) @ B when B carries the norm's
+    gain."""
     pos_dev = None
     if qkv is not None:
         q, k, vt, T, Hq, Hkv, Dh = qkv[:7]
@@ -595,7 +599,8 @@ def gemm(A: DeviceTensor, B: DeviceTensor, *, M, N, K, lda, ldb, b_layout, C=Non
                   bias.ptr if bias is not None else None,
                   residual.ptr if residual is not None else None, ldr, sr[0], sr[1],
                   act, float(divisor), epi, qp, kp, vp, T, Hq, Hkv, Dh, kv_len, kv_pos0,
-                  KFAMILY[family], GEMM_TILES[tile], pos_dev)
+                  KFAMILY[family], GEMM_TILES[tile], pos_dev, int(norm_eps is not None),
+                  float(norm_eps) if norm_eps is not None else 0.0)
     lib_, h = _c()
     check(lib_.tl_gemm(h, ctypes.byref(d)))
     if qkv is not None:
@@ -759,15 +764,20 @@ def _position_ptr(pos: DeviceTensor):
 
 
 def attention_decode_dev(q: DeviceTensor, k: DeviceTensor, vt: DeviceTensor, out: DeviceTensor,
-                         pos: DeviceTensor, *, n_heads_q, n_heads_kv, divisor):
+                         pos: DeviceTensor, *, n_heads_q, n_heads_kv, divisor, rope=None):
     """Causal decode attention at a device position: q [B, Hq, Tq, D] at positions
-    *pos .. *pos + Tq - 1 over the cache k [B, Hkv, L, D] / vt [B, Hkv, D, L]."""
+    *pos .. *pos + Tq - 1 over the cache k [B, Hkv, L, D] / vt [B, Hkv, D, L]. With `rope`
+    (the float [2, Tq, D/2] table of those positions) q and the new cache keys come in
+    unrotated; the kernel rotates both and writes the rotated keys back into k."""
     B, Hq, Tq, D = q.shape
+    if rope is not None and (rope.dtype is not float32 or rope.shape != (2, Tq, D // 2)):
+        raise ValueError("the RoPE table must be float32 [2, Tq, D/2]")
     lib_, h = _c()
     check(lib_.tl_attention_decode_dev(h, q.ptr, k.ptr, vt.ptr, out.ptr, B, n_heads_q,
                                        n_heads_kv, Tq, D, out.pitch, float(divisor), k.shape[2],
-                                       _position_ptr(pos), q.dtype.code))
-    _wrote(out)
+                                       _position_ptr(pos), rope.ptr if rope is not None else None,
+                                       q.dtype.code))
+    _wrote(out, k if rope is not None else None)
     return out
 
 
@@ -886,6 +896,24 @@ def transpose2d(x: DeviceTensor, out=None, out_offset=0, ldy=None) -> DeviceTens
         ptr, ld = out.ptr + out_offset * x.dtype.itemsize, ldy
     lib_, h = _c()
     check(lib_.tl_transpose2d(h, x.ptr, ptr, r, c_, x.pitch, ld, x.dtype.code))
+    _wrote(out)
+    return out
+
+
+def transpose2d_gain(x: DeviceTensor, gain: DeviceTensor, gain_offset=0.0, out=None,
+                     out_offset=0, ldy=None) -> DeviceTensor:
+    """y[c, r] = x[r, c] * (gain_offset + gain[r]); `out`/`out_offset`/`ldy` as transpose2d."""
+    r, c_ = x.shape
+    if gain.size != r or gain.dtype is not x.dtype:
+        raise ValueError("transpose2d_gain needs one gain of x's dtype per row of x")
+    if out is None:
+        out = DeviceTensor((c_, r), x.dtype)
+        ptr, ld = out.ptr, out.pitch
+    else:
+        ptr, ld = out.ptr + out_offset * x.dtype.itemsize, ldy
+    lib_, h = _c()
+    check(lib_.tl_transpose2d_gain(h, x.ptr, ptr, r, c_, x.pitch, ld, gain.ptr,
+                                   float(gain_offset), x.dtype.code))
     _wrote(out)
     return out
 
