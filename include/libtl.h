@@ -174,6 +174,10 @@ int tl_memcpy2d_h2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
                     size_t width_bytes, size_t rows);
 int tl_memcpy2d_d2h(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size_t spitch,
                     size_t width_bytes, size_t rows);
+/* Device-to-device copy of `rows` rows of width_bytes (stream-ordered): the row copies of
+ * `xp.concatenate((tokens, out), axis=1)` (reference demo.ipynb:1533). */
+int tl_memcpy2d_d2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size_t spitch,
+                    size_t width_bytes, size_t rows);
 /* Waits for the stream, then reports any latched kernel data error. */
 int tl_sync(tl_ctx* ctx);
 /* HIP graphs of the context stream, for replaying a whole step (a decode step, a short
@@ -214,6 +218,18 @@ int tl_cast(tl_ctx* ctx, const void* x, void* y, int64_t n, int32_t dtype_x, int
  * init_random_tensor's draw (reference backend.py:27-31, a device draw under CuPy). */
 int tl_random_normal(tl_ctx* ctx, void* y, int64_t n, uint64_t seed, uint64_t stream,
                      float mean, float std_dev, int32_t dtype);
+/* n draws from the categorical distribution p[0 .. cols) (fp32 or bf16, not necessarily
+ * normalised): draw j takes u = (w0 >> 8) 2^-24 from Philox counter (j, 0, stream) under key
+ * `seed` and returns the smallest i with p[0] + .. + p[i] > u * sum(p) (the last index if
+ * rounding leaves none), as int64. Replaces `xp.random.choice(..., p=probs)` (reference
+ * demo.ipynb:1531, CuPy's cumsum + searchsorted). */
+int tl_sample(tl_ctx* ctx, const void* probs, int64_t cols, int32_t dtype, int64_t n,
+              uint64_t seed, uint64_t stream, int64_t* out);
+/* out[i] = src[idx[i]] for elements of elem_bytes (1, 2, 4, 8) bytes; an index outside
+ * [0, src_len) is reported as TL_ERR_BAD_INPUT at the next synchronising call. The gather
+ * of `xp.random.choice(a, ...)` from its candidate array `a`. */
+int tl_take(tl_ctx* ctx, const void* src, int64_t src_len, int32_t elem_bytes,
+            const int64_t* idx, int64_t n, void* out);
 /* y[c*ldy + r] = x[r*ldx + c]: weight pre-packing into the K-contiguous GEMM layout. */
 int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,
                    int64_t ldx, int64_t ldy, int32_t dtype);

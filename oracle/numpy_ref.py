@@ -44,6 +44,12 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
   philox4x32_10    the published known-answer vectors of Random123 (zero, all-ones and
                    pi-digit counters/keys)
   random_normal    moments of a large draw; Box-Muller radius/angle identities
+  sample_uniforms  range [0, 1) on a 2^-24 grid; mean/variance of a large draw; word 0
+                   of the KAT-pinned Philox (a wrong word or shift fails the grid check)
+  sample_categorical  brute-force linear scan of the running sum at tiny sizes; one-hot
+                   and zero-probability rows; empirical frequencies of 200000 draws match
+                   p (chi-square); u = 0 and u just below 1 hit the first and last
+                   nonzero entries
 The reference itself was not imported or run: its files are pure Python over CuPy/NumPy
 with no golden vectors, and every function above is pinned by the checks listed.
 """
@@ -427,6 +433,30 @@ def random_normal(n, seed, stream=0, mean=0.0, std=1.0):
         out[:, a] = r * np.cos(2 * np.pi * u2)
         out[:, b] = r * np.sin(2 * np.pi * u2)
     return (mean + std * out.reshape(-1)[:n]).astype(F32)
+
+
+def sample_uniforms(n, seed, stream=0):
+    """The uniforms of tl_sample: draw j takes u = (w0 >> 8) 2^-24 in [0, 1) from Philox
+    counter (j, 0, stream) under key seed. Evaluated in float64."""
+    j = np.arange(n, dtype=np.uint64)
+    ctr = np.stack([j & np.uint64(0xFFFFFFFF), j >> np.uint64(32),
+                    np.full_like(j, stream & 0xFFFFFFFF), np.full_like(j, stream >> 32)], -1)
+    w = philox4x32_10(ctr, (seed & 0xFFFFFFFF, seed >> 32))
+    return np.floor(w[:, 0].astype(np.float64) / 256) * 2.0 ** -24
+
+
+def sample_categorical(p, u):
+    """xp.random.choice(a, p=p) (reference demo.ipynb:1531). The reference's runtime is CuPy
+    (backend.py:12-18, no version pinned in the repository), whose documented choice draws
+    a uniform u in [0, 1) per sample and returns cdf.searchsorted(u, side='right') for
+    cdf = cumsum(p) / sum(p). Same rule here with the caller's uniforms (the device's Philox
+    stream, sample_uniforms): index = number of running sums <= u * sum(p), clamped to the
+    last index; float64 sums. Returns (indices, u * sum(p), cdf) so a test can tell
+    draws that land within rounding of a boundary."""
+    cdf = np.cumsum(np.asarray(p, dtype=np.float64))
+    x = np.asarray(u, dtype=np.float64) * cdf[-1]
+    idx = np.minimum(np.searchsorted(cdf, x, side="right"), cdf.size - 1)
+    return idx.astype(np.int64), x, cdf
 
 
 # ---- ViT (reference transformer_adapters.py:6-95, demo.ipynb cell 8) ----------------

@@ -1,0 +1,195 @@
+"""The notebook GPT's generation path on the MI355X (reference demo.ipynb:1520-1537):
+basic indexing as views (`tokens[:, a:]`, `predict(tokens)[0, -1]`, `out[0, 0]`),
+xp.concatenate, xp.arange, xp.random.choice (device sampling checked draw by draw against
+the oracle's inverse CDF on the same Philox uniforms), the notebook loop itself with a
+sliding window, and KV-cache decoding of the learned-position GPT against recomputing the
+window. fp32 probabilities: max_rel <= 1e-5; bf16: 2e-2; ids exact where the top-2 gap
+is clear of the tolerance."""
+import numpy as np
+import pytest
+
+from oracle import numpy_ref as ref
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+CHAR = dict(vocab=65, ctx=128, layers=4, d=128, heads=4, act="gelu")
+
+
+@pytest.fixture(scope="module")
+def tl():
+    import tl_hip
+    tl_hip.ctx()
+    import gpt
+    return dict(xp=tl_hip, gpt=gpt)
+
+
+def test_indexing_views_match_numpy(tl):
+    xp = tl["xp"]
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((3, 5, 7)).astype(F32)
+    d = xp.array(a, dtype="fp32")
+    for key in [0, -1, (1,), (0, -1), (2, 3), (1, 2, 4), (-1, -1, -1), (slice(None), 2),
+                (1, slice(1, 4)), (0, slice(None), slice(2, 6)), (slice(None), -1, slice(0, 3)),
+                (0, 0, slice(5, 2)), (slice(1, 3),)]:
+        got = d[key]
+        want = a[key]
+        assert got.shape == want.shape, key
+        np.testing.assert_array_equal(got.get(), want, err_msg=str(key))
+    # a padded tensor (row pitch > columns) and a uint8 row view at an odd byte offset
+    p = xp.empty((4, 6), "fp32", pitch=8)
+    host = rng.standard_normal((4, 6)).astype(F32)
+    p.set(host)
+    np.testing.assert_array_equal(p[1:3, 2:].get(), host[1:3, 2:])
+    np.testing.assert_array_equal(p[-1].get(), host[-1])
+    t = xp.array(np.arange(11, dtype=np.uint8).reshape(1, 11), dtype=xp.uint8)
+    v = t[:, 3:]
+    assert v.shape == (1, 8) and v.get().tolist() == [list(range(3, 11))]
+    assert len(t[0]) == 11 and int(t[0, 4].get()) == 4
+    with pytest.raises(NotImplementedError):
+        d[:, :, 0]  # one column of several rows is strided
+    with pytest.raises(NotImplementedError):
+        d[:, 1:3]   # rows b*5+1, b*5+2: not evenly spaced
+    with pytest.raises(IndexError):
+        d[3]
+
+
+def test_concatenate_and_arange(tl):
+    xp = tl["xp"]
+    rng = np.random.default_rng(2)
+    for dt, host_dt in (("fp32", F32), ("uint8", np.uint8), ("int64", np.int64)):
+        a = (rng.random((2, 3, 4)) * 100).astype(host_dt)
+        b = (rng.random((2, 3, 5)) * 100).astype(host_dt)
+        c = (rng.random((2, 1, 4)) * 100).astype(host_dt)
+        e = (rng.random((1, 3, 4)) * 100).astype(host_dt)
+        da, db, dc, de = (xp.array(v, dtype=dt) for v in (a, b, c, e))
+        np.testing.assert_array_equal(xp.concatenate((da, db), axis=-1).get(),
+                                      np.concatenate((a, b), axis=-1))
+        np.testing.assert_array_equal(xp.concatenate((da, dc), axis=1).get(),
+                                      np.concatenate((a, c), axis=1))
+        np.testing.assert_array_equal(xp.concatenate((da, de, da), axis=0).get(),
+                                      np.concatenate((a, e, a), axis=0))
+    # a view with an offset and a row pitch (the notebook's tokens[:, a:] then append)
+    t = xp.array(np.arange(20, dtype=np.uint8).reshape(2, 10), dtype=xp.uint8)
+    got = xp.concatenate((t[:, 4:], xp.array(np.array([[99], [98]], np.uint8), dtype=xp.uint8)), axis=1)
+    want = np.concatenate((np.arange(20, dtype=np.uint8).reshape(2, 10)[:, 4:], [[99], [98]]), axis=1)
+    np.testing.assert_array_equal(got.get(), want)
+    r = xp.arange(0, 65, dtype=xp.uint8)
+    assert r.dtype is xp.uint8 and r.get().tolist() == list(range(65))
+    with pytest.raises(ValueError):
+        xp.concatenate((xp.zeros((2, 3), "fp32"), xp.zeros((3, 3), "fp32")), axis=1)
+
+
+@pytest.mark.parametrize("V", [1, 7, 65, 50257, 256000])
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_choice_matches_oracle_inverse_cdf(tl, V, dt):
+    """Each device draw is the oracle's searchsorted index for the same Philox uniform,
+    except where u * total lies within float32 rounding of a running-sum boundary."""
+    xp = tl["xp"]
+    rng = np.random.default_rng(V)
+    p = rng.random(V).astype(F32) ** 4  # skewed, with many tiny entries
+    p[rng.random(V) < 0.2] = 0
+    if not p.any():
+        p[0] = 1
+    p = p / p.sum()
+    if dt == "bf16":
+        p = ref.round_bf16(p)
+    dp = xp.array(p, dtype=dt)
+    xp.random.seed(1234)
+    n = 512
+    got = xp.random.choice(V, size=n, p=dp).get()
+    assert got.shape == (n,) and got.dtype == np.int64
+    want, x, cdf = ref.sample_categorical(p, ref.sample_uniforms(n, 1234, 0))
+    tol = 1e-5 * cdf[-1] + 1e-6 * np.abs(x)
+    lo = np.where(got > 0, cdf[np.maximum(got - 1, 0)], 0.0)
+    ok = (got == want) | ((x >= lo - tol) & (x <= cdf[got] + tol))
+    assert ok.all(), (np.nonzero(~ok)[0][:5], got[~ok][:5], want[~ok][:5])
+    assert np.all(p[got] > 0)
+    assert (got == want).mean() > 0.98
+
+
+def test_choice_frequencies_and_candidates(tl):
+    """Draws from `a` (the notebook's xp.arange(0, vocab_size, dtype=uint8)) follow p:
+    chi-square over 100000 draws, and a second call continues the stream."""
+    xp = tl["xp"]
+    p = np.array([0.05, 0.0, 0.3, 0.15, 0.0, 0.25, 0.25], F32)
+    a = xp.array(np.array([10, 11, 12, 13, 14, 15, 16], np.uint8), dtype=xp.uint8)
+    xp.random.seed(77)
+    s1 = xp.random.choice(a, size=(50000,), p=xp.array(p, dtype="fp32")).get()
+    s2 = xp.random.choice(a, size=(50000,), p=xp.array(p, dtype="fp32")).get()
+    assert s1.dtype == np.uint8 and not np.array_equal(s1, s2)
+    cnt = np.bincount(np.concatenate([s1, s2]) - 10, minlength=7)
+    assert cnt[1] == 0 and cnt[4] == 0
+    nz = p > 0
+    e = 100000 * p[nz]
+    assert np.sum((cnt[nz] - e) ** 2 / e) < 25
+    one = xp.random.choice(a, size=(1, 1), p=xp.array(p, dtype="fp32"))
+    assert one.shape == (1, 1) and 10 <= int(one[0, 0].get()) <= 16
+
+
+def _cdf_interval_ok(p, u, tok, tol=1e-5):
+    cdf = np.cumsum(np.asarray(p, dtype=np.float64))
+    x = u * cdf[-1]
+    lo = cdf[tok - 1] if tok > 0 else 0.0
+    return lo - tol <= x <= cdf[tok] + tol
+
+
+def test_notebook_generate_loop_slides_the_window(tl):
+    """The notebook's loop (window of the last ctx tokens, predict, choice over arange,
+    concatenate) for 24 tokens from a 120-token prompt, so the window slides past ctx=128.
+    Every drawn token is checked against the oracle's probabilities for that window and
+    the draw's Philox uniform (sampler stream i for draw i)."""
+    xp, gpt = tl["xp"], tl["gpt"]
+    net, _ = gpt.build_gpt(CHAR, dtype="fp32")
+    gpt.seed_parameters(net, 5, 0.3)
+    P = ref.gpt_params(CHAR, 5, 0.3)
+    prompt = np.random.default_rng(6).integers(0, 65, 120).astype(np.uint8)
+    xp.random.seed(2024)
+    seen = []
+    tokens = gpt.generate_window(net, prompt, 24, CHAR["ctx"], CHAR["vocab"], on_token=seen.append)
+    out = tokens.get()[0]
+    assert out.dtype == np.uint8 and len(seen) == 24
+    # trimmed to ctx before each forward, so the last append leaves ctx + 1 tokens
+    assert tokens.shape == (1, CHAR["ctx"] + 1) and out[-24:].tolist() == seen
+    seq = np.concatenate([prompt, np.array(seen, np.uint8)])
+    for i in range(24):
+        window = seq[max(0, 120 + i - CHAR["ctx"]):120 + i]
+        probs = ref.gpt_forward(window[None, :].astype(np.int64), P, CHAR)[0, -1]
+        u = ref.sample_uniforms(1, 2024, i)[0]
+        assert _cdf_interval_ok(probs, u, seen[i]), i
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_kv_cache_generation_matches_recomputing_the_window(tl, dt):
+    """KV-cache decoding of the learned-position GPT (absent from the reference, which
+    recomputes the window): greedy ids and every step's probabilities equal those of a full
+    forward over the same tokens; sampled generation from the cache draws from the same
+    distributions (draw-by-draw oracle check)."""
+    xp, gpt = tl["xp"], tl["gpt"]
+    net, _ = gpt.build_gpt(CHAR, dtype=dt)
+    gpt.seed_parameters(net, 8, 0.3 if dt == "fp32" else 0.05)
+    ids = np.random.default_rng(9).integers(0, 65, (3, 40))
+    new = gpt.generate(net, ids, 30, sample=False)
+    assert new.shape == (3, 30)
+    seq = np.concatenate([ids, new], axis=1)
+    full = net.predict(seq[:, :-1]).get()  # position 39 + t predicts new[:, t]
+    rows = full[:, 39:, :]
+    tol = 1e-5 if dt == "fp32" else 2e-2
+    cache = gpt.new_cache(net, 3, 70)
+    probs0 = gpt.forward_cached(net, ids, cache, 0).get()
+    assert ref.max_rel(probs0, net.predict(ids).get()) <= tol
+    for t in range(29):
+        step = gpt.forward_cached(net, seq[:, 40 + t:41 + t], cache, 40 + t).get()[:, 0]
+        assert ref.max_rel(step, rows[:, t + 1]) <= tol, t
+    srt = np.sort(rows, -1)
+    clear = (srt[..., -1] - srt[..., -2]) > 4 * tol * srt[..., -1]
+    assert np.array_equal(new[clear], np.argmax(rows, -1)[clear])
+    xp.random.seed(31)
+    drawn = gpt.generate(net, ids[:1], 12, sample=True)
+    seq1 = np.concatenate([ids[:1], drawn], axis=1)
+    if dt == "fp32":
+        P = ref.gpt_params(CHAR, 8, 0.3)
+        for t in range(12):
+            probs = ref.gpt_forward(seq1[:, :40 + t], P, CHAR)[0, -1]
+            assert _cdf_interval_ok(probs, ref.sample_uniforms(1, 31, t)[0], drawn[0, t]), t
+    with pytest.raises(ValueError):
+        gpt.generate(net, ids, 100)  # 40 + 100 - 1 > ctx 128

@@ -374,6 +374,47 @@ def test_random_normal_moments_and_structure():
                                1.0 + 0.02 * ref.random_normal(10, 5, 3), rtol=1e-6)
 
 
+def test_sample_uniforms_grid_and_moments():
+    u = ref.sample_uniforms(400_000, seed=99, stream=3)
+    assert u.min() >= 0 and u.max() < 1
+    assert np.all(u * 2 ** 24 == np.floor(u * 2 ** 24))  # the 2^-24 grid of (w0 >> 8)
+    assert abs(u.mean() - 0.5) < 2e-3 and abs(u.var() - 1 / 12) < 1e-3
+    w = ref.philox4x32_10(np.array([[5, 0, 3, 0]], np.uint32), (99, 0))[0]
+    assert u[5] == (int(w[0]) >> 8) * 2.0 ** -24
+    assert not np.array_equal(ref.sample_uniforms(8, 99, 3), ref.sample_uniforms(8, 99, 4))
+
+
+def test_sample_categorical_brute_force_and_frequencies():
+    rng = np.random.default_rng(51)
+    for n in (1, 2, 5, 17):
+        p = rng.random(n).astype(F32)
+        p[rng.random(n) < 0.3] = 0
+        if p.sum() == 0:
+            p[-1] = 1
+        u = rng.random(64)
+        got, x, _ = ref.sample_categorical(p, u)
+        for j in range(64):  # first index whose running sum exceeds u * total
+            run, want = 0.0, n - 1
+            for i in range(n):
+                run += float(p[i])
+                if run > x[j]:
+                    want = i
+                    break
+            assert got[j] == want and p[got[j]] > 0
+    onehot = np.zeros(9, F32)
+    onehot[4] = 1
+    assert set(ref.sample_categorical(onehot, rng.random(100))[0]) == {4}
+    p = np.array([0, 0.25, 0, 0.5, 0.25, 0], F32)
+    assert ref.sample_categorical(p, [0.0])[0][0] == 1
+    assert ref.sample_categorical(p, [1 - 2 ** -24])[0][0] == 4
+    # frequencies of 200000 draws against p (chi-square, 9 degrees of freedom)
+    p = rng.random(10).astype(F32)
+    idx = ref.sample_categorical(p, ref.sample_uniforms(200_000, seed=7))[0]
+    cnt = np.bincount(idx, minlength=10)
+    e = 200_000 * p / p.sum()
+    assert np.sum((cnt - e) ** 2 / e) < 30
+
+
 # ---- ViT ------------------------------------------------------------------------------------
 def test_patchify_brute_force():
     rng = np.random.default_rng(40)

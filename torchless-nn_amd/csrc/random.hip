@@ -63,9 +63,76 @@ __global__ __launch_bounds__(256) void random_normal_kernel(T* y, int64_t n, uin
   }
 }
 
+// Categorical sampling (the notebook's xp.random.choice(..., p=probs), demo.ipynb:1531):
+// sample j draws u = (w0 >> 8) 2^-24 in [0, 1) from Philox counter (j, 0, stream) and key
+// seed, and returns the smallest index i with cdf[i] > u * total, where cdf is the running
+// sum of p (searchsorted(cdf, u * total, side='right'), clamped to the last index). One
+// workgroup: thread t sums a contiguous chunk of p, a scan over the chunk sums in LDS
+// gives each chunk its [start, end) share of [0, total), and the thread whose share holds
+// u * total walks its chunk to the index.
+template <typename T>
+__global__ __launch_bounds__(1024) void sample_kernel(const T* p, int64_t cols, int64_t n,
+                                                      uint32_t k0, uint32_t k1, uint32_t s0,
+                                                      uint32_t s1, int64_t* out) {
+  __shared__ float incl[1024];
+  const int t = threadIdx.x;
+  const int64_t chunk = (cols + 1023) / 1024;
+  const int64_t lo = min(cols, (int64_t)t * chunk), hi = min(cols, lo + chunk);
+  float sum = 0.f;
+  for (int64_t i = lo; i < hi; ++i) sum += Elem<T>::load(p + i);
+  incl[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan (Hillis-Steele)
+    const float v = t >= off ? incl[t - off] : 0.f;
+    __syncthreads();
+    incl[t] += v;
+    __syncthreads();
+  }
+  const float total = incl[1023];
+  const float start = t > 0 ? incl[t - 1] : 0.f, end = incl[t];
+  for (int64_t j = 0; j < n; ++j) {
+    const Philox4 w = philox4x32_10((uint32_t)j, (uint32_t)((uint64_t)j >> 32), s0, s1, k0, k1);
+    const float x = (float)(w.v[0] >> 8) * 5.9604644775390625e-08f * total;
+    // the share that holds x; past the end (rounding) the last nonempty chunk takes it
+    const bool mine = (x >= start && x < end) || (t == 1023 && x >= total);
+    if (mine && lo < hi) {
+      float c = start;
+      int64_t idx = hi - 1;
+      for (int64_t i = lo; i < hi; ++i) {
+        c += Elem<T>::load(p + i);
+        if (c > x) {
+          idx = i;
+          break;
+        }
+      }
+      out[j] = idx;
+    } else if (mine) {
+      out[j] = cols - 1;
+    }
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
+
+extern "C" int tl_sample(tl_ctx* ctx, const void* probs, int64_t cols, int32_t dtype, int64_t n,
+                         uint64_t seed, uint64_t stream, int64_t* out) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(dtype_is_float(dtype), "sampling takes fp32 or bf16 probabilities");
+  TL_REQUIRE(cols > 0 && n >= 0, "bad sizes");
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(probs && out, "null pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, (double)dtype_size(dtype) * cols + 8.0 * n);
+  const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  const uint32_t s0 = (uint32_t)stream, s1 = (uint32_t)(stream >> 32);
+  if (dtype == TL_F32)
+    sample_kernel<float><<<1, 1024, 0, ctx->stream>>>((const float*)probs, cols, n, k0, k1, s0, s1, out);
+  else
+    sample_kernel<bf16_t><<<1, 1024, 0, ctx->stream>>>((const bf16_t*)probs, cols, n, k0, k1, s0, s1, out);
+  return ls.finish("sample");
+}
 
 extern "C" int tl_random_normal(tl_ctx* ctx, void* y, int64_t n, uint64_t seed, uint64_t stream,
                                 float mean, float std_dev, int32_t dtype) {

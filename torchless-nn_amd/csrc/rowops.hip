@@ -1107,6 +1107,22 @@ static int norm_entry(tl_ctx* ctx, const void* x, const void* g, const void* b, 
   return ls.finish(RMS ? "rmsnorm_fwd" : "layernorm_fwd");
 }
 
+// out[i] = src[idx[i]] as raw elements; an index outside [0, src_len) latches bit 2 of the
+// status word (reported as bad input at the next synchronising call) and writes element 0
+template <typename U>
+__global__ __launch_bounds__(256) void take_kernel(const U* src, int64_t src_len,
+                                                   const int64_t* idx, int64_t n, U* out,
+                                                   int32_t* status) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t j = idx[i];
+    if (j < 0 || j >= src_len) {
+      atomicOr(status, 2);
+      j = 0;
+    }
+    out[i] = src[j];
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
@@ -1235,6 +1251,26 @@ int tl_transpose2d(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t co
   else
     transpose_kernel<uint32_t><<<grid, 256, 0, ctx->stream>>>((const uint32_t*)x, (uint32_t*)y, rows, cols, ldx, ldy);
   return ls.finish("transpose2d");
+}
+
+int tl_take(tl_ctx* ctx, const void* src, int64_t src_len, int32_t elem_bytes,
+            const int64_t* idx, int64_t n, void* out) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8,
+             "take moves 1-, 2-, 4- or 8-byte elements");
+  TL_REQUIRE(src_len > 0 && n >= 0, "bad sizes");
+  if (n == 0) return TL_OK;
+  TL_REQUIRE(src && idx && out, "null pointer");
+  LaunchScope ls(ctx, TL_KF_MISC, 0, (8.0 + 2.0 * elem_bytes) * n);
+  const unsigned g = grid_for(ctx, n, 256);
+  switch (elem_bytes) {
+    case 1: take_kernel<uint8_t><<<g, 256, 0, ctx->stream>>>((const uint8_t*)src, src_len, idx, n, (uint8_t*)out, ctx->status); break;
+    case 2: take_kernel<uint16_t><<<g, 256, 0, ctx->stream>>>((const uint16_t*)src, src_len, idx, n, (uint16_t*)out, ctx->status); break;
+    case 4: take_kernel<uint32_t><<<g, 256, 0, ctx->stream>>>((const uint32_t*)src, src_len, idx, n, (uint32_t*)out, ctx->status); break;
+    default: take_kernel<uint64_t><<<g, 256, 0, ctx->stream>>>((const uint64_t*)src, src_len, idx, n, (uint64_t*)out, ctx->status); break;
+  }
+  return ls.finish("take");
 }
 
 int tl_transpose2d_gain(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64_t cols,

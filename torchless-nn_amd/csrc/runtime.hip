@@ -118,7 +118,8 @@ static int check_status_word(tl_ctx* ctx) {
     int32_t zero = 0;
     TL_CHECK_HIP(hipMemcpy(ctx->status, &zero, sizeof(zero), hipMemcpyHostToDevice));
     return fail(TL_ERR_BAD_INPUT, "a kernel saw invalid input (status 0x%x): %s", word,
-                (word & 1) ? "token id out of range [0, vocab)" : "unknown");
+                (word & 1) ? "token id out of range [0, vocab)"
+                : (word & 2) ? "gather index out of range" : "unknown");
   }
   return TL_OK;
 }
@@ -402,6 +403,18 @@ int tl_memcpy_d2d(tl_ctx* ctx, void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return TL_OK;
   TL_REQUIRE(dst && src, "null pointer");
   TL_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+  return TL_OK;
+}
+
+int tl_memcpy2d_d2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size_t spitch,
+                    size_t width, size_t rows) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  if (width == 0 || rows == 0) return TL_OK;
+  TL_REQUIRE(dst && src, "null pointer");
+  TL_REQUIRE(width <= dpitch && width <= spitch, "width exceeds pitch");
+  TL_CHECK_HIP(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToDevice,
+                                ctx->stream));
   return TL_OK;
 }
 

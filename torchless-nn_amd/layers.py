@@ -179,11 +179,16 @@ class MultiHeadAttention(Layer):
         self.out_weight_grads = self.register_param(self.out_weights)
         self.out_bias_grads = self.register_param(self.out_bias)
 
-    def forward(self, input):
-        return self._forward(input, None)
+    def forward(self, input, cache=None, layer=0, pos0=0):
+        return self._forward(input, None, cache, layer, pos0)
 
-    def _forward(self, input, residual):
-        """Returns heads @ W_o + b_o, plus `residual` when given (fused in the epilogue)."""
+    def _forward(self, input, residual, cache=None, layer=0, pos0=0):
+        """Returns heads @ W_o + b_o, plus `residual` when given (fused in the epilogue).
+        With a KVCache (not in the reference, whose generation recomputes the window,
+        demo.ipynb:1526-1533), a decoder writes this call's keys and values into the cache
+        at positions pos0 .. and attends over positions 0 .. pos0 + T - 1."""
+        if cache is not None:
+            return self._forward_cached(input, residual, cache, layer, pos0)
         self.input = input
         B, T, C = input.shape
         H, D = self.num_heads, self.heads_dim
@@ -214,6 +219,38 @@ class MultiHeadAttention(Layer):
             heads = self._unfused(q, k, vt, B, T, C, H, D, dt, divisor)
         self.heads_out = heads
 
+        out = linear(heads.reshape(B * T, C), self.out_weights, self.out_bias,
+                     residual=(residual.reshape(B * T, C) if residual is not None else None))
+        self.output = out.reshape(B, T, C)
+        return self.res_dropout.forward(self.output)
+
+    def _forward_cached(self, input, residual, cache, layer, pos0):
+        self.input = input
+        B, T, C = input.shape
+        H, D = self.num_heads, self.heads_dim
+        if not self.is_decoder:
+            raise ValueError("a KV cache serves causal (decoder) attention only")
+        if pos0 < 0 or pos0 + T > min(cache.capacity, self.context_length):
+            raise ValueError(f"positions up to {pos0 + T} exceed the cache ({cache.capacity}) "
+                             f"or the context length ({self.context_length})")
+        if self.attn_dropout.dropout_rate > 0.0 and not self.attn_dropout.eval_mode:
+            self.attn_dropout.forward(input)  # raises: no dropout sampling at inference
+        dt, L, Tk = input.dtype, cache.capacity, pos0 + T
+        k, vt = cache.k[layer], cache.vt[layer]
+        q = xp.empty((B, H, T, D), dt)
+        linear(input.reshape(B * T, C), self.qkv_weights, self.qkv_bias,
+               qkv=(q, k, vt, T, H, H, D, L, pos0))
+        self.query, self.key_t, self.value = q, k, vt
+        divisor = float(np.float32(D ** 0.5))
+        heads = xp.empty((B, T, C), dt)
+        if self.fused and xp.attention_supported(dt, D, L):
+            xp.attention(q, k, vt, heads, n_heads_q=H, n_heads_kv=H, divisor=divisor,
+                         causal=True, offset=pos0, seq_k=Tk)
+            self.softmax = None
+        else:
+            self.softmax = _attend_cache_unfused(q, k, vt, heads, B, T, Tk, L, H, H, D, dt,
+                                                 divisor, pos0)
+        self.heads_out = heads
         out = linear(heads.reshape(B * T, C), self.out_weights, self.out_bias,
                      residual=(residual.reshape(B * T, C) if residual is not None else None))
         self.output = out.reshape(B, T, C)
@@ -342,9 +379,10 @@ class TransformerBlock(Layer):
         self.parameters = [*self.pre_attn_norm.parameters, *self.attn_block.parameters,
                            *self.pre_ffn_norm.parameters, *self.ffn.parameters]
 
-    def forward(self, input):
+    def forward(self, input, cache=None, layer=0, pos0=0):
+        """`cache` / `layer` / `pos0`: decode with a KV cache (MultiHeadAttention.forward)."""
         self.input = input
-        y = self.attn_block._forward(self.pre_attn_norm.forward(input), residual=input)
+        y = self.attn_block._forward(self.pre_attn_norm.forward(input), input, cache, layer, pos0)
         self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), residual=y)
         return self.output
 
@@ -523,26 +561,35 @@ class MultiQueryAttention(Layer):
         return self.output
 
     def _unfused(self, q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt, divisor, pos0):
-        g = Hq // Hkv
-        ldS = _round_up(Tk, 8)
-        scores = xp.empty((B, Hq, T, Tk), dt, pitch=ldS)
-        es = dt.itemsize
-        for hk in range(Hkv):  # one batched product per kv head: z = (b, query head in group)
-            qv = xp.DeviceTensor((1,), dt, buf=q.buf, offset=q.offset + hk * g * T * D * es)
-            kv = xp.DeviceTensor((1,), dt, buf=k.buf, offset=k.offset + hk * L * D * es)
-            sv = xp.DeviceTensor((1,), dt, buf=scores.buf, offset=scores.offset + hk * g * T * ldS * es)
-            xp.gemm(qv, kv, M=T, N=Tk, K=D, lda=D, ldb=D, b_layout=xp.TL_B_NK, C=sv, ldc=ldS,
-                    batch=B * g, batch_inner=g, sa=(Hq * T * D, T * D), sb=(Hkv * L * D, 0),
-                    sc=(Hq * T * ldS, T * ldS), divisor=divisor, family="gemm_batched")
-        probs = xp.softmax(scores, causal=True, period=T, offset=pos0, out=scores)
-        self.softmax = probs
-        for hk in range(Hkv):
-            pv = xp.DeviceTensor((1,), dt, buf=probs.buf, offset=probs.offset + hk * g * T * ldS * es)
-            vv = xp.DeviceTensor((1,), dt, buf=vt.buf, offset=vt.offset + hk * D * L * es)
-            hv = xp.DeviceTensor((1,), dt, buf=heads.buf, offset=heads.offset + hk * g * D * es)
-            xp.gemm(pv, vv, M=T, N=D, K=Tk, lda=ldS, ldb=L, b_layout=xp.TL_B_NK, C=hv,
-                    ldc=Hq * D, batch=B * g, batch_inner=g, sa=(Hq * T * ldS, T * ldS),
-                    sb=(Hkv * D * L, 0), sc=(T * Hq * D, D), family="gemm_batched")
+        self.softmax = _attend_cache_unfused(q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt,
+                                             divisor, pos0)
+
+
+def _attend_cache_unfused(q, k, vt, heads, B, T, Tk, L, Hq, Hkv, D, dt, divisor, pos0):
+    """Causal attention of q [B, Hq, T, D] at positions pos0 .. over the first Tk keys of a
+    cache k [B, Hkv, L, D] / vt [B, Hkv, D, L] with materialised probabilities: scores by
+    batched products, the causal softmax, P.V into heads [B, T, Hq D]. Returns the
+    probabilities [B, Hq, T, Tk] (row pitch a multiple of 8)."""
+    g = Hq // Hkv
+    ldS = _round_up(Tk, 8)
+    scores = xp.empty((B, Hq, T, Tk), dt, pitch=ldS)
+    es = dt.itemsize
+    for hk in range(Hkv):  # one batched product per kv head: z = (b, query head in group)
+        qv = xp.DeviceTensor((1,), dt, buf=q.buf, offset=q.offset + hk * g * T * D * es)
+        kv = xp.DeviceTensor((1,), dt, buf=k.buf, offset=k.offset + hk * L * D * es)
+        sv = xp.DeviceTensor((1,), dt, buf=scores.buf, offset=scores.offset + hk * g * T * ldS * es)
+        xp.gemm(qv, kv, M=T, N=Tk, K=D, lda=D, ldb=D, b_layout=xp.TL_B_NK, C=sv, ldc=ldS,
+                batch=B * g, batch_inner=g, sa=(Hq * T * D, T * D), sb=(Hkv * L * D, 0),
+                sc=(Hq * T * ldS, T * ldS), divisor=divisor, family="gemm_batched")
+    probs = xp.softmax(scores, causal=True, period=T, offset=pos0, out=scores)
+    for hk in range(Hkv):
+        pv = xp.DeviceTensor((1,), dt, buf=probs.buf, offset=probs.offset + hk * g * T * ldS * es)
+        vv = xp.DeviceTensor((1,), dt, buf=vt.buf, offset=vt.offset + hk * D * L * es)
+        hv = xp.DeviceTensor((1,), dt, buf=heads.buf, offset=heads.offset + hk * g * D * es)
+        xp.gemm(pv, vv, M=T, N=D, K=Tk, lda=ldS, ldb=L, b_layout=xp.TL_B_NK, C=hv,
+                ldc=Hq * D, batch=B * g, batch_inner=g, sa=(Hq * T * ldS, T * ldS),
+                sb=(Hkv * D * L, 0), sc=(T * Hq * D, D), family="gemm_batched")
+    return probs
 
 
 class GeGLUFeedForward(Layer):

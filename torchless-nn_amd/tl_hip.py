@@ -154,6 +154,7 @@ SIGNATURES = {
     "tl_memcpy_d2d": [_P, _P, _P, _SZ],
     "tl_memcpy2d_h2d": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ],
     "tl_memcpy2d_d2h": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ],
+    "tl_memcpy2d_d2d": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ],
     "tl_sync": [_P],
     "tl_event_create": [_P, ctypes.POINTER(_P)],
     "tl_event_record": [_P, _P],
@@ -166,6 +167,8 @@ SIGNATURES = {
     "tl_fill": [_P, _P, _I64, _I32, _F64],
     "tl_cast": [_P, _P, _P, _I64, _I32, _I32],
     "tl_random_normal": [_P, _P, _I64, ctypes.c_uint64, ctypes.c_uint64, _F32, _F32, _I32],
+    "tl_sample": [_P, _P, _I64, _I32, _I64, ctypes.c_uint64, ctypes.c_uint64, _P],
+    "tl_take": [_P, _P, _I64, _I32, _P, _I64, _P],
     "tl_transpose2d": [_P, _P, _P, _I64, _I64, _I64, _I64, _I32],
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
     "tl_transpose2d_gain": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _F32, _I32],
@@ -380,7 +383,46 @@ class DeviceTensor:
         return self.pitch == self.ncols
 
     def __len__(self):
+        if not self.shape:
+            raise TypeError("len() of a 0-d tensor")
         return self.shape[0]
+
+    def __getitem__(self, key):
+        """Basic indexing (integers, negative ones included, and step-1 slices) as a view of
+        the same memory, where the result keeps one row pitch: evenly spaced whole rows with
+        a column range (e.g. the notebook's `tokens[:, a:]`, `probs[0, -1]`), or one element.
+        Other selections raise NotImplementedError rather than copy."""
+        if not isinstance(key, tuple):
+            key = (key,)
+        if any(k is Ellipsis or k is None for k in key):
+            raise NotImplementedError("indexing with ... or None")
+        if not self.shape or len(key) > self.ndim:
+            raise IndexError(f"too many indices for a {self.ndim}-d tensor")
+        key = key + (slice(None),) * (self.ndim - len(key))
+        lead, last = key[:-1], key[-1]
+        rows = np.arange(self.nrows).reshape(self.shape[:-1])[lead]  # numpy checks the bounds
+        row_shape, flat = rows.shape, rows.reshape(-1)
+        n = self.ncols
+        if isinstance(last, slice):
+            c0, c1, step = last.indices(n)
+            if step != 1:
+                raise NotImplementedError("slices with a step")
+            ncol, col_shape = max(0, c1 - c0), (max(0, c1 - c0),)
+        else:
+            c0 = int(last) + (n if int(last) < 0 else 0)
+            if not 0 <= c0 < n:
+                raise IndexError(f"index {int(last)} out of range for size {n}")
+            ncol, col_shape = 1, ()
+        if flat.size == 0 or ncol == 0:
+            return DeviceTensor(row_shape + col_shape, self.dtype, buf=self.buf, offset=self.offset)
+        off = self.offset + (int(flat[0]) * self.pitch + c0) * self.dtype.itemsize
+        if flat.size == 1:
+            return DeviceTensor(row_shape + col_shape, self.dtype, buf=self.buf, offset=off)
+        steps = np.diff(flat)
+        if col_shape == () or not np.all(steps == steps[0]):
+            raise NotImplementedError("this selection is not a view with one row pitch")
+        return DeviceTensor(row_shape + col_shape, self.dtype, pitch=int(steps[0]) * self.pitch,
+                            buf=self.buf, offset=off)
 
     def __repr__(self):
         return f"DeviceTensor(shape={self.shape}, dtype={self.dtype}, pitch={self.pitch})"
@@ -509,6 +551,54 @@ def array(obj, dtype=None) -> DeviceTensor:
 asarray = array
 
 
+def arange(start, stop=None, step=1, dtype=None) -> DeviceTensor:
+    """xp.arange (reference demo.ipynb:1531 samples from xp.arange(0, vocab_size))."""
+    host = np.arange(start, stop, step) if stop is not None else np.arange(start)
+    if dtype is not None:
+        host = host.astype(as_dtype(dtype).host if as_dtype(dtype) is not bfloat16 else np.float32)
+    return array(host, dtype=dtype)
+
+
+def concatenate(tensors, axis=0) -> DeviceTensor:
+    """xp.concatenate of same-dtype tensors that agree except along `axis` (reference
+    demo.ipynb:1533 appends each sampled token with axis=1), as device row copies."""
+    tensors = list(tensors)
+    if not tensors:
+        raise ValueError("need at least one tensor to concatenate")
+    first = tensors[0]
+    nd = first.ndim
+    axis = axis + nd if axis < 0 else axis
+    if nd == 0 or not 0 <= axis < nd:
+        raise ValueError(f"axis {axis} out of range for {nd}-d tensors")
+    for t in tensors:
+        if t.dtype is not first.dtype or t.ndim != nd or any(
+                t.shape[i] != first.shape[i] for i in range(nd) if i != axis):
+            raise ValueError("concatenate needs one dtype and matching shapes off the axis")
+    shape = list(first.shape)
+    shape[axis] = sum(t.shape[axis] for t in tensors)
+    out = DeviceTensor(tuple(shape), first.dtype)
+    es = first.dtype.itemsize
+    c = ctx()
+    outer = _prod(shape[:axis])            # blocks along the leading axes
+    at = 0                                 # element offset inside each block of `out`
+    block = _prod(shape[axis:])            # elements of one block of `out`
+    for t in tensors:
+        inner = _prod(t.shape[axis:])      # elements of one block of t
+        if t.size:
+            if axis == nd - 1 or t.contiguous:
+                if axis == nd - 1:         # each row of t is one block
+                    check(c.lib.tl_memcpy2d_d2d(c.handle, out.ptr + at * es, block * es, t.ptr,
+                                                t.pitch * es, inner * es, outer))
+                else:
+                    check(c.lib.tl_memcpy2d_d2d(c.handle, out.ptr + at * es, block * es, t.ptr,
+                                                inner * es, inner * es, outer))
+            else:
+                raise NotImplementedError("concatenate of a padded tensor off its last axis")
+        at += inner
+    _wrote(out)
+    return out
+
+
 def asnumpy(t) -> np.ndarray:
     return t.get() if isinstance(t, DeviceTensor) else np.asarray(t)
 
@@ -560,8 +650,52 @@ class _Rng:
         return array(self._g.integers(low, high, size=size), dtype=dtype)
 
 
+# key and next counter stream of xp.random.choice (seeded from TL_SEED; xp.random.seed sets it)
+_SAMPLER = {"seed": int(os.environ.get("TL_SEED", "0")), "stream": 0}
+
+
+def _choice(a, size=None, replace=True, p=None):
+    """xp.random.choice(a, size, p=probs) (reference demo.ipynb:1531): draws on the device
+    from the categorical distribution p (tl_sample; each call takes the next Philox stream
+    of the sampler's key), then gathers the drawn entries of `a` (an int means arange(a)).
+    Returns a device tensor of shape `size` (a's dtype, int64 for an int `a`)."""
+    if p is None or not replace:
+        raise NotImplementedError("choice is implemented with p given and replace=True")
+    if not isinstance(p, DeviceTensor):
+        p = array(np.asarray(p, dtype=np.float32), dtype=float32)
+    if p.ndim != 1 or not p.contiguous:
+        raise ValueError("p must be one contiguous row of probabilities")
+    n_cand = int(a) if not isinstance(a, DeviceTensor) else a.size
+    if n_cand != p.size:
+        raise ValueError(f"a has {n_cand} entries but p has {p.size}")
+    shape = () if size is None else ((int(size),) if isinstance(size, (int, np.integer))
+                                     else tuple(int(v) for v in size))
+    n = _prod(shape)
+    idx = DeviceTensor((max(n, 1),), int64)
+    c = ctx()
+    stream = _SAMPLER["stream"]
+    _SAMPLER["stream"] += 1
+    check(c.lib.tl_sample(c.handle, p.ptr, p.size, p.dtype.code, n, _SAMPLER["seed"] & (2 ** 64 - 1),
+                          stream, idx.ptr))
+    if not isinstance(a, DeviceTensor):
+        return DeviceTensor(shape, int64, buf=idx.buf, offset=idx.offset)
+    if a.ndim != 1 or not a.contiguous:
+        raise ValueError("a must be a 1-d contiguous tensor or an int")
+    out = DeviceTensor(shape, a.dtype)
+    check(c.lib.tl_take(c.handle, a.ptr, a.size, a.dtype.itemsize, idx.ptr, n, out.ptr))
+    return out
+
+
+def _seed(seed=None):
+    """xp.random.seed: fixes the sampler's key and restarts its streams."""
+    _SAMPLER["seed"] = int(seed) if seed is not None else int(os.environ.get("TL_SEED", "0"))
+    _SAMPLER["stream"] = 0
+
+
 class random:  # noqa: N801  (mirrors `xp.random`)
     default_rng = _Rng
+    choice = staticmethod(_choice)
+    seed = staticmethod(_seed)
 
 
 # ---- kernel wrappers used by the layers ------------------------------------------------

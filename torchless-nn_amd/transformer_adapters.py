@@ -120,18 +120,22 @@ class GPTEmbedFront(Layer):
         self.embedding_table = embedding_table
         self.parameters.append(self.embedding_table.table)
 
-    def forward(self, input):
+    def forward(self, input, pos0=0):
+        """`pos0`: the ids sit at positions pos0 .. (a decode step after a cached prefix;
+        the reference always starts at 0, transformer_adapters.py:146-153)."""
         if not isinstance(input, xp.DeviceTensor):
             input = xp.array(np.asarray(input))
         self.input = input
         if input.ndim != 2:
             raise ValueError("token ids must be [batch, time]")
+        if not input.contiguous:
+            input = input.copy()
         B, T = input.shape
-        if T > self.context_length:
-            raise ValueError(f"sequence length {T} exceeds the positional table "
+        if pos0 < 0 or pos0 + T > self.context_length:
+            raise ValueError(f"positions up to {pos0 + T} exceed the positional table "
                              f"({self.context_length})")
         self.output = xp.embed(input, self.embedding_table.table, self.pos_embedding_table, T,
-                               out_shape=(B, T, self.embedding_table.embed_size))
+                               pos0=pos0, out_shape=(B, T, self.embedding_table.embed_size))
         return self.output
 
 
