@@ -488,6 +488,18 @@ def char_gpt_bench(xp, steps=50, warmup=5):
         net.predict(ids)
     host_ms = (time.perf_counter() - t0) / steps * 1e3  # issue time (the queue runs ahead)
     xp.synchronize()
+    # the same forward captured once as a HIP graph and replayed (one host call per forward)
+    fwd = net.capture(ids)
+    fwd(ids)
+    xp.synchronize()
+    e0.record()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fwd(ids)
+    graph_host_ms = (time.perf_counter() - t0) / steps * 1e3
+    e1.record()
+    graph_ms = e0.elapsed_ms(e1) / steps
+    fwd.destroy()
     xp.kprof_reset()
     xp.kprof_enable(list(xp.KFAMILY))
     for _ in range(steps):
@@ -499,6 +511,9 @@ def char_gpt_bench(xp, steps=50, warmup=5):
                        "d 128, 4 heads, GeLU, fp32, batch 4 x 128 token ids, weights seeded",
            "ms_per_step": round(ms, 4), "tokens_per_s": round(512 / (ms * 1e-3), 1),
            "host_issue_ms_per_step": round(host_ms, 4),
+           "graph_ms_per_step": round(graph_ms, 4),
+           "graph_tokens_per_s": round(512 / (graph_ms * 1e-3), 1),
+           "graph_host_ms_per_step": round(graph_host_ms, 4),
            "kernel_breakdown": {f: {"ms_per_step": round(r["ms"] / steps, 4),
                                     "launches_per_step": r["launches"] // steps}
                                 for f, r in fam.items() if r["launches"]}}

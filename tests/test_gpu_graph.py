@@ -332,3 +332,29 @@ def test_staged_host_copies_take_the_data_at_call_time(tl):
     want = big.copy()
     big[:] = 1
     assert np.array_equal(_bits(d), want)
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_captured_forward_matches_predict(tl, dt):
+    """Network.capture: the char-level GPT forward (config 1 shape) replayed from one graph
+    gives predict()'s probabilities bit for bit for several inputs, host and device ids,
+    with eager forwards between the replays."""
+    xp = tl["xp"]
+    import gpt
+    cfg = dict(vocab=65, ctx=128, layers=4, d=128, heads=4, act="gelu")
+    net, _ = gpt.build_gpt(cfg, dtype=dt)
+    gpt.seed_parameters(net, 3, 0.3 if dt == "fp32" else 0.05)
+    rng = np.random.default_rng(4)
+    first = rng.integers(0, 65, (4, 128)).astype(np.int32)
+    fwd = net.capture(first)
+    for r in range(4):
+        ids = first if r == 0 else rng.integers(0, 65, (4, 128)).astype(np.int32)
+        src = ids if r % 2 == 0 else xp.array(ids)
+        got = fwd(src)
+        want = net.predict(ids)  # eager, between replays
+        assert got is fwd.output
+        # probability rows are padded to 72 columns: compare the 65 valid ones
+        assert np.array_equal(got.get().view(np.uint32), want.get().view(np.uint32)), r
+    with pytest.raises(ValueError):
+        fwd(xp.array(first[:2]))
+    fwd.destroy()

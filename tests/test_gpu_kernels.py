@@ -906,10 +906,45 @@ def test_attention_fused_rejects_unsupported(xp):
     with pytest.raises(xp.TLError):
         xp.attention(q, q, xp.empty((1, 1, 64, 12), "bf16"), xp.empty((1, 12, 64), "bf16"),
                      n_heads_q=1, n_heads_kv=1, divisor=8.0)  # Tk % 8 != 0
-    q32 = xp.empty((1, 1, 16, 64), "fp32").fill(0)
+    q32 = xp.empty((1, 1, 16, 256), "fp32").fill(0)  # fp32 takes head_dim 32, 64, 128
     with pytest.raises(xp.TLError):
-        xp.attention(q32, q32, xp.empty((1, 1, 64, 16), "fp32"), xp.empty((1, 16, 64), "fp32"),
-                     n_heads_q=1, n_heads_kv=1, divisor=8.0)
+        xp.attention(q32, q32, xp.empty((1, 1, 256, 16), "fp32"), xp.empty((1, 16, 256), "fp32"),
+                     n_heads_q=1, n_heads_kv=1, divisor=16.0)
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("case", [
+    # B, Hq, Hkv, Tq, Tk, Lk, causal, offset
+    (2, 3, 3, 8, 8, 8, True, 0),
+    (2, 3, 3, 136, 136, 136, False, 0),
+    (1, 2, 2, 520, 520, 520, True, 0),
+    (2, 3, 3, 65, 65, 72, False, 0),        # ViT-like: 65 keys in a capacity of 72 (NaN pad)
+    (2, 8, 1, 40, 96, 104, True, 56),       # one shared kv head, queries at an offset
+    (2, 4, 2, 1, 77, 80, True, 76),         # a decode step
+    (8, 12, 12, 1024, 1024, 1024, True, 0),  # the GPT-2-small shape (D = 64 is config 3)
+])
+def test_attention_fused_f32(xp, D, case):
+    """fp32 attention on the fp32 matrix cores (the reference's FLOAT_TYPE) against the
+    float64 definition at the fp32 bar, with NaN in the key/value capacity padding."""
+    B, Hq, Hkv, Tq, Tk, Lk, causal, offset = case
+    if B * Hq * Tq > 20000 and D != 64:
+        pytest.skip("the GPT-2 shape runs at its own head dim only")
+    rng = np.random.default_rng(Tq + Tk + D)
+    q = rng.standard_normal((B, Hq, Tq, D)).astype(F32)
+    k = rng.standard_normal((B, Hkv, Lk, D)).astype(F32)
+    vt = rng.standard_normal((B, Hkv, D, Lk)).astype(F32)
+    k[:, :, Tk:] = np.nan
+    vt[:, :, :, Tk:] = np.nan
+    out = xp.empty((B, Tq, Hq * D), "fp32")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "fp32"), up(xp, k, "fp32"), up(xp, vt, "fp32"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=divisor, causal=causal, offset=offset, seq_k=Tk)
+    got = out.get()
+    assert np.all(np.isfinite(got)), case
+    sel = [0, B - 1] if B * Hq * Tq > 20000 else list(range(B))
+    want = attention_ref(q[sel], k[sel][:, :, :Tk], vt[sel][:, :, :, :Tk], Hq, Hkv, divisor,
+                         causal, offset)
+    assert ref.max_rel(got[sel], want) <= 1e-5, case
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])

@@ -812,6 +812,203 @@ int attention_scratch_setup(tl_ctx* ctx) {
   return TL_OK;
 }
 
+// fp32 attention (the reference's FLOAT_TYPE, backend.py:24; layers.py:286-304) on the
+// fp32 matrix cores, v_mfma_f32_16x16x4f32: fp32 products and sums, so the scores, the
+// softmax and P.V keep full fp32 precision. The structure is attention_fwd_kernel's: 4
+// waves x 16 query rows, 64-key chunks of K and V^T staged in LDS (registers -> LDS, double
+// buffered), S^T = K Q^T so a lane holds 4 keys of one query row, online softmax with lazy
+// rescaling, O^T += V^T P^T, causal query blocks paired so workgroups carry equal work.
+// A 16x16x4 MFMA takes one element per lane per operand. Q.K sums over d in any order, so
+// lane group fg covers the contiguous d range [fg D/4, (fg + 1) D/4) one d per MFMA (Q and K
+// read as 16-byte chunks); P.V step u = (key tile j, v) takes key 16 j + 4 fg + v from lane
+// group fg, which is exactly the probability that lane holds, and reads V^T[d][16 j + 4 fg
+// .. + 3] as one 16-byte chunk. LDS rows are stored with their 16-byte chunks XOR-swizzled
+// by row so the 16 rows of a fragment read hit distinct banks.
+template <int D>
+__global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
+  constexpr int BKV = 64;
+  constexpr int KCH = D / 4;          // 16-byte chunks per K row
+  constexpr int KSW = KCH - 1;        // swizzle mask of a K row (KCH is a power of two)
+  constexpr int DQ = D / 4;           // d values per lane group (one per MFMA)
+  constexpr int DT = D / 16;          // 16-row d tiles of the output
+  constexpr int K_LOADS = BKV * KCH / 256;
+  constexpr int V_LOADS = D * 16 / 256;  // V^T chunk: D rows x 16 chunks
+  static_assert(K_LOADS >= 1 && V_LOADS >= 1, "head_dim too small");
+  __shared__ __attribute__((aligned(16))) float Ks[2][BKV * D];
+  __shared__ __attribute__((aligned(16))) float Vs[2][D * BKV];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int bh = blockIdx.y;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const int nqb = (p.Tq + 63) / 64;
+  const int x = (int)blockIdx.x;
+  const float* qg = reinterpret_cast<const float*>(p.q);
+  const float* kg = reinterpret_cast<const float*>(p.k);
+  const float* vg = reinterpret_cast<const float*>(p.vt);
+  float* og = reinterpret_cast<float*>(p.out);
+  for (int pass = 0; pass < (p.causal ? 2 : 1); ++pass) {
+    const int qb = pass == 0 ? nqb - 1 - x : x;
+    if (pass == 1 && qb >= nqb - 1 - x) break;
+    const int q0 = qb * 64 + wave * 16;
+    const float* qh = qg + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
+    const float* kh = kg + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
+    const float* vh = vg + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
+
+    // Q (second operand of S^T): lane holds Q[q0 + fr][fg DQ + s], s < DQ
+    float qf[DQ];
+    {
+      const int qi = min(q0 + fr, p.Tq - 1);
+#pragma unroll
+      for (int c = 0; c < DQ / 4; ++c) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(qh + (int64_t)qi * D + fg * DQ + 4 * c);
+        qf[4 * c] = v[0]; qf[4 * c + 1] = v[1]; qf[4 * c + 2] = v[2]; qf[4 * c + 3] = v[3];
+      }
+    }
+    const int q_last = min(qb * 64 + 63, p.Tq - 1);
+    int kv_end = p.Tk;
+    if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q_last + p.offset + 1);
+    const int nchunks = (kv_end + BKV - 1) / BKV;
+
+    f32x4 rk[K_LOADS], rv[V_LOADS];
+    auto load_chunk_regs = [&](int kv0) {
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
+        const int kv = kv0 + r;
+        rk[i] = kv < p.Tk ? *reinterpret_cast<const f32x4*>(kh + (int64_t)kv * D + 4 * c)
+                          : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int i = 0; i < V_LOADS; ++i) {
+        // positions past Tk (capacity padding, never written) are zeroed: 0 * NaN is not 0
+        const int idx = i * 256 + tid, r = idx >> 4, c = idx & 15;
+        const int kv = kv0 + 4 * c;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (kv < p.Tk) {
+          v = *reinterpret_cast<const f32x4*>(vh + (int64_t)r * p.Lk + kv);
+#pragma unroll
+          for (int e = 1; e < 4; ++e)
+            if (kv + e >= p.Tk) v[e] = 0.f;
+        }
+        rv[i] = v;
+      }
+    };
+    auto store_chunk_lds = [&](int buf) {
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
+        *reinterpret_cast<f32x4*>(&Ks[buf][r * D + ((c ^ (r & KSW)) << 2)]) = rk[i];
+      }
+#pragma unroll
+      for (int i = 0; i < V_LOADS; ++i) {
+        const int idx = i * 256 + tid, r = idx >> 4, c = idx & 15;
+        *reinterpret_cast<f32x4*>(&Vs[buf][r * BKV + ((c ^ (r & 15)) << 2)]) = rv[i];
+      }
+    };
+
+    f32x4 o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_part = 0.f;
+    const int qpos = q0 + fr;
+
+    load_chunk_regs(0);
+    store_chunk_lds(0);
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ++ch) {
+      const int cur = ch & 1;
+      const int kv0 = ch * BKV;
+      if (ch + 1 < nchunks) load_chunk_regs(kv0 + BKV);
+
+      f32x4 s[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int r = j * 16 + fr;
+#pragma unroll
+        for (int c = 0; c < DQ / 4; ++c) {
+          const int cc = fg * (DQ / 4) + c;
+          const f32x4 kf = *reinterpret_cast<const f32x4*>(&Ks[cur][r * D + ((cc ^ (r & KSW)) << 2)]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[e], qf[4 * c + e], s[j], 0, 0, 0);
+        }
+      }
+      float mx = -INFINITY;
+      const bool full = kv0 + BKV <= p.Tk &&
+                        (!p.causal || (int64_t)(kv0 + BKV - 1) <= (int64_t)q0 + p.offset);
+      if (full) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[j][v]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int kv = kv0 + j * 16 + 4 * fg + v;
+            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
+            s[j][v] = ok ? s[j][v] : -INFINITY;
+            mx = fmaxf(mx, s[j][v]);
+          }
+      }
+      if (__any(mx * p.scale_log2 > m_run + 8.0f)) {
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mxs = mx * p.scale_log2;
+        const bool grow = mxs > m_run + 8.0f;
+        const float m_new = grow ? mxs : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_part *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o[t][v] *= alpha;
+        m_run = m_new;
+      }
+      const float m_ref = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][v], p.scale_log2, -m_ref));
+          s[j][v] = e;
+          l_part += e;
+        }
+      // O^T += V^T P^T: step (j, v) takes key 16 j + 4 fg + v of lane group fg
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int r = t * 16 + fr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int cc = 4 * j + fg;
+          const f32x4 vf = *reinterpret_cast<const f32x4*>(&Vs[cur][r * BKV + ((cc ^ (r & 15)) << 2)]);
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[v], s[j][v], o[t], 0, 0, 0);
+        }
+      }
+      if (ch + 1 < nchunks) store_chunk_lds(cur ^ 1);
+      __syncthreads();
+    }
+
+    float l_run = l_part + __shfl_xor(l_part, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (qpos < p.Tq) {
+      const float inv = 1.0f / l_run;
+      float* orow = og + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const f32x4 w = {o[t][0] * inv, o[t][1] * inv, o[t][2] * inv, o[t][3] * inv};
+        *reinterpret_cast<f32x4*>(orow + t * 16 + 4 * fg) = w;
+      }
+    }
+  }
+}
+
 template <int D>
 static void launch_decode(int nw, int jt, dim3 g1, dim3 g2, hipStream_t st, const AttnParams& p,
                           const DecodeWs& w) {
@@ -847,8 +1044,10 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
   TL_REQUIRE(divisor > 0.f, "divisor must be positive");
   TL_REQUIRE(!causal || offset >= 0, "causal attention needs offset >= 0");
   TL_REQUIRE(batch * n_heads_q <= 65535, "batch * heads exceeds 65535");
-  if (dtype != TL_BF16)
-    return fail(TL_ERR_UNSUPPORTED, "fused attention is implemented for bf16 only");
+  if (dtype != TL_BF16 && dtype != TL_F32)
+    return fail(TL_ERR_UNSUPPORTED, "fused attention takes bf16 or fp32");
+  if (dtype == TL_F32 && !(head_dim == 32 || head_dim == 64 || head_dim == 128))
+    return fail(TL_ERR_UNSUPPORTED, "fp32 fused attention supports head_dim 32, 64, 128");
   if (!(head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256))
     return fail(TL_ERR_UNSUPPORTED, "fused attention supports head_dim 32, 64, 128, 256");
   const int64_t cap = kv_capacity > 0 ? kv_capacity : seq_k;
@@ -857,6 +1056,9 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     return fail(TL_ERR_UNSUPPORTED, "fused attention needs kv_capacity %% 8 == 0 and ld_out %% 4 == 0");
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)vt) & 15u || ((uintptr_t)out & 7u))
     return fail(TL_ERR_UNSUPPORTED, "fused attention needs 16-byte aligned q, k, vt");
+  if (dtype == TL_F32 && (((uintptr_t)out & 15u) || (pos_dev || rope)))
+    return fail(TL_ERR_UNSUPPORTED, "fp32 fused attention needs a 16-byte aligned output and "
+                "takes no device position or fused RoPE");
   AttnParams p;
   p.q = (const bf16_t*)q; p.k = (const bf16_t*)k; p.vt = (const bf16_t*)vt; p.out = (bf16_t*)out;
   p.Hq = (int)n_heads_q; p.Hkv = (int)n_heads_kv; p.Tq = (int)seq_q; p.Tk = (int)seq_k;
@@ -882,7 +1084,18 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
   const double bh = (double)batch * n_heads_q;
   const double flops = bh * kept * 4.0 * head_dim;
   const double bytes = 2.0 * (bh * seq_q * head_dim * 2 + (double)batch * n_heads_kv * seq_k * head_dim * 2);
-  LaunchScope ls(ctx, noalloc ? -1 : TL_KF_ATTENTION, flops, bytes);
+  LaunchScope ls(ctx, noalloc ? -1 : TL_KF_ATTENTION, dtype == TL_F32 ? flops : flops,
+                 dtype == TL_F32 ? 2.0 * bytes : bytes);
+  if (dtype == TL_F32) {
+    const int64_t nqb = (seq_q + 63) / 64;
+    const dim3 grid((unsigned)(causal ? (nqb + 1) / 2 : nqb), (unsigned)(batch * n_heads_q));
+    switch (head_dim) {
+      case 32: attention_fwd_f32_kernel<32><<<grid, 256, 0, ctx->stream>>>(p); break;
+      case 64: attention_fwd_f32_kernel<64><<<grid, 256, 0, ctx->stream>>>(p); break;
+      default: attention_fwd_f32_kernel<128><<<grid, 256, 0, ctx->stream>>>(p); break;
+    }
+    return ls.finish("attention_fwd_f32");
+  }
   const int64_t rows_per_kv = (n_heads_q / n_heads_kv) * seq_q;
   if (rows_per_kv <= 16) {  // decode: split the keys over many small workgroups
     DecodeWs w;

@@ -1680,13 +1680,18 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
                                 (double)eo * d->M * d->N * (d->residual ? 2 : 1));
   // fp32 operands on the matrix cores under the same layout rules (4-element alignment) when
   // there are at least 128 output tiles of 128x128; fewer stay on the split-K VALU kernel.
-  const bool mfma32 = d->dtype_in == TL_F32 && d->b_layout == TL_B_NK && d->K % 4 == 0 &&
-                      d->lda % 4 == 0 && d->ldb % 4 == 0 && d->sa_o % 4 == 0 &&
-                      d->sa_i % 4 == 0 && d->sb_o % 4 == 0 && d->sb_i % 4 == 0 &&
-                      al16(d->A) && al16(d->B) && d->lda * 128 < (1LL << 31) &&
-                      d->ldb * 128 < (1LL << 31) &&
-                      ((d->M + 127) / 128) * ((d->N + 127) / 128) * batch >= 128;
-  const int family = (mfma || mfma32) ? d->family : TL_KF_GEMM_SIMT;
+  const bool mfma32_layout = d->dtype_in == TL_F32 && d->b_layout == TL_B_NK && d->K % 4 == 0 &&
+                             d->lda % 4 == 0 && d->ldb % 4 == 0 && d->sa_o % 4 == 0 &&
+                             d->sa_i % 4 == 0 && d->sb_o % 4 == 0 && d->sb_i % 4 == 0 &&
+                             al16(d->A) && al16(d->B) && d->lda * 128 < (1LL << 31) &&
+                             d->ldb * 128 < (1LL << 31);
+  const bool mfma32 = mfma32_layout && ((d->M + 127) / 128) * ((d->N + 127) / 128) * batch >= 128;
+  // small fp32 products with a short K loop (the char-level GPT: M = 512, K = 128 .. 512)
+  // on 64x64 fp32 MFMA tiles rather than the vector ALUs; long K with few tiles stays on the
+  // split-K vector kernel
+  const bool mfma32_small = mfma32_layout && !mfma32 && d->K <= 1024 &&
+                            ((d->M + 63) / 64) * ((d->N + 63) / 64) * batch >= 8;
+  const int family = (mfma || mfma32 || mfma32_small) ? d->family : TL_KF_GEMM_SIMT;
   TL_REQUIRE(family >= 0 && family < TL_KF_COUNT, "bad kernel family");
   const bool f32out = d->dtype_out == TL_F32;
   const bool skinny = mfma && (d->tile == TL_TILE_SKINNY || (d->tile == TL_TILE_AUTO && d->M <= 16));
@@ -1784,6 +1789,15 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
     else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
     return ls.finish("gemm_mfma_f32");
+  }
+  if (mfma32_small) {
+    p.tiles_m = (int)((d->M + 63) / 64);
+    p.tiles_n = (int)((d->N + 63) / 64);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
+    LaunchScope ls(ctx, family, flops, bytes);
+    if (f32out) gemm_mfma_f32_kernel<float, 64, 64, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    else gemm_mfma_f32_kernel<bf16_t, 64, 64, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    return ls.finish("gemm_mfma_f32_small");
   }
   p.tiles_m = (int)((d->M + 63) / 64);
   p.tiles_n = (int)((d->N + 63) / 64);

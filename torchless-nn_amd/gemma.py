@@ -89,7 +89,8 @@ class GemmaDecoder:
         if cache is None:
             cache = self.new_cache(B, T + n_new)
         if (graph and not return_logits and n_new >= 2
-                and xp.attention_supported(self.dtype, self.cfg["head_dim"], cache.capacity)):
+                and xp.attention_decode_dev_supported(self.dtype, self.cfg["head_dim"],
+                                                      cache.capacity)):
             return self._generate_graph(ids, n_new, cache)
         logits = self.forward(ids, cache, 0)
         steps, kept = [], []

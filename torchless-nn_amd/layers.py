@@ -13,9 +13,9 @@ reference; every forward is a handful of libtl kernel launches on one HIP stream
 The MFMA GEMMs read a weight in a K-contiguous copy ([out, in]) that is packed on the
 device the first time the weight is used and again after its buffer has been written (by
 `set`, `fill` or any kernel writing into any view of it). bf16 weights always take that copy;
-fp32 weights take it for products the fp32 matrix-core kernel runs (K % 4 == 0 and at least
-128 output tiles of 128x128), which doubles their HBM use, and are read in place by the fp32
-VALU GEMM otherwise.
+fp32 weights take it for products the fp32 matrix-core kernels run (K % 4 == 0, and either
+at least 128 output tiles of 128x128 or K <= 1024 with at least 8 tiles of 64x64), which
+doubles their HBM use, and are read in place by the fp32 VALU GEMM otherwise.
 """
 import numpy as np
 
@@ -90,9 +90,11 @@ def linear(x2d, w, bias=None, act=xp.TL_ACT_NONE, residual=None, out=None, qkv=N
     x2d, norm_eps = _prenorm(x2d, prenorm, w.dtype)
     if qkv is None and out is None:
         out = xp.empty((M, N), x2d.dtype)
-    # bf16 always, fp32 when the product is large enough for the fp32 matrix-core kernel
-    # (at least 128 output tiles of 128x128, K % 4 == 0): both read B as [N, K]
-    if w.dtype is xp.bfloat16 or (K % 4 == 0 and -(-M // 128) * -(-N // 128) >= 128):
+    # bf16 always; fp32 when the fp32 matrix-core kernels take the product (K % 4 == 0, and
+    # either at least 128 output tiles of 128x128 or K <= 1024 with 8 or more 64x64 tiles):
+    # both read B as [N, K]
+    if w.dtype is xp.bfloat16 or (K % 4 == 0 and (-(-M // 128) * -(-N // 128) >= 128 or
+                                                  (K <= 1024 and -(-M // 64) * -(-N // 64) >= 8))):
         B, ldb, layout = _packed_nk(w, fold), K, xp.TL_B_NK
     else:
         B, ldb, layout = w, w.pitch, xp.TL_B_KN
@@ -490,7 +492,7 @@ class MultiQueryAttention(Layer):
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.heads_dim
         if (cache is not None and self.fused and (Hq // Hkv) * T <= 16 and
                 pos0 + T <= min(cache.capacity, self.context_length) and
-                xp.attention_supported(input.dtype, D, cache.capacity)):
+                xp.attention_decode_dev_supported(input.dtype, D, cache.capacity)):
             # a decode step: the same kernels as a replayed one (position in device memory)
             dpos = DevicePosition.at(pos0, T, D, self.rope_base)
             return self._forward_dev(input, residual, cache, layer, dpos, prenorm)
@@ -540,8 +542,8 @@ class MultiQueryAttention(Layer):
         if dpos.T != T or dpos.head_dim != D or dpos.base != self.rope_base:
             raise ValueError("the device position's RoPE table does not match this call")
         dt = input.dtype
-        if not (self.fused and xp.attention_supported(dt, D, cache.capacity)):
-            raise ValueError("decoding at a device position needs the fused attention kernel")
+        if not (self.fused and xp.attention_decode_dev_supported(dt, D, cache.capacity)):
+            raise ValueError("decoding at a device position needs the fused bf16 attention kernel")
         q = xp.empty((B, Hq, T, D), dt)
         k, vt, L = cache.k[layer], cache.vt[layer], cache.capacity
         linear(input.reshape(B * T, C), self.qkv_weights, qkv=(q, k, vt, T, Hq, Hkv, D, L, dpos.pos),

@@ -2,7 +2,7 @@
 import tl_hip as xp
 from utils import Layer
 
-__all__ = ["Network"]
+__all__ = ["Network", "CapturedForward"]
 
 
 class Network:
@@ -29,3 +29,42 @@ class Network:
 
     def train(self, *args, **kwargs):
         raise NotImplementedError("training is not part of the MI355X runtime")
+
+    def capture(self, example_input):
+        """predict() captured once as a HIP graph for inputs shaped like `example_input`
+        (not in the reference, which dispatches every op from Python each call,
+        network.py:36-39): see CapturedForward."""
+        return CapturedForward(self, example_input)
+
+
+class CapturedForward:
+    """A forward captured as one HIP graph. Each call copies the input into the captured
+    input tensor (stream-ordered) and replays every kernel of the forward with one launch,
+    then returns the captured output tensor: the same device tensor every call, rewritten
+    by the next call, so read or copy it before calling again. destroy() (or garbage
+    collection) frees the graph and the intermediates it holds."""
+
+    def __init__(self, net, example_input):
+        if not isinstance(example_input, xp.DeviceTensor):
+            example_input = xp.array(example_input)
+        self.net = net
+        self.input = example_input.copy()
+        net.predict(self.input)  # eager first: packed weights and scratch exist before capture
+        with xp.capture() as cap:
+            self.output = net.predict(self.input)
+        self._graph = cap
+
+    def __call__(self, input):
+        if isinstance(input, xp.DeviceTensor):
+            if input.shape != self.input.shape or input.dtype is not self.input.dtype:
+                raise ValueError(f"captured for {self.input.shape} {self.input.dtype}, got "
+                                 f"{input.shape} {input.dtype}")
+            src = input if input.contiguous else input.copy()
+            xp.copy_into(self.input, src)
+        else:
+            self.input.set(input)
+        self._graph.launch()
+        return self.output
+
+    def destroy(self):
+        self._graph.destroy()

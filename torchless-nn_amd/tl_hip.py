@@ -559,6 +559,16 @@ def arange(start, stop=None, step=1, dtype=None) -> DeviceTensor:
     return array(host, dtype=dtype)
 
 
+def copy_into(dst: DeviceTensor, src: DeviceTensor):
+    """dst[...] = src for contiguous tensors of one shape and dtype (stream-ordered)."""
+    if dst.shape != src.shape or dst.dtype is not src.dtype or not (dst.contiguous and src.contiguous):
+        raise ValueError("copy_into needs contiguous tensors of one shape and dtype")
+    c = ctx()
+    check(c.lib.tl_memcpy_d2d(c.handle, dst.ptr, src.ptr, src.nbytes))
+    _wrote(dst)
+    return dst
+
+
 def concatenate(tensors, axis=0) -> DeviceTensor:
     """xp.concatenate of same-dtype tensors that agree except along `axis` (reference
     demo.ipynb:1533 appends each sampled token with axis=1), as device row copies."""
@@ -1013,8 +1023,15 @@ class capture:  # noqa: N801  (used as a context manager, like torch.cuda.graph)
 
 
 def attention_supported(dtype, head_dim, kv_capacity) -> bool:
-    """Whether tl_attention_fwd takes this configuration (bf16, D in {32, 64, 128, 256},
-    key capacity a multiple of 8)."""
+    """Whether tl_attention_fwd takes this configuration (bf16 with D in {32, 64, 128, 256}
+    or fp32 with D in {32, 64, 128}; key capacity a multiple of 8)."""
+    dt = as_dtype(dtype)
+    return kv_capacity % 8 == 0 and ((dt is bfloat16 and head_dim in (32, 64, 128, 256)) or
+                                     (dt is float32 and head_dim in (32, 64, 128)))
+
+
+def attention_decode_dev_supported(dtype, head_dim, kv_capacity) -> bool:
+    """Whether tl_attention_decode_dev takes this configuration (bf16 only)."""
     return (as_dtype(dtype) is bfloat16 and head_dim in (32, 64, 128, 256)
             and kv_capacity % 8 == 0)
 
