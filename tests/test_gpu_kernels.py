@@ -876,6 +876,36 @@ def test_attention_wide_long_sequences(xp, D, case):
     assert ref.max_rel(got, want) <= 2e-2, case
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("case", [
+    # B, Hq, Hkv, Tq, Tk, Lk, causal, offset: at most 128 queries and keys
+    (3, 2, 2, 17, 17, 24, True, 0),
+    (2, 3, 3, 32, 33, 40, False, 0),
+    (2, 2, 2, 65, 65, 72, False, 0),        # ViT-S/4: 64 patches + CLS
+    (1, 4, 2, 64, 96, 96, True, 32),        # grouped heads, queries at an offset
+    (1, 2, 2, 127, 127, 128, True, 0),
+    (2, 2, 2, 128, 128, 128, False, 0),
+])
+def test_attention_short_sequences(xp, D, case):
+    """The short-sequence kernel (one workgroup per head, one-pass softmax) at the edges of
+    its 32-key halves and 16-row waves, with NaN in the capacity padding."""
+    B, Hq, Hkv, Tq, Tk, Lk, causal, offset = case
+    rng = np.random.default_rng(Tq * 7 + Tk + D)
+    q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, Hkv, Lk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
+    k[:, :, Tk:] = np.nan
+    vt[:, :, :, Tk:] = np.nan
+    out = xp.empty((B, Tq, Hq * D), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=divisor, causal=causal, offset=offset, seq_k=Tk)
+    got = out.get()
+    assert np.all(np.isfinite(got)), case
+    want = attention_ref(q, k[:, :, :Tk], vt[:, :, :, :Tk], Hq, Hkv, divisor, causal, offset)
+    assert ref.max_rel(got, want) <= 2e-2, case
+
+
 @pytest.mark.parametrize("case", [
     # B, Hq, Hkv, Tq, Tk, Lk, D, causal, offset
     (4, 8, 1, 1, 2049, 2056, 256, True, 2048),

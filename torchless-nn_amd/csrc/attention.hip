@@ -812,6 +812,142 @@ int attention_scratch_setup(tl_ctx* ctx) {
   return TL_OK;
 }
 
+// Short sequences (at most 128 queries and 128 keys, e.g. the ViT-S/4 encoder's 65): one
+// workgroup per (batch, head) with one wave per 16 query rows, all keys and values of the
+// head staged in LDS once, and the softmax taken over the whole row at once (no running
+// maximum, no rescaling). Keys are covered in NKH 32-key halves, so 65 keys cost 96 rather
+// than the two 64-key chunks (128 keys) and 128 query rows of the long-sequence kernels.
+// Lane layouts, the S^T = K Q^T and O^T = V^T P^T products and the key order are
+// attention_fwd_kernel's.
+template <int D, int NKH>
+__global__ __launch_bounds__(512) void attention_fwd_short_kernel(AttnParams p) {
+  constexpr int NK = 32 * NKH, NKT = 2 * NKH;
+  constexpr int KCH = D / 8;
+  constexpr int KSW = KCH >= 8 ? 7 : KCH - 1;
+  constexpr int DT = D / 16, KS = D / 32;
+  constexpr int VCH = 16;  // 16-byte chunks per staged V^T row (128 keys)
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[NK * D];
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[D * VCH * 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nt = blockDim.x;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hq, h = bh - b * p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+  const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
+  const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
+  const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
+
+  // stage K [NK, D] and V^T [D, NK] (keys past Tk as zeros: 0 * NaN would not be 0)
+  for (int idx = tid; idx < NK * KCH; idx += nt) {
+    const int r = idx / KCH, c = idx - r * KCH;
+    const uint4 v = r < p.Tk ? *reinterpret_cast<const uint4*>(kh + (int64_t)r * D + c * 8)
+                             : make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(&Ks[r * D + ((c ^ (r & KSW)) << 3)]) = v;
+  }
+  for (int idx = tid; idx < D * (NK / 8); idx += nt) {
+    const int r = idx / (NK / 8), c = idx - r * (NK / 8);
+    const int kv = c * 8;
+    uint4 v = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Lk + kv)
+                        : make_uint4(0, 0, 0, 0);
+    if (kv < p.Tk && kv + 8 > p.Tk) v = keep_first(v, p.Tk - kv);
+    *reinterpret_cast<uint4*>(&Vs[r * (VCH * 8) + ((c ^ (r & 15)) << 3)]) = v;
+  }
+  const int q0 = wave * 16;
+  bf16x8 qf[KS];
+  {
+    const int qi = min(q0 + fr, p.Tq - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[ks] = *reinterpret_cast<const bf16x8*>(qh + (int64_t)qi * D + 32 * ks + 8 * fg);
+  }
+  __syncthreads();
+
+  f32x4 s[NKT];
+#pragma unroll
+  for (int j = 0; j < NKT; ++j) {
+    s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int r = j * 16 + fr;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int c = ks * 4 + fg;
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[r * D + ((c ^ (r & KSW)) << 3)]);
+      s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
+    }
+  }
+  const int qpos = q0 + fr;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NKT; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int kv = j * 16 + 4 * fg + v;
+      const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
+      s[j][v] = ok ? s[j][v] * p.scale_log2 : -INFINITY;
+      mx = fmaxf(mx, s[j][v]);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_ref = mx == -INFINITY ? 0.f : mx;
+  float l = 0.f;
+#pragma unroll
+  for (int j = 0; j < NKT; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float e = __builtin_amdgcn_exp2f(s[j][v] - m_ref);
+      s[j][v] = e;
+      l += e;
+    }
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+
+  f32x4 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c2 = 0; c2 < NKH; ++c2) {
+    bf16x8 pf;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      pf[v] = (__bf16)s[2 * c2][v];
+      pf[4 + v] = (__bf16)s[2 * c2 + 1][v];
+    }
+    const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
+    const int ca = ka >> 3, cb = kb >> 3;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const int r = t * 16 + fr;
+      const bf16_t* row = &Vs[r * (VCH * 8)];
+      const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 15)) << 3) + (ka & 7));
+      const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 15)) << 3) + (kb & 7));
+      const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
+    }
+  }
+  if (qpos < p.Tq) {
+    const float inv = 1.0f / l;
+    bf16_t* orow = p.out + ((int64_t)b * p.Tq + qpos) * p.ld_out + (int64_t)h * D;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      uint2 w;
+      w.x = (uint32_t)f2bf(o[t][0] * inv) | ((uint32_t)f2bf(o[t][1] * inv) << 16);
+      w.y = (uint32_t)f2bf(o[t][2] * inv) | ((uint32_t)f2bf(o[t][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(orow + t * 16 + 4 * fg) = w;
+    }
+  }
+}
+
+template <int D>
+static void launch_short(int nkh, dim3 grid, int threads, hipStream_t st, const AttnParams& p) {
+  switch (nkh) {
+    case 1: attention_fwd_short_kernel<D, 1><<<grid, threads, 0, st>>>(p); break;
+    case 2: attention_fwd_short_kernel<D, 2><<<grid, threads, 0, st>>>(p); break;
+    case 3: attention_fwd_short_kernel<D, 3><<<grid, threads, 0, st>>>(p); break;
+    default: attention_fwd_short_kernel<D, 4><<<grid, threads, 0, st>>>(p); break;
+  }
+}
+
 // fp32 attention (the reference's FLOAT_TYPE, backend.py:24; layers.py:286-304) on the
 // fp32 matrix cores, v_mfma_f32_16x16x4f32: fp32 products and sums, so the scores, the
 // softmax and P.V keep full fp32 precision. The structure is attention_fwd_kernel's: 4
@@ -1137,6 +1273,19 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
       default: launch_decode<256>(nw, jt, g1, g2, ctx->stream, p, w); break;
     }
     return ls.finish("attention_decode");
+  }
+  // at most 128 queries and keys at head dim <= 128 (the ViT-S/4 encoder: 65): one workgroup
+  // per (batch, head), the head's keys and values staged once, the softmax in one pass
+  if (seq_q <= 128 && seq_k <= 128 && head_dim <= 128) {
+    const int nkh = (int)((seq_k + 31) / 32);
+    const int threads = (int)((seq_q + 15) / 16) * 64;
+    const dim3 grid((unsigned)(batch * n_heads_q));
+    switch (head_dim) {
+      case 32: launch_short<32>(nkh, grid, threads, ctx->stream, p); break;
+      case 64: launch_short<64>(nkh, grid, threads, ctx->stream, p); break;
+      default: launch_short<128>(nkh, grid, threads, ctx->stream, p); break;
+    }
+    return ls.finish("attention_fwd_short");
   }
   // sequences longer than one 64-row block at head dim 32 / 64: the wide kernel (128-row
   // blocks, 32 rows per wave). On an MI355X: GPT-2-small attention (T 1024) 0.475 -> 0.412 ms
