@@ -73,6 +73,32 @@ __device__ __forceinline__ void rope8(bf16x8& a, bf16x8& b, const float* c, cons
   }
 }
 
+// V^T rows of a 64-key chunk in LDS (the long-sequence kernels): the P.V operand of lane
+// group fg in 32-key half c2 is keys 32 c2 + 4 fg .. +3 and 32 c2 + 16 + 4 fg .. +3, so
+// within each half the 4-key groups are stored in the order 0, 4, 1, 5, 2, 6, 3, 7 and a
+// lane's 8 keys are one 16-byte piece, read straight into the MFMA operand. 16-byte pieces
+// are XOR-swizzled by row (r & 7) against bank conflicts. Offsets in bf16 elements.
+__device__ __forceinline__ int vperm_piece(int c2, int fg, int r) {
+  return (((c2 * 4 + fg) ^ (r & 7)) << 3);
+}
+// the 8-byte slot of 4-key group g4 (keys 4 g4 .. 4 g4 + 3 of the chunk) in row r
+__device__ __forceinline__ int vperm_slot(int g4, int r) {
+  const int c2 = g4 >> 3, lg = g4 & 7;
+  const int slot = lg < 4 ? 2 * lg : 2 * (lg - 4) + 1;  // 8-byte slot within the half
+  return vperm_piece(c2, slot >> 1, r) + ((slot & 1) << 2);
+}
+
+// The same order for V^T rows of 128 keys (the short-sequence kernel), pieces swizzled by
+// (r & 15).
+__device__ __forceinline__ int vperm_piece16(int c2, int fg, int r) {
+  return (((c2 * 4 + fg) ^ (r & 15)) << 3);
+}
+__device__ __forceinline__ int vperm_slot16(int g4, int r) {
+  const int c2 = g4 >> 3, lg = g4 & 7;
+  const int slot = lg < 4 ? 2 * lg : 2 * (lg - 4) + 1;
+  return vperm_piece16(c2, slot >> 1, r) + ((slot & 1) << 2);
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   constexpr int BKV = 64;
@@ -165,7 +191,9 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   #pragma unroll
       for (int i = 0; i < V_LOADS; ++i) {
         const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-        *reinterpret_cast<uint4*>(&Vs[buf][r * BKV + ((c ^ (r & 7)) << 3)]) = rv[i];
+        bf16_t* row = &Vs[buf][r * BKV];
+        *reinterpret_cast<uint2*>(row + vperm_slot(2 * c, r)) = make_uint2(rv[i].x, rv[i].y);
+        *reinterpret_cast<uint2*>(row + vperm_slot(2 * c + 1, r)) = make_uint2(rv[i].z, rv[i].w);
       }
     };
 
@@ -259,17 +287,12 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
           pf[v] = (__bf16)s[2 * c2][v];
           pf[4 + v] = (__bf16)s[2 * c2 + 1][v];
         }
-        // keys of item i: 32 c2 + 4 fg + i (i < 4) and 32 c2 + 16 + 4 fg + (i - 4)
-        const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
+        // keys of item i: 32 c2 + 4 fg + i (i < 4) and 32 c2 + 16 + 4 fg + (i - 4): one
+        // 16-byte piece of the permuted V^T row (vperm_slot)
   #pragma unroll
         for (int t = 0; t < DT; ++t) {
           const int r = t * 16 + fr;
-          const bf16_t* row = &Vs[cur][r * BKV];
-          const int ca = ka >> 3, cb = kb >> 3;
-          const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 7)) << 3) + (ka & 7));
-          const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 7)) << 3) + (kb & 7));
-          const uint4 vv = make_uint4(va.x, va.y, vb.x, vb.y);
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
+          const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&Vs[cur][r * BKV + vperm_piece(c2, fg, r)]);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
         }
       }
@@ -323,6 +346,7 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
   const int nqb = (p.Tq + RB - 1) / RB;
   const int qb = nqb - 1 - (int)blockIdx.y;
   const int w0 = qb * RB + wave * 32;  // first row of this wave; group g starts at w0 + 16 g
+  const int off = (int)p.offset;        // < 2^30 (host-checked)
   const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
   const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
   const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
@@ -383,7 +407,9 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
       const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
-      *reinterpret_cast<uint4*>(&Vs[buf][r * BKV + ((c ^ (r & 7)) << 3)]) = rv[i];
+      bf16_t* row = &Vs[buf][r * BKV];
+      *reinterpret_cast<uint2*>(row + vperm_slot(2 * c, r)) = make_uint2(rv[i].x, rv[i].y);
+      *reinterpret_cast<uint2*>(row + vperm_slot(2 * c + 1, r)) = make_uint2(rv[i].z, rv[i].w);
     }
   };
 
@@ -428,8 +454,7 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
     for (int g = 0; g < G; ++g) {
       const int q0 = w0 + 16 * g, qpos = q0 + fr;
       float mx = -INFINITY;
-      const bool full = kv0 + BKV <= p.Tk &&
-                        (!p.causal || (int64_t)(kv0 + BKV - 1) <= (int64_t)q0 + p.offset);
+      const bool full = kv0 + BKV <= p.Tk && (!p.causal || kv0 + BKV - 1 <= q0 + off);
       if (full) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -441,7 +466,7 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int kv = kv0 + j * 16 + 4 * fg + v;
-            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
+            const bool ok = kv < p.Tk && (!p.causal || kv <= qpos + off);
             s[g][j][v] = ok ? s[g][j][v] : -INFINITY;
             mx = fmaxf(mx, s[g][j][v]);
           }
@@ -479,18 +504,14 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
         }
     }
 
-    // O^T += V^T P^T over two 32-key halves, both row groups from each V fragment
+    // O^T += V^T P^T over two 32-key halves, both row groups from each V fragment: a lane's
+    // 8 keys are one 16-byte piece of the permuted V^T row (vperm_slot)
 #pragma unroll
     for (int c2 = 0; c2 < 2; ++c2) {
-      const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const int r = t * 16 + fr;
-        const bf16_t* row = &Vs[cur][r * BKV];
-        const int ca = ka >> 3, cb = kb >> 3;
-        const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 7)) << 3) + (ka & 7));
-        const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 7)) << 3) + (kb & 7));
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+        const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&Vs[cur][r * BKV + vperm_piece(c2, fg, r)]);
 #pragma unroll
         for (int g = 0; g < G; ++g)
           o[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[g][c2], o[g][t], 0, 0, 0);
@@ -852,7 +873,9 @@ __global__ __launch_bounds__(512) void attention_fwd_short_kernel(AttnParams p) 
     uint4 v = kv < p.Tk ? *reinterpret_cast<const uint4*>(vh + (int64_t)r * p.Lk + kv)
                         : make_uint4(0, 0, 0, 0);
     if (kv < p.Tk && kv + 8 > p.Tk) v = keep_first(v, p.Tk - kv);
-    *reinterpret_cast<uint4*>(&Vs[r * (VCH * 8) + ((c ^ (r & 15)) << 3)]) = v;
+    bf16_t* row = &Vs[r * (VCH * 8)];
+    *reinterpret_cast<uint2*>(row + vperm_slot16(2 * c, r)) = make_uint2(v.x, v.y);
+    *reinterpret_cast<uint2*>(row + vperm_slot16(2 * c + 1, r)) = make_uint2(v.z, v.w);
   }
   const int q0 = wave * 16;
   bf16x8 qf[KS];
@@ -913,15 +936,10 @@ __global__ __launch_bounds__(512) void attention_fwd_short_kernel(AttnParams p) 
       pf[v] = (__bf16)s[2 * c2][v];
       pf[4 + v] = (__bf16)s[2 * c2 + 1][v];
     }
-    const int ka = 32 * c2 + 4 * fg, kb = ka + 16;
-    const int ca = ka >> 3, cb = kb >> 3;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
       const int r = t * 16 + fr;
-      const bf16_t* row = &Vs[r * (VCH * 8)];
-      const uint2 va = *reinterpret_cast<const uint2*>(row + ((ca ^ (r & 15)) << 3) + (ka & 7));
-      const uint2 vb = *reinterpret_cast<const uint2*>(row + ((cb ^ (r & 15)) << 3) + (kb & 7));
-      const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+      const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&Vs[r * (VCH * 8) + vperm_piece16(c2, fg, r)]);
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
     }
   }
