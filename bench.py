@@ -204,7 +204,7 @@ def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None, model="gpt"):
     return table
 
 
-def gemma_bench(xp, prefill_reps=3, decode_steps=128):
+def gemma_bench(xp, prefill_reps=3, decode_steps=128, graph=True):
     """Gemma-style bf16 decoder (2.5B weights, device-seeded N(0,0.02)):
     prefill B=4 x T=2048 into the KV cache, then `decode_steps` greedy steps at M=4 whose
     ids are fed back on the device. Decode is weight-streaming: every step reads all
@@ -260,19 +260,21 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
         dpos.advance(1)
 
     gstep()  # eager at the device position: everything the capture needs exists after it
-    with xp.capture() as g:
-        gstep()
-    dpos.pos.set(np.array([T], np.int64))
-    xp.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    for t in range(decode_steps):
-        g.launch()
-    e1.record()
-    xp.synchronize()
-    gwall = (time.perf_counter() - t0) / decode_steps * 1e3
-    graph_ms = e0.elapsed_ms(e1) / decode_steps
-    g.destroy()
+    graph_ms = gwall = float("nan")
+    if graph:
+        with xp.capture() as g:
+            gstep()
+        dpos.pos.set(np.array([T], np.int64))
+        xp.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        for t in range(decode_steps):
+            g.launch()
+        e1.record()
+        xp.synchronize()
+        gwall = (time.perf_counter() - t0) / decode_steps * 1e3
+        graph_ms = e0.elapsed_ms(e1) / decode_steps
+        g.destroy()
     # per-family kernel time of the decode steps (HIP events around every launch)
     xp.kprof_reset()
     xp.kprof_enable(list(xp.KFAMILY))
@@ -303,12 +305,14 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128):
         "decode_bytes_per_step": w_bytes + kv_bytes,
         "decode_hbm_gbs": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9, 1),
         "decode_hbm_frac": round((w_bytes + kv_bytes) / (decode_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-        "decode_graph_ms_per_step": round(graph_ms, 4),
-        "decode_graph_wall_ms_per_step": round(gwall, 4),
-        "decode_graph_tokens_per_s": round(B / (graph_ms * 1e-3), 1),
-        "decode_graph_hbm_frac": round((w_bytes + kv_bytes) / (graph_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         "decode_kernel_breakdown": decode_breakdown,
     }
+    if graph:
+        out.update({
+            "decode_graph_ms_per_step": round(graph_ms, 4),
+            "decode_graph_wall_ms_per_step": round(gwall, 4),
+            "decode_graph_tokens_per_s": round(B / (graph_ms * 1e-3), 1),
+            "decode_graph_hbm_frac": round((w_bytes + kv_bytes) / (graph_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
     log(f"gemma config 5: {json.dumps(out)}")
     del model, cache, logits
     return out
@@ -427,6 +431,78 @@ def decode_sweep(xp, reps=50):
         out[name] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
     log(f"decode sweep (skinny cfg {os.environ.get('TL_SKINNY_CFG', '0')}, attention cfg "
         f"{os.environ.get('TL_ATTN_DECODE_CFG', '0')}): {json.dumps(out)}")
+    return out
+
+
+VENDOR_SHAPES = {"qkv": (768, 2304), "out_proj": (768, 768), "ffn1": (768, 3072),
+                 "ffn2": (3072, 768), "lm_head": (768, 50257)}  # (K, N) at M = 8192
+
+
+def vendor_gemm_child(reps=20):
+    """Child process of vendor_gemm_compare: times PyTorch's F.linear (bias, bf16; hipBLASLt
+    on ROCm) at the config-3 shapes and prints {name: microseconds} as JSON. It runs in its
+    own process because PyTorch carries its own HIP runtime, which does not see the GPU in a
+    process where libtl.so has already loaded the system one."""
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "torch sees no GPU"}))
+        return
+    M, out = BATCH * SEQ, {}
+    for name, (K, N) in VENDOR_SHAPES.items():
+        a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16)
+        w = torch.randn(N, K, device="cuda", dtype=torch.bfloat16) * 0.02
+        b = torch.randn(N, device="cuda", dtype=torch.bfloat16) * 0.02
+        for _ in range(3):
+            torch.nn.functional.linear(a, w, b)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            torch.nn.functional.linear(a, w, b)
+        t1.record()
+        torch.cuda.synchronize()
+        out[name] = t0.elapsed_time(t1) / reps * 1e3
+        del a, w, b
+    print(json.dumps(out), flush=True)
+
+
+def vendor_gemm_compare(xp, reps=20):
+    """The config-3 dense products (M = 8192, bias epilogue, bf16) through this library's
+    tl_gemm and through the vendor library behind PyTorch's F.linear (hipBLASLt on ROCm),
+    each timed with events over `reps` back-to-back calls on hot operands: a reference point
+    for what the matrix cores reach at these shapes, not part of the product."""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--vendor-child"],
+                           capture_output=True, text=True, timeout=300)
+        vend = json.loads(r.stdout.strip().splitlines()[-1])
+    except Exception as e:  # noqa: BLE001  (a measurement leg only)
+        log(f"vendor GEMM comparison skipped: {type(e).__name__}: {e}")
+        return None
+    if "error" in vend:
+        log(f"vendor GEMM comparison skipped: {vend['error']}")
+        return None
+    M, out = BATCH * SEQ, {}
+    for name, (K, N) in VENDOR_SHAPES.items():
+        a = xp.random_normal((M, K), 1, 0, std=1.0, dtype="bf16")
+        bt = xp.random_normal((N, K), 2, 0, std=0.02, dtype="bf16")
+        bias = xp.random_normal((N,), 3, 0, std=0.02, dtype="bf16")
+        ldc = (N + 7) // 8 * 8
+        c = xp.empty((M, N), "bf16", pitch=ldc)
+        fn = lambda: xp.gemm(a, bt, M=M, N=N, K=K, lda=K, ldb=K, b_layout=xp.TL_B_NK, C=c,
+                             ldc=ldc, bias=bias)
+        fn()
+        e0, e1 = xp.Event(), xp.Event()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        ours = e0.elapsed_ms(e1) / reps * 1e3
+        del a, bt, bias, c
+        fl = 2.0 * M * N * K
+        out[name] = {"tl_us": round(ours, 1), "vendor_us": round(vend[name], 1),
+                     "tl_tflops": round(fl / (ours * 1e-6) / 1e12, 1),
+                     "vendor_tflops": round(fl / (vend[name] * 1e-6) / 1e12, 1)}
+    log(f"vendor GEMM comparison: {json.dumps(out)}")
     return out
 
 
@@ -589,6 +665,11 @@ def main():
     ap.add_argument("--no-gemma", action="store_true", help="skip the config-5 decoder section")
     ap.add_argument("--no-vit", action="store_true", help="skip the config-4 ViT section")
     ap.add_argument("--no-gpt2-fp32", action="store_true", help="skip the fp32 GPT-2 section")
+    ap.add_argument("--no-char", action="store_true", help="skip the config-1 section")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the config-5 decode replayed from a HIP graph (profiling runs)")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the hipBLASLt (PyTorch F.linear) GEMM comparison")
     ap.add_argument("--sweep-gemm", action="store_true",
                     help="only time the dense GEMM shapes under every tile shape")
     ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
@@ -600,7 +681,11 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
                          "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--vendor-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.vendor_child:
+        vendor_gemm_child()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
               f"(--gpus {args.gpus} requested)", file=sys.stderr)
@@ -684,12 +769,13 @@ def main():
                 "traffic": traffic, "traffic_unit": "bytes per launch (HBM, measured)"}
 
     rows = {} if args.no_row_kernels else row_kernel_bench(xp)
-    gem = None if args.no_gemma else gemma_bench(xp)
+    gem = None if args.no_gemma else gemma_bench(xp, graph=not args.no_graph)
     vit_line = None if args.no_vit else vit_bench(xp)
-    char = char_gpt_bench(xp)
+    char = None if args.no_char else char_gpt_bench(xp)
     f32 = None if args.no_gpt2_fp32 else gpt2_fp32_bench(xp)
+    vendor = None if args.no_vendor else vendor_gemm_compare(xp)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
-    if not args.no_cpu_baseline:
+    if char is not None and not args.no_cpu_baseline:
         char["cpu_baseline"] = cpu_baseline_char_gpt()
         log(f"char gpt config 1 cpu baseline: {char['cpu_baseline']}")
     if cpu:
@@ -714,6 +800,7 @@ def main():
         "vit_classifier": vit_line,
         "char_gpt": char,
         "gpt2_fp32": f32,
+        "vendor_gemm": vendor,
     }
     print(json.dumps(line), flush=True)
 
