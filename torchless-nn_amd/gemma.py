@@ -44,11 +44,19 @@ class GemmaDecoder:
 
     def forward(self, ids, cache=None, pos0=0):
         x = self.front.forward(ids)
+        c = self.cfg
+        T, start = x.shape[1], pos0
+        if (cache is not None and (c["heads"] // c["kv_heads"]) * T <= 16 and
+                pos0 + T <= min(cache.capacity, c["ctx"]) and
+                xp.attention_decode_dev_supported(self.dtype, c["head_dim"], cache.capacity)):
+            # a decode step: one device copy of the position (and one RoPE table) serves
+            # every block, and the blocks run the kernels a replayed step runs
+            pos0 = DevicePosition.at(pos0, T, c["head_dim"], c.get("rope_base", 10000.0))
         for i, blk in enumerate(self.blocks):
             x = blk.forward(x, cache, i, pos0)
         logits = self.back.forward(self.final_norm.forward(x))
         if cache is not None:
-            cache.length = pos0 + x.shape[1]
+            cache.length = start + T
         return logits
 
     @staticmethod
