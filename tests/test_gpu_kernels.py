@@ -917,12 +917,15 @@ def test_attention_short_sequences(xp, D, case):
 ])
 def test_attention_decode_split_kv(xp, case):
     """Few query rows per kv head (decode): split-KV kernel + combine, keys read from a cache
-    of capacity Lk whose first Tk positions are valid (the rest hold other finite values)."""
+    of capacity Lk whose first Tk positions are valid; the rest hold NaN, which the kernel
+    reads (its loads are unconditional) and must mask out of the scores and the values."""
     B, Hq, Hkv, Tq, Tk, Lk, D, causal, offset = case
     rng = np.random.default_rng(Tk + D)
     q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
     k = ref.round_bf16(rng.standard_normal((B, Hkv, Lk, D)).astype(F32))
     vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
+    k[:, :, Tk:] = np.nan
+    vt[:, :, :, Tk:] = np.nan
     out = xp.empty((B, Tq, Hq * D), "bf16")
     divisor = float(np.float32(np.sqrt(D)))
     xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,

@@ -22,8 +22,8 @@
 
 namespace tl {
 
-// Keep the first n (1..7) bf16 values of an 8-value chunk (or 1..3 of a 4-value run) and
-// zero the rest: value rows past the last valid key.
+// Keep the first n (1..7) bf16 values of an 8-value chunk and zero the rest: value rows
+// past the last valid key.
 __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -32,10 +32,6 @@ __device__ __forceinline__ uint4 keep_first(uint4 v, int n) {
     else if (2 * i + 1 >= n) w[i] &= 0xffffu;
   }
   return make_uint4(w[0], w[1], w[2], w[3]);
-}
-__device__ __forceinline__ uint2 keep_first4(uint2 v, int n) {
-  const uint4 t = keep_first(make_uint4(v.x, v.y, 0, 0), n);
-  return make_uint2(t.x, t.y);
 }
 
 struct AttnParams {
@@ -56,22 +52,6 @@ struct AttnParams {
   // cache keys (positions offset ..) itself and writes the rotated keys back to the cache.
   const float* rope;
 };
-
-// Rotate-half RoPE of 8 consecutive elements a (index d < D/2) and their partners b
-// (index d + D/2) with cos c and sin s, in fp32 and rounded to bf16 as a separate RoPE pass
-// would store them.
-__device__ __forceinline__ void rope8(bf16x8& a, bf16x8& b, const float* c, const float* s) {
-  const float4 c0 = *reinterpret_cast<const float4*>(c), c1 = *reinterpret_cast<const float4*>(c + 4);
-  const float4 s0 = *reinterpret_cast<const float4*>(s), s1 = *reinterpret_cast<const float4*>(s + 4);
-  const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-  const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float fa = (float)a[e], fb = (float)b[e];
-    a[e] = (__bf16)(fa * cv[e] - fb * sv[e]);
-    b[e] = (__bf16)(fb * cv[e] + fa * sv[e]);
-  }
-}
 
 // V^T rows of a 64-key chunk in LDS (the long-sequence kernels): the P.V operand of lane
 // group fg in 32-key half c2 is keys 32 c2 + 4 fg .. +3 and 32 c2 + 16 + 4 fg .. +3, so
@@ -541,6 +521,28 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
   }
 }
 
+// Rotate-half RoPE of 8 consecutive elements a (index d < D/2) and their partners b
+// (index d + D/2) with the table values in registers (c[0], c[1]: the 8 cosines; c[2], c[3]:
+// the 8 sines), in fp32 and rounded to bf16 as a separate RoPE pass would store them.
+__device__ __forceinline__ void rope8v(bf16x8& a, bf16x8& b, const float4 (&c)[4]) {
+  const float cv[8] = {c[0].x, c[0].y, c[0].z, c[0].w, c[1].x, c[1].y, c[1].z, c[1].w};
+  const float sv[8] = {c[2].x, c[2].y, c[2].z, c[2].w, c[3].x, c[3].y, c[3].z, c[3].w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float fa = (float)a[e], fb = (float)b[e];
+    a[e] = (__bf16)(fa * cv[e] - fb * sv[e]);
+    b[e] = (__bf16)(fb * cv[e] + fa * sv[e]);
+  }
+}
+
+// Keep the first n of a run of 4 bf16 values (all of them for n >= 4, none for n <= 0),
+// with selects rather than branches.
+__device__ __forceinline__ uint2 keep_below(uint2 v, int n) {
+  const uint32_t lo = n >= 2 ? 0xffffffffu : (n == 1 ? 0x0000ffffu : 0u);
+  const uint32_t hi = n >= 4 ? 0xffffffffu : (n == 3 ? 0x0000ffffu : 0u);
+  return make_uint2(v.x & lo, v.y & hi);
+}
+
 // ---------------------------------------------------------------------------------------
 // Decode (split-KV) attention for a few query rows per kv head: the query rows that share a
 // kv head (Hq / Hkv heads x Tq positions, at most 16) form one MFMA column block, so every
@@ -580,56 +582,95 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
   const int64_t qpos = (int64_t)t + p.offset;
   const bf16x8 zero = {};
 
+  // Every load below reads a clamped, in-bounds address unconditionally, and what lies past
+  // the valid rows or keys is masked or zeroed afterwards. (With a condition on each load the
+  // compiler gives each one its own exec-masked branch and waits for it inside, so the loads
+  // completed one after another: 14.8 us per config-5 layer for 8.5 MB.)
   bf16x8 qf[KS];
   {
     const bf16_t* qrow = p.q + ((int64_t)(b * p.Hq + hk * g + jh) * p.Tq + t) * D + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[ks] = rowok ? *reinterpret_cast<const bf16x8*>(qrow + 32 * ks) : zero;
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *reinterpret_cast<const bf16x8*>(qrow + 32 * ks);
   }
   // fused RoPE (D >= 64): element d = 32 ks + 8 grp + e of qf[ks] has its partner d + D/2 in
-  // qf[ks + KS/2] of the same lane
+  // qf[ks + KS/2] of the same lane; the table row is loaded here, applied after the K and V
+  // loads are issued
   constexpr int KH = KS / 2;
+  float4 qcs[KH > 0 ? KH : 1][4];
   if constexpr (KH > 0) {
-    if (p.rope && rowok) {
+    if (p.rope) {
       const float* cs = p.rope + (int64_t)t * (D / 2) + 8 * grp;
       const float* sn = cs + (int64_t)p.Tq * (D / 2);
 #pragma unroll
-      for (int ks = 0; ks < KH; ++ks) rope8(qf[ks], qf[ks + KH], cs + 32 * ks, sn + 32 * ks);
+      for (int ks = 0; ks < KH; ++ks) {
+        qcs[ks][0] = *reinterpret_cast<const float4*>(cs + 32 * ks);
+        qcs[ks][1] = *reinterpret_cast<const float4*>(cs + 32 * ks + 4);
+        qcs[ks][2] = *reinterpret_cast<const float4*>(sn + 32 * ks);
+        qcs[ks][3] = *reinterpret_cast<const float4*>(sn + 32 * ks + 4);
+      }
     }
   }
   const bf16_t* kh = p.k + (int64_t)bh * p.Lk * D;
   const bf16_t* vh = p.vt + (int64_t)bh * D * p.Lk;
   const int kc0 = (blockIdx.x * NW + wave) * KPW;
+  // a wave whose keys all lie past the valid ones (a device position short of the capacity)
+  // loads nothing: its scores are masked and its values zero
+  const bool live = kc0 < p.Tk;
 
   // All of this wave's K and V^T fragments are requested up front (the V^T reads do not
-  // depend on the softmax), so the wave waits for one memory round trip, not two.
+  // depend on the softmax), so the wave waits for one memory round trip, not two. Keys past
+  // Tk are read from the cache's own rows (clamped to the capacity) and masked in the scores.
   bf16x8 kf[J][KS];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int key = kc0 + 16 * j + col;
-    const bool kin = key < p.Tk;
-    const bf16_t* krow = kh + (int64_t)(kin ? key : 0) * D + 8 * grp;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kf[j][ks] = kin ? *reinterpret_cast<const bf16x8*>(krow + 32 * ks) : zero;
-  }
   // V^T rows in the key order of the P.V B operand: keys 32 hp + 4 grp + 0..3 and
-  // 32 hp + 16 + 4 grp + 0..3 (values past Tk zeroed, since 0 * NaN would not be 0)
+  // 32 hp + 16 + 4 grp + 0..3 (values past Tk zeroed, since 0 * NaN would not be 0; the
+  // capacity is a multiple of 8, so a 4-key run that starts inside it ends inside it)
   uint2 vfa[J / 2][DT], vfb[J / 2][DT];
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int key = min(kc0 + 16 * j + col, p.Lk - 1);
+      const bf16_t* krow = kh + (int64_t)key * D + 8 * grp;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[j][ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+    }
+#pragma unroll
+    for (int hp = 0; hp < J / 2; ++hp) {
+      const int ka = min(kc0 + 32 * hp + 4 * grp, p.Lk - 4), kb = min(kc0 + 32 * hp + 16 + 4 * grp, p.Lk - 4);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
+        vfa[hp][dt] = *reinterpret_cast<const uint2*>(vrow + ka);
+        vfb[hp][dt] = *reinterpret_cast<const uint2*>(vrow + kb);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[j][ks] = zero;
+#pragma unroll
+    for (int hp = 0; hp < J / 2; ++hp)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) vfa[hp][dt] = vfb[hp][dt] = make_uint2(0, 0);
+  }
+  if (!rowok) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = zero;
+  }
+  if constexpr (KH > 0) {
+    if (p.rope) {
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) rope8v(qf[ks], qf[ks + KH], qcs[ks]);
+    }
+  }
+  // zero the values of keys >= Tk (unrotated key index: keys 32 hp + 4 grp + i)
 #pragma unroll
   for (int hp = 0; hp < J / 2; ++hp) {
-    const int ka = kc0 + 32 * hp + 4 * grp, kb = ka + 16;
-    const bool ina = ka < p.Tk, inb = kb < p.Tk;
+    const int na = p.Tk - (kc0 + 32 * hp + 4 * grp), nb = na - 16;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
-      uint2 va = ina ? *reinterpret_cast<const uint2*>(vrow + ka) : make_uint2(0, 0);
-      uint2 vb = inb ? *reinterpret_cast<const uint2*>(vrow + kb) : make_uint2(0, 0);
-      if (ina && ka + 4 > p.Tk) va = keep_first4(va, p.Tk - ka);
-      if (inb && kb + 4 > p.Tk) vb = keep_first4(vb, p.Tk - kb);
-      vfa[hp][dt] = va;
-      vfb[hp][dt] = vb;
+      vfa[hp][dt] = keep_below(vfa[hp][dt], na);
+      vfb[hp][dt] = keep_below(vfb[hp][dt], nb);
     }
   }
   // fused RoPE of this call's new keys (positions offset .. offset + Tq - 1): the one lane
@@ -644,9 +685,19 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
           const float* cs = p.rope + tn * (D / 2) + 8 * grp;
           const float* sn = cs + (int64_t)p.Tq * (D / 2);
           bf16_t* krow = const_cast<bf16_t*>(kh) + (int64_t)key * D + 8 * grp;
+          // the whole table row first, then the rotations and stores (a load after a store
+          // to the cache would wait for it)
+          float4 kcs[KH][4];
 #pragma unroll
           for (int ks = 0; ks < KH; ++ks) {
-            rope8(kf[j][ks], kf[j][ks + KH], cs + 32 * ks, sn + 32 * ks);
+            kcs[ks][0] = *reinterpret_cast<const float4*>(cs + 32 * ks);
+            kcs[ks][1] = *reinterpret_cast<const float4*>(cs + 32 * ks + 4);
+            kcs[ks][2] = *reinterpret_cast<const float4*>(sn + 32 * ks);
+            kcs[ks][3] = *reinterpret_cast<const float4*>(sn + 32 * ks + 4);
+          }
+#pragma unroll
+          for (int ks = 0; ks < KH; ++ks) {
+            rope8v(kf[j][ks], kf[j][ks + KH], kcs[ks]);
             *reinterpret_cast<bf16x8*>(krow + 32 * ks) = kf[j][ks];
             *reinterpret_cast<bf16x8*>(krow + 32 * (ks + KH)) = kf[j][ks + KH];
           }
@@ -746,13 +797,15 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
   }
 }
 
-// One workgroup per (query row, batch x kv head). The partials' maxima and sums are read
-// in parallel into LDS and turned into weights exp2(m_k - max); thread d then sums the
-// partials of head-dim d with independent (unrolled) loads.
+// One workgroup per (query row, batch x kv head). Thread d requests its first PF partial
+// outputs of head-dim d and the (max, sum) pair of partial d before anything else (none of
+// these loads depends on another), so the kernel waits for one memory round trip; the
+// maxima give the weights exp2(m_k - max), and the partials are summed with those weights.
 template <int D>
 __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(AttnParams p, DecodeWs w) {
   constexpr int NT = D < 64 ? 64 : D;  // whole waves, so the shuffles see only live lanes
   constexpr int NWV = NT / 64;
+  constexpr int PF = 64;                // partials prefetched into registers
   __shared__ float wk[1024];
   __shared__ float red[NWV];
   __shared__ float stats[2];
@@ -760,13 +813,15 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(Attn
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int g = p.Hq / p.Hkv;
   const int jh = r / p.Tq, t = r - jh * p.Tq;
-  const int64_t base = (int64_t)bh * w.nblk;
-  float m = -INFINITY;
-  for (int k = d; k < w.nblk; k += NT) {
-    const float mk = w.ml[((base + k) * 16 + r) * 2];
-    wk[k] = mk;
-    m = fmaxf(m, mk);
-  }
+  const int nblk = w.nblk;
+  const int64_t base = (int64_t)bh * nblk;
+  const float* src = w.o + (base * 16 + r) * D + min(d, D - 1);
+  float pre[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) pre[u] = src[(int64_t)min(u, nblk - 1) * 16 * D];
+  const float2 ml0 = *reinterpret_cast<const float2*>(w.ml + ((base + min(d, nblk - 1)) * 16 + r) * 2);
+  float m = d < nblk ? ml0.x : -INFINITY;
+  for (int k = d + NT; k < nblk; k += NT) m = fmaxf(m, w.ml[((base + k) * 16 + r) * 2]);
   m = wave_max(m);
   if ((d & 63) == 0) red[d >> 6] = m;
   __syncthreads();
@@ -778,8 +833,14 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(Attn
   __syncthreads();
   m = stats[0];
   float l = 0.f;
-  for (int k = d; k < w.nblk; k += NT) {
-    const float f = wk[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(wk[k] - m);
+  if (d < nblk) {
+    const float f = ml0.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml0.x - m);
+    wk[d] = f;
+    l = ml0.y * f;
+  }
+  for (int k = d + NT; k < nblk; k += NT) {
+    const float mk = w.ml[((base + k) * 16 + r) * 2];
+    const float f = mk == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mk - m);
     wk[k] = f;
     l += w.ml[((base + k) * 16 + r) * 2 + 1] * f;
   }
@@ -793,16 +854,18 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(Attn
   }
   __syncthreads();
   if (d >= D) return;
-  const float* src = w.o + (base * 16 + r) * D + d;
-  // partial k always accumulates into acc[k % 4], so the sum does not depend on how many
-  // (empty, weight-0) partials follow the last live one
+  // partial k always accumulates into acc[k % 4], in increasing k, so the sum does not
+  // depend on how many (empty, weight-0) partials follow the last live one
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  int k = 0;
-  for (; k + 4 <= w.nblk; k += 4) {
+#pragma unroll
+  for (int u = 0; u < PF; ++u)
+    if (u < nblk) acc[u & 3] += pre[u] * wk[u];
+  int k = PF;
+  for (; k + 4 <= nblk; k += 4) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] += src[(int64_t)(k + u) * 16 * D] * wk[k + u];
   }
-  for (; k < w.nblk; ++k) acc[k & 3] += src[(int64_t)k * 16 * D] * wk[k];
+  for (; k < nblk; ++k) acc[k & 3] += src[(int64_t)k * 16 * D] * wk[k];
   const float o = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   const int h = hk * g + jh;
   p.out[((int64_t)b * p.Tq + t) * p.ld_out + (int64_t)h * D + d] = f2bf(o / stats[1]);
