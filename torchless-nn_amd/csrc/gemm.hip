@@ -110,6 +110,15 @@ __device__ __forceinline__ void gload_f4(const float* p, float (&v)[4]) {
   v[2] = __uint_as_float(t.z); v[3] = __uint_as_float(t.w);
 }
 
+// Bias value of column n, 0 past N. The load itself is unconditional (column clamped to
+// N - 1) and the value is selected afterwards: a load under a per-lane condition compiles to
+// its own exec-masked branch that waits for it, so a fragment's loads would complete one
+// after another instead of together.
+__device__ __forceinline__ float bias_at(const GemmParams& e, int64_t n) {
+  const float b = bf2f(gload((const bf16_t*)e.bias + (n < e.N ? n : e.N - 1)));
+  return n < e.N ? b : 0.f;
+}
+
 // Applies the epilogue to 4 consecutive columns n0..n0+3 of row m and stores them.
 template <typename TI, typename TO>
 __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64_t zi, int64_t m,
@@ -120,10 +129,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = v[e] / p.divisor;
   }
-  if (p.bias) {
+  if (p.bias) {  // unconditional loads (clamped to column N - 1), selected afterwards
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (e < cnt) v[e] = v[e] + gload_elem((const TI*)p.bias + n0 + e);
+    for (int e = 0; e < 4; ++e) {
+      const float b = gload_elem((const TI*)p.bias + (e < cnt ? n0 + e : p.N - 1));
+      if (e < cnt) v[e] = v[e] + b;
+    }
   }
   if (p.geglu) {  // columns (gate f, up f, gate f+1, up f+1), n0 even
     TO* c = (TO*)p.C + zo * p.sc_o + zi * p.sc_i + m * p.ldc + n0 / 2;
@@ -136,10 +147,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int64_t zo, int64
     for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], p.act);
   }
   if (p.res) {
-    const TO* r = (const TO*)p.res + zo * p.sr_o + zi * p.sr_i + m * p.ldr + n0;
+    const TO* r = (const TO*)p.res + zo * p.sr_o + zi * p.sr_i + m * p.ldr;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (e < cnt) v[e] = v[e] + gload_elem(r + e);
+    for (int e = 0; e < 4; ++e) {
+      const float x = gload_elem(r + (e < cnt ? n0 + e : p.N - 1));
+      if (e < cnt) v[e] = v[e] + x;
+    }
   }
   if (p.qkv) {
     // Dh % 4 == 0 (checked on the host), so the 4 columns share one head of one part.
@@ -219,9 +232,18 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
   for (int j = 0; j < TN; ++j) {
     const int64_t n = nb + 16 * j;
     cnt[j] = n >= e.N ? 0 : (e.N - n >= 4 ? 4 : (int)(e.N - n));
+  }
+  // one branch around all the bias loads (a branch per load would wait inside each)
+  if (e.bias) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      bias[j][q] = (e.bias && q < cnt[j]) ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bias[j][q] = bias_at(e, nb + 16 * j + q);
+  } else {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bias[j][q] = 0.f;
   }
   auto finish = [&](float (&v)[4], int j) {
 #pragma unroll
@@ -310,6 +332,24 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t m = mb + 16 * i;
+    // the row's vector residual pieces, requested together before any is used (reads of
+    // rows past M or of fragments that end past N are clamped in bounds and not used)
+    float rq[TN][4];
+    if (rz && e.vec_res) {
+      const TO* r0 = rz + (m < e.M ? m : e.M - 1) * e.ldr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t c = nb + 16 * j;
+        const TO* src = r0 + (c + 4 <= e.N ? c : 0);
+        if constexpr (sizeof(TO) == 2) {
+          const uint2 u = gload8(src);
+          rq[j][0] = __uint_as_float(u.x << 16); rq[j][1] = __uint_as_float(u.x & 0xffff0000u);
+          rq[j][2] = __uint_as_float(u.y << 16); rq[j][3] = __uint_as_float(u.y & 0xffff0000u);
+        } else {
+          gload_f4(reinterpret_cast<const float*>(src), rq[j]);
+        }
+      }
+    }
     if (m >= e.M) continue;
     TO* crow = cz + m * e.ldc + nb;
     const TO* rrow = rz ? rz + m * e.ldr + nb : nullptr;
@@ -320,16 +360,8 @@ __device__ __forceinline__ void mfma_epilogue(const GemmParams& e, int64_t zo, i
       finish(v, j);
       if (rrow) {
         if (cnt[j] == 4 && e.vec_res) {
-          float r[4];
-          if (sizeof(TO) == 2) {
-            const uint2 u = gload8(rrow + 16 * j);
-            r[0] = __uint_as_float(u.x << 16); r[1] = __uint_as_float(u.x & 0xffff0000u);
-            r[2] = __uint_as_float(u.y << 16); r[3] = __uint_as_float(u.y & 0xffff0000u);
-          } else {
-            gload_f4(reinterpret_cast<const float*>(rrow + 16 * j), r);
-          }
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = v[q] + r[q];
+          for (int q = 0; q < 4; ++q) v[q] = v[q] + rq[j][q];
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
@@ -390,8 +422,7 @@ __device__ __forceinline__ void load_epi_bias(const GemmParams& e, int64_t nw,
     for (int j = 0; j < TN; ++j) {
       const int64_t n = nw + 16 * j + 4 * fc;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bias[j][q] = n + q < e.N ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
+      for (int q = 0; q < 4; ++q) bias[j][q] = bias_at(e, n + q);
     }
   }
 }
@@ -409,13 +440,26 @@ __device__ __forceinline__ void stage_rows(const GemmParams& e, const bf16_t* rz
   constexpr bool BIAS = EpiTraits<KIND>::BIAS, RES = EpiTraits<KIND>::RES;
   constexpr int U = WN / 8;
   const int lane = threadIdx.x & 63, fr = lane & 15, fc = lane >> 4;
+  // All residual pieces of these rows are requested before any is used (one memory round
+  // trip, not one per fragment). Rows past M and columns past N are computed and staged but
+  // never stored, so their reads are clamped to the last row and to column N - 4 (N % 4 == 0
+  // on this path) and their values do not matter.
+  uint2 rv[RES ? NI : 1][RES ? TN : 1];
+  if constexpr (RES) {
+#pragma unroll
+    for (int ii = 0; ii < NI; ++ii) {
+      const int64_t m = mw + 16 * (I0 + ii) + fr;
+      const bf16_t* rrow = rz + (m < e.M ? m : e.M - 1) * e.ldr;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = nw + 16 * j + 4 * fc;
+        rv[ii][j] = gload8(rrow + (n < e.N ? n : e.N - 4));
+      }
+    }
+  }
 #pragma unroll
   for (int ii = 0; ii < NI; ++ii) {
     const int i = I0 + ii, r = 16 * ii + fr;
-    const int64_t m = mw + 16 * i + fr;
-    // rows past M are computed and staged but never stored; their residual reads stay on
-    // the last row
-    const bf16_t* rrow = RES ? rz + (m < e.M ? m : e.M - 1) * e.ldr + nw + 4 * fc : nullptr;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
@@ -431,8 +475,8 @@ __device__ __forceinline__ void stage_rows(const GemmParams& e, const bf16_t* rz
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = silu_tanh(v[q]);
       }
-      if (RES && nw + 16 * j + 4 * fc < e.N) {  // N % 4 == 0 on this path
-        const uint2 w = gload8(rrow + 16 * j);
+      if constexpr (RES) {
+        const uint2 w = rv[ii][j];
         v[0] = v[0] + __uint_as_float(w.x << 16);
         v[1] = v[1] + __uint_as_float(w.x & 0xffff0000u);
         v[2] = v[2] + __uint_as_float(w.y << 16);
@@ -512,8 +556,7 @@ __device__ __forceinline__ bool staged_qkv_epilogue(const GemmParams& e, int64_t
     for (int j = 0; j < (BIAS ? TN : 1); ++j) {
       const int64_t n = nw + 16 * j + 4 * fc;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bias[j][q] = n + q < e.N ? bf2f(gload((const bf16_t*)e.bias + n + q)) : 0.f;
+      for (int q = 0; q < 4; ++q) bias[j][q] = bias_at(e, n + q);
     }
   }
   const int base = part == 0 ? 0 : (part == 1 ? qw : qw + kw);
