@@ -180,6 +180,14 @@ int tl_memcpy2d_d2d(tl_ctx* ctx, void* dst, size_t dpitch, const void* src, size
                     size_t width_bytes, size_t rows);
 /* Waits for the stream, then reports any latched kernel data error. */
 int tl_sync(tl_ctx* ctx);
+/* Cache warming, no reference counterpart (the reference leaves memory traffic to
+ * CuPy/NumPy). Names a device region (4-byte aligned, up to 4 regions per launch) that the
+ * next tl_layernorm_fwd / tl_rmsnorm_fwd on this context also reads, one word per 128-byte
+ * line, so a weight that the product after the norm reads arrives from the device caches
+ * instead of HBM. Advisory: results do not change, the values read are discarded, and the
+ * list is cleared by that launch. The region must stay allocated until the launch has run
+ * (in a captured graph, until the graph is destroyed). */
+int tl_prefetch_hint(tl_ctx* ctx, const void* ptr, int64_t bytes);
 /* HIP graphs of the context stream, for replaying a whole step (a decode step, a short
  * forward) with one launch instead of one host call per kernel. No reference counterpart
  * (the reference dispatches every op from Python, network.py:36-39).

@@ -82,7 +82,11 @@ def test_cast_rejects_overlapping_operands(xp):
 
 
 # ---- LayerNorm / RMSNorm ------------------------------------------------------------------
-NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (33, 4096), (2, 5000), (4, 8192), (3, 12000)]
+# (64, 768) bf16, (7, 256) bf16 and (9, 384) fp32 rows fill 32 lanes but not 64 (two rows per
+# wave; an odd row count leaves the last wave's second row empty); (13, 1280) bf16 does not fit
+# 32 lanes and falls back to one row per wave
+NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (7, 256), (9, 384), (13, 1280), (33, 4096),
+               (2, 5000), (4, 8192), (3, 12000)]
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
@@ -176,6 +180,35 @@ def test_norms_many_rows(xp, dt, rows, cols):
     assert ref.max_rel(y, rnd(dt, ref.layernorm(x, g, b))) <= TOL[dt], (dt, rows, cols)
     y = xp.rmsnorm(up(xp, x, dt), up(xp, g, dt), F32(1e-6), 1.0).get()
     assert ref.max_rel(y, rnd(dt, ref.rmsnorm(x, g, F32(1e-6), 1.0))) <= TOL[dt], (dt, rows, cols)
+
+
+def test_prefetch_hint_changes_no_result(xp):
+    """tl_prefetch_hint: the next norm launch also reads up to four named regions (whole
+    tensors, a pitched view, a 130-byte and a 4-byte one), its results are bit-identical to a
+    launch without them, a fifth pending region is refused, and the launch clears the list."""
+    rng = np.random.default_rng(5)
+    for dt, shape in (("bf16", (8192, 768)), ("fp32", (257, 384)), ("bf16", (3, 7))):
+        x = up(xp, rng.standard_normal(shape).astype(F32), dt)
+        g = up(xp, rng.standard_normal(shape[1]).astype(F32), dt)
+        b = up(xp, rng.standard_normal(shape[1]).astype(F32), dt)
+        y0 = xp.layernorm(x, g, b, F32(1e-5)).get()
+        r0 = xp.rmsnorm(x, g, F32(1e-6), 1.0).get()
+        big = xp.random_normal((768, 2304), seed=1, dtype="bf16")
+        full = xp.random_normal((40, 96), seed=2, dtype="fp32")
+        regions = [big, xp.DeviceTensor((39, 65), full.dtype, pitch=96, buf=full.buf,
+                                        offset=full.offset),
+                   xp.DeviceTensor((65,), xp.bfloat16, buf=big.buf, offset=big.offset),
+                   xp.DeviceTensor((1,), full.dtype, buf=full.buf, offset=full.offset)]
+        for t in regions:
+            xp.prefetch_hint(t)
+        with pytest.raises(xp.TLError):
+            xp.prefetch_hint(big)
+        assert np.array_equal(xp.layernorm(x, g, b, F32(1e-5)).get(), y0), (dt, shape)
+        for t in regions:  # room again after the launch
+            xp.prefetch_hint(t)
+        assert np.array_equal(xp.rmsnorm(x, g, F32(1e-6), 1.0).get(), r0), (dt, shape)
+    with pytest.raises(xp.TLError):  # a misaligned region
+        xp.prefetch_hint(xp.DeviceTensor((3,), xp.bfloat16, buf=big.buf, offset=big.offset + 1))
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])

@@ -224,6 +224,34 @@ __device__ __forceinline__ void store16(void* p, const uint4& w) {
   }
 }
 
+// Sum / maximum over a group of LPR lanes (a power of two up to 64, groups aligned to
+// multiples of LPR): xor shuffles with offsets below LPR stay inside the group.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int LPR>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Thread `tid` of `nthreads` loads one 4-byte word of every nthreads-th 128-byte line of the
+// prefetch regions, so their lines are fetched into the caches while the kernel runs; the
+// words are xor-ed together and kept only so the loads are not removed.
+__device__ __forceinline__ uint32_t prefetch_lines(const PrefetchList& pf, int64_t tid,
+                                                   int64_t nthreads) {
+  uint32_t acc = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    for (int64_t l = tid; l < pf.lines[r]; l += nthreads)
+      acc ^= *reinterpret_cast<const uint32_t*>(pf.ptr[r] + l * 128);
+  return acc;
+}
+
 // One wavefront per row, the row held in registers as raw 16-byte chunks (CH per lane),
 // unpacked to float for each pass. Lanes whose chunk lies past the row end load the row's
 // first chunk (a line the wave fetches anyway) and mask it out, so every load is issued
@@ -234,37 +262,40 @@ __device__ __forceinline__ void store16(void* p, const uint4& w) {
 // non-temporally (the host sets it for tensors far larger than the caches, where nothing
 // would be re-read from them). FULL: the row fills all CH x 64 chunks exactly, so no lane
 // needs a mask (124 selects fewer per wave at bf16 x 4096).
-template <typename T, int CH, bool RMS, bool NT, bool FULL>
+template <typename T, int CH, bool RMS, bool NT, bool FULL, int LPR>
 __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
                                                         const T* __restrict__ g,
                                                         const T* __restrict__ b,
                                                         T* __restrict__ y, int64_t rows, int cols,
                                                         int64_t ldx, int64_t ldy, float eps,
-                                                        float goff) {
+                                                        float goff, PrefetchList pf) {
   constexpr int VW = Elem<T>::kVec;
   constexpr bool PRE = CH * sizeof(T) <= 16;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
   if (row >= rows) return;
   const T* xr = x + row * ldx;
   uint4 raw[CH], graw[PRE ? CH : 1], braw[PRE && !RMS ? CH : 1];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
+    const int col = (c * LPR + lane) * VW;
     raw[c] = load16<NT>(xr + (col < cols ? col : 0));
   }
   if constexpr (PRE) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int col = (c * 64 + lane) * VW;
+      const int col = (c * LPR + lane) * VW;
       graw[c] = *reinterpret_cast<const uint4*>(g + (col < cols ? col : 0));
       if constexpr (!RMS) braw[c] = *reinterpret_cast<const uint4*>(b + (col < cols ? col : 0));
     }
   }
+  // after the row's own loads, so the waits for them do not include these
+  const uint32_t pf_word = prefetch_lines(pf, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                                          (int64_t)gridDim.x * blockDim.x);
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const bool in = FULL || (c * 64 + lane) * VW < cols;
+    const bool in = FULL || (c * LPR + lane) * VW < cols;
     float v[VW];
     Elem<T>::unpack(raw[c], v);
 #pragma unroll
@@ -272,13 +303,13 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
   }
   float mean = 0.f, rstd;
   if (RMS) {
-    rstd = 1.0f / sqrtf(wave_sum(s) / (float)cols + eps);
+    rstd = 1.0f / sqrtf(group_sum<LPR>(s) / (float)cols + eps);
   } else {
-    mean = wave_sum(s) / (float)cols;
+    mean = group_sum<LPR>(s) / (float)cols;
     float q = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const bool in = FULL || (c * 64 + lane) * VW < cols;
+      const bool in = FULL || (c * LPR + lane) * VW < cols;
       float v[VW];
       Elem<T>::unpack(raw[c], v);
 #pragma unroll
@@ -287,12 +318,12 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
         q += in ? d * d : 0.f;
       }
     }
-    rstd = 1.0f / sqrtf(wave_sum(q) / (float)cols + eps);
+    rstd = 1.0f / sqrtf(group_sum<LPR>(q) / (float)cols + eps);
   }
   T* yr = y + row * ldy;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
+    const int col = (c * LPR + lane) * VW;
     if (FULL || col < cols) {
       float v[VW], gv[VW], bv[VW], o[VW];
       Elem<T>::unpack(raw[c], v);
@@ -309,6 +340,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
       store16<NT>(yr + col, Elem<T>::pack(o));
     }
   }
+  asm volatile("" ::"v"(pf_word));
 }
 
 // Any shape: one workgroup per row, three passes over the row in global memory.
@@ -389,15 +421,15 @@ __device__ __forceinline__ uint4 load_raw_partial(const T* p, int n) {
 // VALU instructions per element), and a short bf16 row is bound by VALU issue, not HBM.
 // Masked elements hold -inf, so 2^((-inf - max) k) = 0 needs no per-element select.
 // NT: row loads and stores are non-temporal (set by the host for large fp32 tensors).
-template <typename T, int CH, bool CAUSAL, bool TAIL, bool NT>
+template <typename T, int CH, bool CAUSAL, bool TAIL, bool NT, int LPR>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__ x,
                                                            T* __restrict__ y, int64_t rows,
                                                            int cols, int64_t ldx, int64_t ldy,
                                                            float temp, int64_t period,
                                                            int64_t offset) {
   constexpr int VW = Elem<T>::kVec;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
   if (row >= rows) return;
   int valid = cols;
   if (CAUSAL) {
@@ -409,7 +441,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
   uint4 raw[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
+    const int col = (c * LPR + lane) * VW;
     if (TAIL && col < valid && col + VW > cols)
       raw[c] = load_raw_partial(xr + col, cols - col);
     else
@@ -419,7 +451,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
   float mx = -INFINITY;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
+    const int col = (c * LPR + lane) * VW;
     Elem<T>::unpack(raw[c], v[c]);
 #pragma unroll
     for (int e = 0; e < VW; ++e) {
@@ -427,7 +459,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
       mx = fmaxf(mx, v[c][e]);
     }
   }
-  mx = wave_max(mx);
+  mx = group_max<LPR>(mx);
   const float mref = mx == -INFINITY ? 0.f : mx;  // a row with no visible column
   float s = 0.f;
 #pragma unroll
@@ -439,11 +471,11 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
       s += ex;
     }
   }
-  const float rs = 1.0f / wave_sum(s);
+  const float rs = 1.0f / group_sum<LPR>(s);
   T* yr = y + row * ldy;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
-    const int col = (c * 64 + lane) * VW;
+    const int col = (c * LPR + lane) * VW;
     float o[VW];
 #pragma unroll
     for (int e = 0; e < VW; ++e) o[e] = v[c][e] * rs;
@@ -907,6 +939,42 @@ static void launch_embed(tl_ctx* ctx, int ids_dtype, const void* ids, const void
   else go(int64_t());
 }
 
+// Lanes per row of the one-wave norm kernel: 64 (one row per wave) unless a row's 16-byte
+// chunks fill 32 lanes exactly but not 64, then 32 (two rows per wave, no idle lanes). The
+// config-3 LayerNorm, bf16 [8192, 768] (96 chunks): 6.96 -> 5.94 us on hot operands, 9.24 ->
+// 8.82 us rotated. The causal softmax rows (bf16 x 1024, 128 chunks) measured no gain from
+// two or four rows per wave, so the softmax keeps one row per wave.
+static int norm_row_lanes(int64_t chunks) {
+  return (chunks % 64 != 0 && chunks % 32 == 0 && chunks / 32 <= 4) ? 32 : 64;
+}
+// Runs wave(CH, LPR) with the smallest instantiated chunks-per-lane count CH that covers a
+// row of `chunks` 16-byte chunks with LPR lanes (LPR 32 only when LANES32); false when none
+// does (at most MAXCH chunks per lane at 64 lanes, 4 at 32).
+template <int MAXCH, bool LANES32, typename W>
+static bool dispatch_row_shape(int lpr, int64_t chunks, W&& wave) {
+  using std::integral_constant;
+  auto at = [&](auto lpr_tag) -> bool {
+    constexpr int LPR = decltype(lpr_tag)::value;
+    const int64_t per = (chunks + LPR - 1) / LPR;
+    if (per <= 1) wave(integral_constant<int, 1>(), lpr_tag);
+    else if (per <= 2) wave(integral_constant<int, 2>(), lpr_tag);
+    else if (per <= 3) wave(integral_constant<int, 3>(), lpr_tag);
+    else if (per <= 4) wave(integral_constant<int, 4>(), lpr_tag);
+    else if constexpr (LPR == 64) {
+      if (per <= 8) wave(integral_constant<int, 8>(), lpr_tag);
+      else if (MAXCH >= 16 && per <= 16) wave(integral_constant<int, MAXCH >= 16 ? 16 : 8>(), lpr_tag);
+      else return false;
+    } else {
+      return false;
+    }
+    return true;
+  };
+  if constexpr (LANES32) {
+    if (lpr == 32 && (chunks + 31) / 32 <= 4) return at(integral_constant<int, 32>());
+  }
+  return at(integral_constant<int, 64>());
+}
+
 template <typename T, bool RMS>
 static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b, void* y,
                         int64_t rows, int64_t cols, int64_t ldx, int64_t ldy, float eps,
@@ -914,30 +982,29 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
   constexpr int VW = Elem<T>::kVec;
   const bool vec = cols % VW == 0 && ldx % VW == 0 && ldy % VW == 0 && aligned16(x) &&
                    aligned16(y) && aligned16(g) && (RMS || aligned16(b));
-  const int64_t chunks = (cols / VW + 63) / 64;
+  const int64_t cchunks = cols / VW;  // 16-byte chunks per row
   // Rows far larger than the caches (here >= 64 MiB in) are streamed non-temporally: bf16
   // LayerNorm over [16384, 4096] 5.26 -> 5.81 TB/s with gamma/beta loaded early, fp32
   // 5.30 -> 5.75 TB/s. Smaller tensors keep cached stores, since the next kernel reads them.
   const bool nt = rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
-  auto wave = [&](auto ch_tag) {
-    constexpr int CH = decltype(ch_tag)::value;
+  auto wave = [&](auto ch_tag, auto lpr_tag) {
+    constexpr int CH = decltype(ch_tag)::value, LPR = decltype(lpr_tag)::value;
     auto go = [&](auto nt_tag, auto full_tag) {
-      norm_wave_kernel<T, CH, RMS, decltype(nt_tag)::value, decltype(full_tag)::value>
-          <<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
-              (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff);
+      norm_wave_kernel<T, CH, RMS, decltype(nt_tag)::value, decltype(full_tag)::value, LPR>
+          <<<(unsigned)((rows + 256 / LPR - 1) / (256 / LPR)), 256, 0, ctx->stream>>>(
+              (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff,
+              ctx->prefetch);
     };
-    const bool full = cols == (int64_t)CH * 64 * VW;
+    const bool full = cols == (int64_t)CH * LPR * VW;
     if (nt && full) go(std::true_type(), std::true_type());
     else if (nt) go(std::true_type(), std::false_type());
     else if (full) go(std::false_type(), std::true_type());
     else go(std::false_type(), std::false_type());
   };
-  if (vec && chunks <= 1) wave(std::integral_constant<int, 1>());
-  else if (vec && chunks <= 2) wave(std::integral_constant<int, 2>());
-  else if (vec && chunks <= 4) wave(std::integral_constant<int, 4>());
-  else if (vec && chunks <= 8) wave(std::integral_constant<int, 8>());
-  else if (vec && chunks <= 16) wave(std::integral_constant<int, 16>());
-  else
+  const int lpr = norm_row_lanes(cchunks);
+  bool done = false;
+  if (vec) done = dispatch_row_shape<16, true>(lpr, cchunks, wave);
+  if (!done)
     norm_generic_kernel<T, RMS><<<(unsigned)rows, 256, 0, ctx->stream>>>(
         (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, cols, ldx, ldy, eps, goff);
 }
@@ -952,12 +1019,12 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
   // Non-temporal row access for fp32 tensors far larger than the caches (causal fp32
   // [8, 12, 1024, 1024]: 5.04 -> 5.41 TB/s in a probe; the same change slowed bf16 rows).
   const bool nt = sizeof(T) == 4 && rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
-  auto wave = [&](auto ch_tag) {
-    constexpr int CH = decltype(ch_tag)::value;
+  auto wave = [&](auto ch_tag, auto lpr_tag) {
+    constexpr int CH = decltype(ch_tag)::value, LPR = decltype(lpr_tag)::value;
     auto go = [&](auto tail_tag, auto nt_tag) {
       constexpr bool TAIL = decltype(tail_tag)::value;
-      softmax_wave_kernel<T, CH, CAUSAL, TAIL, decltype(nt_tag)::value>
-          <<<(unsigned)((rows + 3) / 4), 256, 0, ctx->stream>>>(
+      softmax_wave_kernel<T, CH, CAUSAL, TAIL, decltype(nt_tag)::value, LPR>
+          <<<(unsigned)((rows + 256 / LPR - 1) / (256 / LPR)), 256, 0, ctx->stream>>>(
               (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
     };
     if (cols % VW != 0) go(std::true_type(), std::false_type());
@@ -999,14 +1066,8 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
     try_ch(std::integral_constant<int, 16>());
     return done;
   };
-  if (vec && chunks <= 64) {
-    wave(std::integral_constant<int, 1>());
-  } else if (vec && chunks <= 128) {
-    wave(std::integral_constant<int, 2>());
-  } else if (vec && chunks <= 256) {
-    wave(std::integral_constant<int, 4>());
-  } else if (vec && chunks <= 512) {
-    wave(std::integral_constant<int, 8>());
+  if (vec && chunks <= 512) {
+    dispatch_row_shape<8, false>(64, chunks, wave);
   } else if (vec && chunks <= 1024 * 16) {
     const int c = lcfg >= 1 && lcfg <= 4 ? lcfg : 5;
     const bool keep = c <= 4 && c % 2 == 0, ntm = c == 5;
@@ -1104,6 +1165,7 @@ static int norm_entry(tl_ctx* ctx, const void* x, const void* g, const void* b, 
                  es * (2.0 * rows * cols + (RMS ? 1 : 2) * cols));
   if (dtype == TL_F32) launch_norm<float, RMS>(ctx, x, g, b, y, rows, cols, ldx, ldy, eps, goff);
   else launch_norm<bf16_t, RMS>(ctx, x, g, b, y, rows, cols, ldx, ldy, eps, goff);
+  ctx->prefetch = PrefetchList{};  // the hint covers one launch
   return ls.finish(RMS ? "rmsnorm_fwd" : "layernorm_fwd");
 }
 

@@ -464,6 +464,23 @@ int tl_sync(tl_ctx* ctx) {
   return check_status_word(ctx);
 }
 
+int tl_prefetch_hint(tl_ctx* ctx, const void* ptr, int64_t bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(bytes >= 0, "negative size");
+  if (bytes < 4) return TL_OK;
+  TL_REQUIRE(ptr && ((uintptr_t)ptr & 3) == 0, "prefetch region must be a non-null, 4-byte aligned "
+             "device pointer");
+  for (int i = 0; i < 4; ++i)
+    if (ctx->prefetch.lines[i] == 0) {
+      ctx->prefetch.ptr[i] = (const unsigned char*)ptr;
+      // words at offsets 0, 128, ..., all inside [ptr, ptr + bytes)
+      ctx->prefetch.lines[i] = (bytes - 4) / 128 + 1;
+      return TL_OK;
+    }
+  return fail(TL_ERR_INVALID, "at most 4 prefetch regions may wait for the next norm launch");
+}
+
 int tl_graph_begin(tl_ctx* ctx) {
   int rc = enter(ctx);
   if (rc) return rc;

@@ -18,6 +18,12 @@
 // host side
 // ---------------------------------------------------------------------------------------
 namespace tl {
+// Up to four device regions a kernel streams into the caches alongside its own work (one
+// 4-byte load per 128-byte line, values discarded): tl_prefetch_hint.
+struct PrefetchList {
+  const unsigned char* ptr[4];
+  int64_t lines[4];
+};
 
 // Records the message for tl_last_error() and returns `code`.
 int fail(int code, const char* fmt, ...);
@@ -58,6 +64,8 @@ struct tl_ctx {
   int attn_decode_cfg = 0;
   // long-row softmax shape (TL_SOFTMAX_LONG_CFG): 0 default, 1..4 (threads, keep) choices
   int softmax_long_cfg = 0;
+  // regions named by tl_prefetch_hint, passed to the next LayerNorm / RMSNorm launch
+  tl::PrefetchList prefetch{};
   // per-shape GEMM tile overrides for automatic calls (TL_GEMM_TILE_FOR="M,N,K=tile;...",
   // tile a tl_gemm_tile value): tuning sweeps inside a whole forward
   struct TileRule {

@@ -49,6 +49,16 @@ def _packed_nk(w, prenorm=None):
     return packed
 
 
+def _warm(*weights):
+    """Name the weights of the products that follow the next norm launch to that launch
+    (xp.prefetch_hint), so they arrive from the device caches rather than HBM. bf16 weights
+    are read by the products as their packed [N, K] copies, which are the ones named; the
+    other dtypes are left alone."""
+    for w in weights:
+        if w.dtype is xp.bfloat16:
+            xp.prefetch_hint(_packed_nk(w))
+
+
 _UNIT_GAIN = {}
 
 
@@ -384,7 +394,11 @@ class TransformerBlock(Layer):
     def forward(self, input, cache=None, layer=0, pos0=0):
         """`cache` / `layer` / `pos0`: decode with a KV cache (MultiHeadAttention.forward)."""
         self.input = input
+        # each norm launch also pulls the next two products' weights into the device caches
+        # (after a forward's 0.8 GB of logits none of them is left there)
+        _warm(self.attn_block.qkv_weights, self.attn_block.out_weights)
         y = self.attn_block._forward(self.pre_attn_norm.forward(input), input, cache, layer, pos0)
+        _warm(self.ffn.weights1, self.ffn.weights2)
         self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), residual=y)
         return self.output
 

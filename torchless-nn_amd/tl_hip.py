@@ -156,6 +156,7 @@ SIGNATURES = {
     "tl_memcpy2d_d2h": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ],
     "tl_memcpy2d_d2d": [_P, _P, _SZ, _P, _SZ, _SZ, _SZ],
     "tl_sync": [_P],
+    "tl_prefetch_hint": [_P, _P, _I64],
     "tl_event_create": [_P, ctypes.POINTER(_P)],
     "tl_event_record": [_P, _P],
     "tl_event_elapsed_ms": [_P, _P, ctypes.POINTER(_F32)],
@@ -769,6 +770,15 @@ def rmsnorm(x: DeviceTensor, gamma, eps, gamma_offset=0.0, out=None):
                               out.pitch, float(eps), float(gamma_offset), x.dtype.code))
     _wrote(out)
     return out
+
+
+def prefetch_hint(t: DeviceTensor):
+    """Have the next layernorm / rmsnorm launch also read `t`'s memory (one word per 128-byte
+    line) so a product right after the norm finds it in the device caches. Advisory: no
+    result changes; up to 4 tensors per norm launch."""
+    span = ((t.nrows - 1) * t.pitch + t.ncols) * t.dtype.itemsize if t.size else 0
+    lib_, h = _c()
+    check(lib_.tl_prefetch_hint(h, t.ptr, span))
 
 
 def softmax(x: DeviceTensor, temperature=1.0, causal=False, period=1, offset=0, out=None):
