@@ -92,7 +92,8 @@ enum tl_gemm_tile {
   TL_TILE_DMA_128x96 = 16,     /* direct global->LDS, 4 waves of 64x48, 2 stages */
   TL_TILE_DMA_256x96_W8 = 17,  /* direct global->LDS, 8 waves of 64x48, 3 stages */
   TL_TILE_PERSIST_256x96_W8 = 18,  /* persistent (see above), 3 stages */
-  TL_TILE_PERSIST_256x256_W8 = 19  /* persistent (see above), 2 stages */
+  TL_TILE_PERSIST_256x256_W8 = 19, /* persistent (see above), 2 stages */
+  TL_TILE_DMA_256x192_W8 = 20      /* direct global->LDS, 8 waves of 64x96, 2 stages */
 };
 
 /* Kernel families for the built-in per-launch event profiler (tl_kprof_*). */

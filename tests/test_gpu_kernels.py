@@ -505,7 +505,8 @@ def test_gemm_qkv_split(xp, dt, heads, dims):
 
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x64s3", "dma128x128s3",
                                   "dma256x256w8", "dma128x96", "dma256x96w8", "persist256x96w8",
-                                  "persist256x128w8", "persist128x128", "persist256x256w8"])
+                                  "persist256x128w8", "persist128x128", "persist256x256w8",
+                                  "dma256x192w8"])
 @pytest.mark.parametrize("mnk", [(300, 524, 192), (513, 1000, 256), (64, 60, 64), (1000, 777, 128)])
 def test_gemm_staged_epilogue_kinds(xp, tile, mnk):
     """bf16 outputs of the direct-to-LDS tiles go through the LDS-staged epilogue: every kind
@@ -629,7 +630,7 @@ def test_gemm_qkv_staged_scatter(xp, tile, cfg):
                                   "256x128w8", "dma128x128", "dma256x128w8", "dma128x64s3",
                                   "dma128x128s3", "persist256x128w8", "persist128x128",
                                   "dma256x256w8", "dma128x96", "dma256x96w8", "persist256x96w8",
-                                  "persist256x256w8"])
+                                  "persist256x256w8", "dma256x192w8"])
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (64, 64, 64), (513, 129, 776), (700, 300, 640)])
 def test_gemm_every_tile_shape(xp, tile, mnk):
     """Forces each MFMA tile shape on ragged M/N and a K tail, with a full epilogue."""

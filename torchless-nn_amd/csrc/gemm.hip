@@ -1492,7 +1492,7 @@ static const TileShape kTiles[] = {{0, 0, 0},      {256, 256, 512}, {256, 128, 2
                                    {256, 128, 512}, {128, 64, 256},  {128, 128, 256},
                                    {256, 128, 512}, {128, 128, 256}, {16, 16, 256},
                                    {256, 256, 512}, {128, 96, 256},  {256, 96, 512},
-                                   {256, 96, 512},  {256, 256, 512}};
+                                   {256, 96, 512},  {256, 256, 512}, {256, 192, 512}};
 static bool is_persistent(int tile) {
   return tile == TL_TILE_PERSIST_256x128_W8 || tile == TL_TILE_PERSIST_128x128 ||
          tile == TL_TILE_PERSIST_256x96_W8 || tile == TL_TILE_PERSIST_256x256_W8;
@@ -1515,7 +1515,7 @@ static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_128x128 
 // tiles when there are enough of them, else with 128-row tiles sized to the last round of
 // resident workgroups; register-prefetch tiles cover other K; 64x64 covers grids too
 // small to fill the GPU.
-static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
+static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool wide_ok) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
   const int64_t t128 = tiles(128, 128), t64 = tiles(128, 64);
   if (K % 64 == 0) {
@@ -1532,7 +1532,18 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) 
     const int64_t t96w = tiles(256, 96), t128w = tiles(256, 128);
     if (K >= 256 && t96w >= cus) {
       const int64_t w96 = (t96w + cus - 1) / cus * 96, w128 = (t128w + cus - 1) / cus * 128;
-      return w96 < w128 ? TL_TILE_DMA_256x96_W8 : TL_TILE_DMA_256x128_W8;
+      int best = w96 < w128 ? TL_TILE_DMA_256x96_W8 : TL_TILE_DMA_256x128_W8;
+      // 192 wide on the same terms, preferred on a tie: 8 waves of 64x96 read a sixth fewer
+      // LDS fragment bytes per flop than 64x64 (the inner loop alone 1.86 vs 1.47 PFLOP/s),
+      // though only two stages fit the LDS. GPT-2 FFN1 (N = 3072: 2 rounds of 192 against
+      // 3 of 128): 54.6 -> 49.1 us behind a warming LayerNorm in a standalone harness. Only
+      // for the staged plain / bias / activation / residual epilogues (a 96-column wave slab
+      // would straddle QKV parts or GeGLU pairs) and K > 512 (shorter K runs persistent).
+      if (wide_ok && K > 512) {
+        const int64_t w192 = (tiles(256, 192) + cus - 1) / cus * 192;
+        if (w192 <= std::min(w96, w128)) best = TL_TILE_DMA_256x192_W8;
+      }
+      return best;
     }
     // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
     // workgroups wastes the least area (N = 768 or 2304: 128x96; 3072: 128x128)
@@ -1590,6 +1601,7 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
     case TL_TILE_DMA_256x256_W8: gemm_dma_kernel<TO, 256, 256, 2, 4, 2, 2><<<grid, 512, 0, st>>>(p); break;
     case TL_TILE_DMA_128x96: gemm_dma_kernel<TO, 128, 96, 2, 2, 2, 2><<<grid, 256, 0, st>>>(p); break;
     case TL_TILE_DMA_256x96_W8: gemm_dma_kernel<TO, 256, 96, 4, 2, 2, 3><<<grid, 512, 0, st>>>(p); break;
+    case TL_TILE_DMA_256x192_W8: gemm_dma_kernel<TO, 256, 192, 4, 2, 2, 2><<<grid, 512, 0, st>>>(p); break;
     default: gemm_mfma_kernel<TO, 64, 64, 2, 2><<<grid, 256, 0, st>>>(p); break;
   }
 }
@@ -1630,7 +1642,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   TL_REQUIRE(d->b_layout == TL_B_NK || d->b_layout == TL_B_KN, "bad b_layout %d", d->b_layout);
   TL_REQUIRE(d->act == TL_ACT_NONE || d->act == TL_ACT_GELU || d->act == TL_ACT_SILU, "bad activation");
   TL_REQUIRE(d->divisor != 0.f, "divisor must be non-zero");
-  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_PERSIST_256x256_W8, "bad tile hint %d", d->tile);
+  TL_REQUIRE(d->tile >= 0 && d->tile <= TL_TILE_DMA_256x192_W8, "bad tile hint %d", d->tile);
   const int64_t batch = d->batch <= 0 ? 1 : d->batch;
   const int64_t binner = d->batch_inner <= 0 ? 1 : d->batch_inner;
   TL_REQUIRE(batch <= 65535, "batch %lld exceeds 65535", (long long)batch);
@@ -1772,12 +1784,13 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   }
   if (mfma) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus);
+    const bool wide_ok = !f32out && p.epi >= EPI_PLAIN && p.epi <= EPI_RES;
+    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus, wide_ok);
     bool fixed = d->tile != 0;  // a caller's tile, or a TL_GEMM_TILE_FOR one, is kept as is
     if (!d->tile)
       for (const auto& r : ctx->tile_rules)
         if (r.M == d->M && r.N == d->N && r.K == d->K && r.tile > 0 &&
-            r.tile <= TL_TILE_PERSIST_256x256_W8 && r.tile != TL_TILE_SKINNY) {
+            r.tile <= TL_TILE_DMA_256x192_W8 && r.tile != TL_TILE_SKINNY) {
           tile = r.tile;
           fixed = true;
         }

@@ -28,7 +28,7 @@ GEMM_TILES = {"auto": 0, "256x256": 1, "256x128": 2, "128x128": 3, "128x64": 4, 
               "dma128x64s3": 10, "dma128x128s3": 11, "persist256x128w8": 12,
               "persist128x128": 13, "skinny": 14, "dma256x256w8": 15,
               "dma128x96": 16, "dma256x96w8": 17, "persist256x96w8": 18,
-              "persist256x256w8": 19}
+              "persist256x256w8": 19, "dma256x192w8": 20}
 KFAMILY = {
     "gemm_mfma": 0, "gemm_batched": 1, "gemm_simt": 2, "layernorm": 3, "rmsnorm": 4,
     "softmax": 5, "rope": 6, "act": 7, "embed": 8, "argmax": 9, "attention": 10, "misc": 11,
