@@ -186,8 +186,9 @@ int tl_sync(tl_ctx* ctx);
  * next tl_layernorm_fwd / tl_rmsnorm_fwd on this context also reads, one word per 128-byte
  * line, so a weight that the product after the norm reads arrives from the device caches
  * instead of HBM. Advisory: results do not change, the values read are discarded, and the
- * list is cleared by that launch. The region must stay allocated until the launch has run
- * (in a captured graph, until the graph is destroyed). */
+ * list is cleared by that launch. The region must lie inside one live tl_malloc block
+ * (TL_ERR_INVALID otherwise); freeing that block drops it from the list. In a captured graph
+ * the region is read on every replay, so it must stay allocated while the graph lives. */
 int tl_prefetch_hint(tl_ctx* ctx, const void* ptr, int64_t bytes);
 /* HIP graphs of the context stream, for replaying a whole step (a decode step, a short
  * forward) with one launch instead of one host call per kernel. No reference counterpart

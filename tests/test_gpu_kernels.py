@@ -209,6 +209,22 @@ def test_prefetch_hint_changes_no_result(xp):
         assert np.array_equal(xp.rmsnorm(x, g, F32(1e-6), 1.0).get(), r0), (dt, shape)
     with pytest.raises(xp.TLError):  # a misaligned region
         xp.prefetch_hint(xp.DeviceTensor((3,), xp.bfloat16, buf=big.buf, offset=big.offset + 1))
+    # memory the library did not hand out is refused on the host (nothing is read)
+    lib, h = xp.lib(), xp.ctx().handle
+    assert lib.tl_prefetch_hint(h, 0x10000, 4096) == xp.TL_ERR_INVALID
+    end = big.buf.ptr + big.buf.nbytes
+    assert lib.tl_prefetch_hint(h, end - 64, 128) == xp.TL_ERR_INVALID  # runs past the block
+    # freeing a hinted tensor drops its region: the four slots have room again
+    tmp = [xp.empty((1000,), "fp32") for _ in range(4)]
+    for t in tmp:
+        xp.prefetch_hint(t)
+    del tmp[2]
+    xp.prefetch_hint(big)
+    with pytest.raises(xp.TLError):
+        xp.prefetch_hint(big)
+    x = up(xp, rng.standard_normal((64, 768)).astype(F32), "bf16")
+    g = up(xp, rng.standard_normal(768).astype(F32), "bf16")
+    assert np.array_equal(xp.rmsnorm(x, g, F32(1e-6), 1.0).get(), xp.rmsnorm(x, g, F32(1e-6), 1.0).get())
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])

@@ -304,6 +304,13 @@ int tl_free(tl_ctx* ctx, void* ptr) {
   if (!ptr) return TL_OK;
   auto it = ctx->live.find(ptr);
   if (it == ctx->live.end()) return fail(TL_ERR_INVALID, "tl_free: %p was not allocated by tl_malloc", ptr);
+  // a pending prefetch region inside this block is dropped: the block may be released to
+  // the driver before the norm launch that would read it
+  for (int i = 0; i < 4; ++i) {
+    const unsigned char* b = (const unsigned char*)ptr;
+    if (ctx->prefetch.lines[i] > 0 && ctx->prefetch.ptr[i] >= b && ctx->prefetch.ptr[i] < b + it->second)
+      ctx->prefetch.lines[i] = 0;
+  }
   if (ctx->graph_block_size.count(ptr)) {
     // a live graph still writes it on every replay: held until tl_graph_destroy
     ctx->graph_released.insert(ptr);
@@ -471,6 +478,19 @@ int tl_prefetch_hint(tl_ctx* ctx, const void* ptr, int64_t bytes) {
   if (bytes < 4) return TL_OK;
   TL_REQUIRE(ptr && ((uintptr_t)ptr & 3) == 0, "prefetch region must be a non-null, 4-byte aligned "
              "device pointer");
+  // only memory this context handed out, so a stray pointer is an error here and never a
+  // fault in the norm kernel
+  bool inside = false;
+  const unsigned char* p = (const unsigned char*)ptr;
+  for (const auto& blk : ctx->live) {
+    const unsigned char* b = (const unsigned char*)blk.first;
+    if (p >= b && p < b + blk.second) {
+      inside = bytes <= (int64_t)(b + blk.second - p);
+      break;
+    }
+  }
+  TL_REQUIRE(inside, "prefetch region [%p, +%lld) is not inside one live tl_malloc block", ptr,
+             (long long)bytes);
   for (int i = 0; i < 4; ++i)
     if (ctx->prefetch.lines[i] == 0) {
       ctx->prefetch.ptr[i] = (const unsigned char*)ptr;
