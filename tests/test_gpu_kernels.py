@@ -83,10 +83,11 @@ def test_cast_rejects_overlapping_operands(xp):
 
 # ---- LayerNorm / RMSNorm ------------------------------------------------------------------
 # (64, 768) bf16, (7, 256) bf16 and (9, 384) fp32 rows fill 32 lanes but not 64 (two rows per
-# wave; an odd row count leaves the last wave's second row empty); (13, 1280) bf16 does not fit
-# 32 lanes and falls back to one row per wave
-NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (7, 256), (9, 384), (13, 1280), (33, 4096),
-               (2, 5000), (4, 8192), (3, 12000)]
+# wave; an odd row count leaves the last wave's second row empty); (5, 128) and (9, 384) bf16
+# fill 16 lanes (four rows per wave, the last wave partly empty); (6, 640) and (13, 1280)
+# bf16 fit neither and take one row per wave
+NORM_SHAPES = [(1, 8), (3, 7), (5, 128), (64, 768), (7, 256), (9, 384), (6, 640), (13, 1280),
+               (33, 4096), (2, 5000), (4, 8192), (3, 12000)]
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])

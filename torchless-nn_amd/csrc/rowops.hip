@@ -940,16 +940,20 @@ static void launch_embed(tl_ctx* ctx, int ids_dtype, const void* ids, const void
 }
 
 // Lanes per row of the one-wave norm kernel: 64 (one row per wave) unless a row's 16-byte
-// chunks fill 32 lanes exactly but not 64, then 32 (two rows per wave, no idle lanes). The
-// config-3 LayerNorm, bf16 [8192, 768] (96 chunks): 6.96 -> 5.94 us on hot operands, 9.24 ->
-// 8.82 us rotated. The causal softmax rows (bf16 x 1024, 128 chunks) measured no gain from
+// chunks fill 32 (or else 16) lanes exactly but not 64: then two (four) rows per wave and no
+// idle lanes. The config-3 LayerNorm, bf16 [8192, 768] (96 chunks): 6.96 -> 5.94 us on hot
+// operands, 9.24 -> 8.82 us rotated. The causal softmax rows (bf16 x 1024, 128 chunks) measured no gain from
 // two or four rows per wave, so the softmax keeps one row per wave.
 static int norm_row_lanes(int64_t chunks) {
-  return (chunks % 64 != 0 && chunks % 32 == 0 && chunks / 32 <= 4) ? 32 : 64;
+  if (chunks % 64 == 0) return 64;
+  if (chunks % 32 == 0 && chunks / 32 <= 4) return 32;
+  // the ViT-S/4 LayerNorm, bf16 [33280, 384] = 48 chunks: four rows per wave, 3 chunks a lane
+  if (chunks % 16 == 0 && chunks / 16 <= 4) return 16;
+  return 64;
 }
 // Runs wave(CH, LPR) with the smallest instantiated chunks-per-lane count CH that covers a
-// row of `chunks` 16-byte chunks with LPR lanes (LPR 32 only when LANES32); false when none
-// does (at most MAXCH chunks per lane at 64 lanes, 4 at 32).
+// row of `chunks` 16-byte chunks with LPR lanes (LPR 32 or 16 only when LANES32); false when
+// none does (at most MAXCH chunks per lane at 64 lanes, 4 at 32 or 16).
 template <int MAXCH, bool LANES32, typename W>
 static bool dispatch_row_shape(int lpr, int64_t chunks, W&& wave) {
   using std::integral_constant;
@@ -971,6 +975,7 @@ static bool dispatch_row_shape(int lpr, int64_t chunks, W&& wave) {
   };
   if constexpr (LANES32) {
     if (lpr == 32 && (chunks + 31) / 32 <= 4) return at(integral_constant<int, 32>());
+    if (lpr == 16 && (chunks + 15) / 16 <= 4) return at(integral_constant<int, 16>());
   }
   return at(integral_constant<int, 64>());
 }
