@@ -281,6 +281,26 @@ def test_gemma_decode_bf16_matches_prefill(tl):
     assert ref.max_rel(rows[0][:1], want[:, -1]) <= 2e-2
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_gemma_last_only_prefill(tl, dt):
+    """forward(last_only=True), the prefill of a generation: logits [B, 1, V] of each
+    sequence's last position equal the last rows of the full forward (the final norm reads
+    the strided last rows in place; the LM head runs as the few-row product), and both
+    fill the KV cache identically."""
+    cfg = dict(vocab=1000, ctx=512, layers=2, d=256, heads=8, kv_heads=1, head_dim=256,
+               ffn=1024, rope_base=10000.0)
+    model = _gemma(tl, cfg, dt, 21, 0.05)
+    ids = np.random.default_rng(22).integers(0, 1000, (3, 77))
+    c_full, c_last = model.new_cache(3, 80), model.new_cache(3, 80)
+    full = model.forward(ids, c_full, 0).get()
+    last = model.forward(ids, c_last, 0, last_only=True)
+    assert last.shape == (3, 1, 1000)
+    assert ref.max_rel(last.get()[:, 0], full[:, -1]) <= _tol(dt)
+    for layer in range(cfg["layers"]):  # k [B, Hkv, L, D], vt [B, Hkv, D, L]: 77 positions
+        assert np.array_equal(c_full.k[layer].get()[:, :, :77], c_last.k[layer].get()[:, :, :77])
+        assert np.array_equal(c_full.vt[layer].get()[..., :77], c_last.vt[layer].get()[..., :77])
+
+
 def _device_params(model, cfg):
     """Download the device-seeded parameters under the oracle's names."""
     names = [n for n, _ in ref.gemma_param_shapes(cfg)]

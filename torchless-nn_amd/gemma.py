@@ -42,7 +42,11 @@ class GemmaDecoder:
         c = self.cfg
         return KVCache(c["layers"], batch, c["kv_heads"], capacity, c["head_dim"], self.dtype)
 
-    def forward(self, ids, cache=None, pos0=0):
+    def forward(self, ids, cache=None, pos0=0, last_only=False):
+        """Logits [B, T, V]; with last_only, [B, 1, V] for each sequence's last position
+        only (what a generation step needs: the final norm and the LM head run on B rows
+        instead of B x T, the weight-streaming decode product instead of a 4 GB logits
+        write at config 5)."""
         x = self.front.forward(ids)
         c = self.cfg
         T, start = x.shape[1], pos0
@@ -54,6 +58,11 @@ class GemmaDecoder:
             pos0 = DevicePosition.at(pos0, T, c["head_dim"], c.get("rope_base", 10000.0))
         for i, blk in enumerate(self.blocks):
             x = blk.forward(x, cache, i, pos0)
+        if last_only and T > 1:
+            B, _, C = x.shape
+            es = x.dtype.itemsize
+            x = xp.DeviceTensor((B, 1, C), x.dtype, pitch=T * x.pitch, buf=x.buf,
+                                offset=x.offset + (T - 1) * x.pitch * es)
         logits = self.back.forward(self.final_norm.forward(x))
         if cache is not None:
             cache.length = start + T
@@ -100,7 +109,7 @@ class GemmaDecoder:
                 and xp.attention_decode_dev_supported(self.dtype, self.cfg["head_dim"],
                                                       cache.capacity)):
             return self._generate_graph(ids, n_new, cache)
-        logits = self.forward(ids, cache, 0)
+        logits = self.forward(ids, cache, 0, last_only=True)
         steps, kept = [], []
         for t in range(n_new):
             last = self.last_rows(logits)
@@ -118,7 +127,7 @@ class GemmaDecoder:
         if T + n_new - 1 > cache.capacity:
             raise ValueError("KV cache too small")
         c = self.cfg
-        logits = self.forward(ids, cache, 0)
+        logits = self.forward(ids, cache, 0, last_only=True)
         tok = xp.empty((B,), xp.int64)
         xp.argmax(self.last_rows(logits), out=tok)
         del logits
