@@ -183,6 +183,12 @@ def test_kv_cache_generation_matches_recomputing_the_window(tl, dt):
     cache = gpt.new_cache(net, 3, 70)
     gpt.forward_cached(net, ids, cache, 0)
     assert ref.max_rel(head.output.get()[:, -1], lrows[:, 0]) <= tol
+    # the generation prefill: the layers after the last block on the last position only
+    cache2 = gpt.new_cache(net, 3, 70)
+    last = gpt.forward_cached(net, ids, cache2, 0, last_only=True)
+    assert last.shape == (3, 1, 65)
+    assert ref.max_rel(head.output.get()[:, 0], lrows[:, 0]) <= tol
+    assert ref.max_rel(last.get()[:, 0], rows[:, 0]) <= tol
     for t in range(29):
         gpt.forward_cached(net, seq[:, 40 + t:41 + t], cache, 40 + t)
         assert ref.max_rel(head.output.get()[:, 0], lrows[:, t + 1]) <= tol, t

@@ -73,10 +73,13 @@ def new_cache(net, batch, capacity):
                    net.layers[0].embedding_table.table.dtype)
 
 
-def forward_cached(net, ids, cache, pos0):
+def forward_cached(net, ids, cache, pos0, last_only=False):
     """The network's layers over ids [B, T] sitting at positions pos0 .. pos0 + T - 1, with
     each block's keys and values kept in `cache` (earlier positions are read from it).
-    Returns the last layer's output (the SoftMax probabilities) [B, T, V]."""
+    Returns the last layer's output (the SoftMax probabilities) [B, T, V], or with last_only
+    [B, 1, V] for each sequence's last position (the layers after the last block run on B
+    rows: what a generation step needs)."""
+    n_blocks = sum(isinstance(layer, TransformerBlock) for layer in net.layers)
     x, i = ids, 0
     for layer in net.layers:
         if isinstance(layer, GPTEmbedFront):
@@ -84,6 +87,10 @@ def forward_cached(net, ids, cache, pos0):
         elif isinstance(layer, TransformerBlock):
             x = layer.forward(x, cache, i, pos0)
             i += 1
+            if last_only and i == n_blocks and x.shape[1] > 1:
+                B, T, C = x.shape
+                x = xp.DeviceTensor((B, 1, C), x.dtype, pitch=T * x.pitch, buf=x.buf,
+                                    offset=x.offset + (T - 1) * x.pitch * x.dtype.itemsize)
         else:
             x = layer.forward(x)
     return x
@@ -113,7 +120,7 @@ def generate(net, ids, n_new, sample=True, cache=None):
         return np.zeros((B, 0), np.int64)
     if cache is None:
         cache = new_cache(net, B, T + n_new)
-    probs = forward_cached(net, ids, cache, 0)
+    probs = forward_cached(net, ids, cache, 0, last_only=True)
     V = probs.shape[-1]
     steps = []
     for t in range(n_new):
