@@ -441,13 +441,14 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[g][j][v]);
       } else {
+        // key kv0 + 16 j + 4 fg + v is visible when 16 j + v <= lim: one per-lane limit, so
+        // each element is a compare against an immediate (no per-element key index)
+        const int lim = min(p.Tk - 1, p.causal ? qpos + off : p.Tk - 1) - kv0 - 4 * fg;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int kv = kv0 + j * 16 + 4 * fg + v;
-            const bool ok = kv < p.Tk && (!p.causal || kv <= qpos + off);
-            s[g][j][v] = ok ? s[g][j][v] : -INFINITY;
+            s[g][j][v] = j * 16 + v <= lim ? s[g][j][v] : -INFINITY;
             mx = fmaxf(mx, s[g][j][v]);
           }
       }
