@@ -218,13 +218,15 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   #pragma unroll
           for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[j][v]);
       } else {
+        // key kv0 + 16 j + 4 fg + v is visible when 16 j + v <= lim (one per-lane limit)
+        const int lim = (int)max(min(min((int64_t)p.Tk - 1, p.causal ? (int64_t)qpos + p.offset
+                                                                    : (int64_t)p.Tk - 1) -
+                                         kv0 - 4 * fg, (int64_t)64), (int64_t)-1);
   #pragma unroll
         for (int j = 0; j < 4; ++j)
   #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int kv = kv0 + j * 16 + 4 * fg + v;
-            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
-            s[j][v] = ok ? s[j][v] : -INFINITY;
+            s[j][v] = j * 16 + v <= lim ? s[j][v] : -INFINITY;
             mx = fmaxf(mx, s[j][v]);
           }
       }
@@ -965,13 +967,15 @@ __global__ __launch_bounds__(512) void attention_fwd_short_kernel(AttnParams p) 
   }
   const int qpos = q0 + fr;
   float mx = -INFINITY;
+  // key 16 j + 4 fg + v is visible when 16 j + v <= lim (one per-lane limit)
+  const int lim = (int)max(min(min((int64_t)p.Tk - 1, p.causal ? (int64_t)qpos + p.offset
+                                                              : (int64_t)p.Tk - 1) - 4 * fg,
+                               (int64_t)16 * NKT), (int64_t)-1);
 #pragma unroll
   for (int j = 0; j < NKT; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int kv = j * 16 + 4 * fg + v;
-      const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
-      s[j][v] = ok ? s[j][v] * p.scale_log2 : -INFINITY;
+      s[j][v] = j * 16 + v <= lim ? s[j][v] * p.scale_log2 : -INFINITY;
       mx = fmaxf(mx, s[j][v]);
     }
   mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -1163,13 +1167,15 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[j][v]);
       } else {
+        // key kv0 + 16 j + 4 fg + v is visible when 16 j + v <= lim (one per-lane limit)
+        const int lim = (int)max(min(min((int64_t)p.Tk - 1, p.causal ? (int64_t)qpos + p.offset
+                                                                    : (int64_t)p.Tk - 1) -
+                                         kv0 - 4 * fg, (int64_t)64), (int64_t)-1);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int kv = kv0 + j * 16 + 4 * fg + v;
-            const bool ok = kv < p.Tk && (!p.causal || (int64_t)kv <= (int64_t)qpos + p.offset);
-            s[j][v] = ok ? s[j][v] : -INFINITY;
+            s[j][v] = j * 16 + v <= lim ? s[j][v] : -INFINITY;
             mx = fmaxf(mx, s[j][v]);
           }
       }
