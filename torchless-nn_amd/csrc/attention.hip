@@ -320,7 +320,8 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][BKV * D];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][D * BKV];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar mask branches
   const int fr = lane & 15, fg = lane >> 4;
   const int bh = blockIdx.x;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
