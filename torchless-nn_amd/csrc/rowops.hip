@@ -262,7 +262,10 @@ __device__ __forceinline__ uint32_t prefetch_lines(const PrefetchList& pf, int64
 // non-temporally (the host sets it for tensors far larger than the caches, where nothing
 // would be re-read from them). FULL: the row fills all CH x 64 chunks exactly, so no lane
 // needs a mask (124 selects fewer per wave at bf16 x 4096).
-template <typename T, int CH, bool RMS, bool NT, bool FULL, int LPR>
+// PF: the launch also reads the prefetch regions (a separate instantiation, so that norms
+// launched without regions keep their registers: the loads issued after the row's own hold
+// those registers live, 126 -> 161 VGPRs at bf16 x 4096, a wave less per SIMD).
+template <typename T, int CH, bool RMS, bool NT, bool FULL, int LPR, bool PF>
 __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
                                                         const T* __restrict__ g,
                                                         const T* __restrict__ b,
@@ -290,8 +293,10 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
     }
   }
   // after the row's own loads, so the waits for them do not include these
-  const uint32_t pf_word = prefetch_lines(pf, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
-                                          (int64_t)gridDim.x * blockDim.x);
+  uint32_t pf_word = 0;
+  if constexpr (PF)
+    pf_word = prefetch_lines(pf, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                             (int64_t)gridDim.x * blockDim.x);
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -340,7 +345,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
       store16<NT>(yr + col, Elem<T>::pack(o));
     }
   }
-  asm volatile("" ::"v"(pf_word));
+  if constexpr (PF) asm volatile("" ::"v"(pf_word));
 }
 
 // Any shape: one workgroup per row, three passes over the row in global memory.
@@ -992,13 +997,26 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
   // LayerNorm over [16384, 4096] 5.26 -> 5.81 TB/s with gamma/beta loaded early, fp32
   // 5.30 -> 5.75 TB/s. Smaller tensors keep cached stores, since the next kernel reads them.
   const bool nt = rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
+  const bool pf = ctx->prefetch.lines[0] || ctx->prefetch.lines[1] || ctx->prefetch.lines[2] ||
+                  ctx->prefetch.lines[3];
   auto wave = [&](auto ch_tag, auto lpr_tag) {
     constexpr int CH = decltype(ch_tag)::value, LPR = decltype(lpr_tag)::value;
     auto go = [&](auto nt_tag, auto full_tag) {
-      norm_wave_kernel<T, CH, RMS, decltype(nt_tag)::value, decltype(full_tag)::value, LPR>
-          <<<(unsigned)((rows + 256 / LPR - 1) / (256 / LPR)), 256, 0, ctx->stream>>>(
+      constexpr bool NTV = decltype(nt_tag)::value, FULLV = decltype(full_tag)::value;
+      const unsigned grid = (unsigned)((rows + 256 / LPR - 1) / (256 / LPR));
+      // weights are warmed for products over in-cache activations only, so the streamed
+      // (non-temporal) instantiations carry no prefetch
+      if constexpr (!NTV) {
+        if (pf) {
+          norm_wave_kernel<T, CH, RMS, false, FULLV, LPR, true><<<grid, 256, 0, ctx->stream>>>(
               (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff,
               ctx->prefetch);
+          return;
+        }
+      }
+      norm_wave_kernel<T, CH, RMS, NTV, FULLV, LPR, false><<<grid, 256, 0, ctx->stream>>>(
+          (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff,
+          ctx->prefetch);
     };
     const bool full = cols == (int64_t)CH * LPR * VW;
     if (nt && full) go(std::true_type(), std::true_type());
