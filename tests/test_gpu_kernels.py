@@ -900,11 +900,16 @@ def test_attention_fused_grouped_heads_and_offset(xp, heads):
     (1, 4, 2, 300, 300, 304, True, 0),      # ragged last block and chunk, NaN capacity pad
     (2, 4, 1, 330, 400, 408, True, 70),     # grouped kv heads, queries at an offset
     (1, 2, 2, 257, 390, 392, False, 0),     # unmasked, one row in the last block
-    (8, 12, 12, 1024, 1024, 1024, True, 0),  # the GPT-2-small shape
+    (8, 12, 12, 1024, 1024, 1024, True, 0),  # the GPT-2-small shape (768 blocks, 3 rounds)
+    (3, 12, 12, 1024, 1024, 1024, True, 0),  # 288 blocks: a partial second round of CUs
+    (5, 12, 12, 1000, 1000, 1000, True, 0),  # 480 blocks
+    (9, 12, 12, 1024, 1024, 1024, True, 0),  # 864 blocks: more than are resident at once
 ])
 def test_attention_wide_long_sequences(xp, D, case):
     """The wide prefill kernel (32 query rows per wave, 128-row blocks, heaviest causal block
-    first) against the float64 definition, with NaN in the key/value capacity padding."""
+    first, or CU-balanced when the grid is resident at once) against the float64 definition,
+    with NaN in the key/value capacity padding and in the output beforehand, so a query
+    block that no workgroup computes fails the finiteness check."""
     B, Hq, Hkv, Tq, Tk, Lk, causal, offset = case
     rng = np.random.default_rng(Tq + Tk + D)
     q = ref.round_bf16(rng.standard_normal((B, Hq, Tq, D)).astype(F32))
@@ -912,7 +917,7 @@ def test_attention_wide_long_sequences(xp, D, case):
     vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
     k[:, :, Tk:] = np.nan
     vt[:, :, :, Tk:] = np.nan
-    out = xp.empty((B, Tq, Hq * D), "bf16")
+    out = up(xp, np.full((B, Tq, Hq * D), np.nan, F32), "bf16")
     divisor = float(np.float32(np.sqrt(D)))
     xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
                  n_heads_kv=Hkv, divisor=divisor, causal=causal, offset=offset, seq_k=Tk)

@@ -51,6 +51,9 @@ struct AttnParams {
   // offset + Tq - 1. When set, the decode kernel rotates the queries and this call's new
   // cache keys (positions offset ..) itself and writes the rotated keys back to the cache.
   const float* rope;
+  // wide kernel, causal: CUs per round of the resident grid for its balanced block order
+  // (0: heaviest first)
+  int fold;
 };
 
 // V^T rows of a 64-key chunk in LDS (the long-sequence kernels): the P.V operand of lane
@@ -323,11 +326,24 @@ __global__ __launch_bounds__(256) void attention_fwd_wide_kernel(AttnParams p) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar mask branches
   const int fr = lane & 15, fg = lane >> 4;
-  const int bh = blockIdx.x;
+  const int nqb = (p.Tq + RB - 1) / RB;
+  // Block ranks run heaviest first: rank r is head r % nbh, query block nqb - 1 - r / nbh
+  // (a causal block reads qb + 1 chunks of 128 keys). When the whole grid is resident at
+  // once (p.fold = CUs), workgroups land breadth-first, so CU c holds dispatch positions c,
+  // c + CUs, c + 2 CUs; every second round of CUs then takes its ranks in reverse, so each
+  // CU pairs heavy blocks with light ones (GPT-2 B 8 T 1024: busiest CU 34 -> 30 chunk
+  // units against a mean of 27). Otherwise blocks keep the heaviest-first order.
+  const int nbh = (int)gridDim.x;
+  const int pos = (int)blockIdx.y * nbh + (int)blockIdx.x;
+  int r = pos;
+  if (p.fold) {
+    const int t = pos / p.fold, c = pos - t * p.fold;
+    if (t & 1) r = t * p.fold + min(p.fold, nbh * nqb - t * p.fold) - 1 - c;
+  }
+  const int bh = r % nbh;
+  const int qb = nqb - 1 - r / nbh;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
-  const int nqb = (p.Tq + RB - 1) / RB;
-  const int qb = nqb - 1 - (int)blockIdx.y;
   const int w0 = qb * RB + wave * 32;  // first row of this wave; group g starts at w0 + 16 g
   const int off = (int)p.offset;        // < 2^30 (host-checked)
   const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
@@ -1025,6 +1041,21 @@ __global__ __launch_bounds__(512) void attention_fwd_short_kernel(AttnParams p) 
   }
 }
 
+// Resident wide-kernel workgroups per CU (register-limited: 3 at head dim 64), queried once;
+// 0 if the query fails, which keeps the heaviest-first block order.
+template <int D>
+static int wide_blocks_per_cu() {
+  static const int n = [] {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attention_fwd_wide_kernel<D>, 256, 0) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    return b;
+  }();
+  return n;
+}
+
 template <int D>
 static void launch_short(int nkh, dim3 grid, int threads, hipStream_t st, const AttnParams& p) {
   switch (nkh) {
@@ -1292,6 +1323,7 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
   p.scale_log2 = 1.4426950408889634f / divisor;
   p.pos_dev = pos_dev;
   p.rope = rope;
+  p.fold = 0;
   if (rope) {
     TL_REQUIRE(head_dim >= 64 && (n_heads_q / n_heads_kv) * seq_q <= 16 && causal && ((uintptr_t)rope & 15u) == 0,
                "fused RoPE is implemented for causal decode at head_dim >= 64 (16-byte aligned table)");
@@ -1384,6 +1416,11 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     const int64_t nqb = (seq_q + 127) / 128;
     TL_REQUIRE(nqb <= 65535, "too many 128-row query blocks");
     const dim3 grid((unsigned)(batch * n_heads_q), (unsigned)nqb);
+    if (causal && nqb > 1) {
+      const int per_cu = head_dim == 32 ? wide_blocks_per_cu<32>() : wide_blocks_per_cu<64>();
+      const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+      if (per_cu > 0 && (int64_t)grid.x * nqb <= per_cu * cus) p.fold = (int)cus;
+    }
     if (head_dim == 32) attention_fwd_wide_kernel<32><<<grid, 256, 0, ctx->stream>>>(p);
     else attention_fwd_wide_kernel<64><<<grid, 256, 0, ctx->stream>>>(p);
     return ls.finish("attention_fwd_wide");
