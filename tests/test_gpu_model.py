@@ -101,6 +101,50 @@ def test_multihead_attention_layer(tl, dt, decoder, shape):
     assert ref.max_rel(y, want) <= tol, (dt, decoder, shape)
 
 
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_block_sublayer_taps_like_the_reference(tl, dt):
+    """TransformerBlock with fuse_residual = False (reference layers.py:463-467): attn_block
+    .output is MHA(LN1 x) and ffn.output is FFN(LN2 y), each against the oracle's sublayer
+    (not the residual stream), and the block output equals both the oracle's block and the
+    fused-residual path's."""
+    tl["backend"].set_float_type(dt)
+    B, T, C, H = 2, 40, 64, 4
+    import activations
+    blk = tl["layers"].TransformerBlock(C, T, H, activations.GeLU, decoder=True)
+    rng = np.random.default_rng(29)
+    P = [rng.standard_normal(p.shape).astype(F32) * F32(0.2) for p in blk.parameters]
+    P[0] = 1 + P[0]  # LN1 gamma around 1
+    P[6] = 1 + P[6]  # LN2 gamma around 1
+    rnd = ref.round_bf16 if dt == "bf16" else None
+    P = [rnd(p) if rnd else p for p in P]
+    for p, a in zip(blk.parameters, P):
+        p.set(a)
+    x = rng.standard_normal((B, T, C)).astype(F32)
+    x = rnd(x) if rnd else x
+    xd = tl["xp"].array(x, dtype=dt)
+    fused = blk.forward(xd).get()
+    blk.fuse_residual = False
+    try:
+        out = blk.forward(xd).get()
+        attn_tap = blk.attn_block.output.get()
+        ffn_tap = blk.ffn.output.get()
+    finally:
+        del blk.fuse_residual
+    g1, be1, wqkv, bqkv, wo, bo, g2, be2, w1, bb1, w2, bb2 = P
+    r = rnd or (lambda a: a)
+    want_attn = ref.mha(r(ref.layernorm(x, g1, be1)), wqkv, bqkv, wo, bo, H, True, T, rnd)
+    y = r(x + r(want_attn))
+    want_ffn = ref.ffn(r(ref.layernorm(y, g2, be2)), w1, bb1, w2, bb2, "gelu", rnd)
+    tol = 1e-5 if dt == "fp32" else 2e-2
+    assert ref.max_rel(attn_tap, want_attn) <= tol
+    assert ref.max_rel(ffn_tap, want_ffn) <= tol
+    assert ref.max_rel(out, ref.block(x, P, H, "gelu", True, T, rnd)) <= tol
+    assert ref.max_rel(out, fused) <= (1e-6 if dt == "fp32" else 2e-2)
+    # the default path keeps the residual stream in the taps
+    blk.forward(xd)
+    assert ref.max_rel(blk.ffn.output.get(), fused) == 0.0
+
+
 @pytest.mark.parametrize("dt", ["bf16", "fp32"])
 @pytest.mark.parametrize("decoder", [True, False])
 def test_attention_fused_matches_unfused_layer(tl, decoder, dt):

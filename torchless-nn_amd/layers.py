@@ -373,9 +373,15 @@ class RMSNorm(Layer):
 
 
 class TransformerBlock(Layer):
-    """Pre-LN block x + MHA(LN1 x), then + FFN(LN2 .) (reference layers.py:444-467). Both
-    residual adds run in the epilogues of the out-projection and second FFN GEMMs, so
-    `attn_block.output` and `ffn.output` hold the residual stream after each add."""
+    """Pre-LN block x + MHA(LN1 x), then + FFN(LN2 .) (reference layers.py:444-467).
+
+    With `fuse_residual` (the default) both residual adds run in the epilogues of the
+    out-projection and second FFN GEMMs, so `attn_block.output` and `ffn.output` hold the
+    residual stream after each add. With `fuse_residual = False` (on the class or one block)
+    the sublayers return their own outputs and the adds are separate launches, as in the
+    reference (layers.py:464-466), so `attn_block.output` is heads @ W_o + b_o and
+    `ffn.output` is act(. W1 + b1) W2 + b2: per-layer taps read what the reference's do."""
+    fuse_residual = True
 
     def __init__(self, embed_dim, context_length, num_heads, activation, decoder=False,
                  attn_dropout_rate=0.0, res_dropout_rate=0.0):
@@ -397,6 +403,12 @@ class TransformerBlock(Layer):
         # each norm launch also pulls the next two products' weights into the device caches
         # (after a forward's 0.8 GB of logits none of them is left there)
         _warm(self.attn_block.qkv_weights, self.attn_block.out_weights)
+        if not self.fuse_residual:
+            y = input + self.attn_block._forward(self.pre_attn_norm.forward(input), None, cache,
+                                                 layer, pos0)
+            _warm(self.ffn.weights1, self.ffn.weights2)
+            self.output = y + self.ffn._forward(self.pre_ffn_norm.forward(y), None)
+            return self.output
         y = self.attn_block._forward(self.pre_attn_norm.forward(input), input, cache, layer, pos0)
         _warm(self.ffn.weights1, self.ffn.weights2)
         self.output = self.ffn._forward(self.pre_ffn_norm.forward(y), residual=y)
