@@ -1837,13 +1837,28 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     return ls.finish("gemm_mfma");
   }
   if (mfma32) {
+    // 128x96 tiles when they take less rounds x width than 128x128 with two workgroups per
+    // CU (both fit twice in LDS): the N = 768 and N = 2304 products of GPT-2 small fill 0.75
+    // and 2.25 rounds of 128x128 tiles but exactly 1 and 3 rounds of 128x96
+    const int64_t slots = 2 * (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
+    auto round_width = [&](int64_t bn) {
+      const int64_t tiles = ((d->M + 127) / 128) * ((d->N + bn - 1) / bn) * batch;
+      return (tiles + slots - 1) / slots * bn;
+    };
+    const bool n96 = round_width(96) < round_width(128);
+    const int bn = n96 ? 96 : 128;
     p.tiles_m = (int)((d->M + 127) / 128);
-    p.tiles_n = (int)((d->N + 127) / 128);
+    p.tiles_n = (int)((d->N + bn - 1) / bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
     LaunchScope ls(ctx, family, flops, bytes);
-    if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
-    else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    if (n96) {
+      if (f32out) gemm_mfma_f32_kernel<float, 128, 96, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+      else gemm_mfma_f32_kernel<bf16_t, 128, 96, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    } else {
+      if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+      else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    }
     return ls.finish("gemm_mfma_f32");
   }
   if (mfma32_small) {
