@@ -1069,24 +1069,28 @@ static void launch_short(int nkh, dim3 grid, int threads, hipStream_t st, const 
 // fp32 attention (the reference's FLOAT_TYPE, backend.py:24; layers.py:286-304) on the
 // fp32 matrix cores, v_mfma_f32_16x16x4f32: fp32 products and sums, so the scores, the
 // softmax and P.V keep full fp32 precision. The structure is attention_fwd_kernel's: 4
-// waves x 16 query rows, 64-key chunks of K and V^T staged in LDS (registers -> LDS, double
+// waves x 16 query rows, BKV-key chunks of K and V^T staged in LDS (registers -> LDS, double
 // buffered), S^T = K Q^T so a lane holds 4 keys of one query row, online softmax with lazy
 // rescaling, O^T += V^T P^T, causal query blocks paired so workgroups carry equal work.
+// Chunks of 32 keys keep a workgroup's LDS at 32 KB (head dim 64), so three workgroups fit a
+// CU and GPT-2's 768 paired blocks run as one round; 64-key chunks (64 KB) fit two, and the
+// second half-round ran at one wave per SIMD.
 // A 16x16x4 MFMA takes one element per lane per operand. Q.K sums over d in any order, so
 // lane group fg covers the contiguous d range [fg D/4, (fg + 1) D/4) one d per MFMA (Q and K
 // read as 16-byte chunks); P.V step u = (key tile j, v) takes key 16 j + 4 fg + v from lane
 // group fg, which is exactly the probability that lane holds, and reads V^T[d][16 j + 4 fg
 // .. + 3] as one 16-byte chunk. LDS rows are stored with their 16-byte chunks XOR-swizzled
 // by row so the 16 rows of a fragment read hit distinct banks.
-template <int D>
+template <int D, int BKV>
 __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
-  constexpr int BKV = 64;
+  constexpr int NJ = BKV / 16;       // 16-key tiles per chunk
+  constexpr int VCH = BKV / 4;       // 16-byte chunks per V^T row
   constexpr int KCH = D / 4;          // 16-byte chunks per K row
   constexpr int KSW = KCH - 1;        // swizzle mask of a K row (KCH is a power of two)
   constexpr int DQ = D / 4;           // d values per lane group (one per MFMA)
   constexpr int DT = D / 16;          // 16-row d tiles of the output
   constexpr int K_LOADS = BKV * KCH / 256;
-  constexpr int V_LOADS = D * 16 / 256;  // V^T chunk: D rows x 16 chunks
+  constexpr int V_LOADS = D * VCH / 256;  // V^T chunk: D rows x VCH chunks
   static_assert(K_LOADS >= 1 && V_LOADS >= 1, "head_dim too small");
   __shared__ __attribute__((aligned(16))) float Ks[2][BKV * D];
   __shared__ __attribute__((aligned(16))) float Vs[2][D * BKV];
@@ -1137,7 +1141,7 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
 #pragma unroll
       for (int i = 0; i < V_LOADS; ++i) {
         // positions past Tk (capacity padding, never written) are zeroed: 0 * NaN is not 0
-        const int idx = i * 256 + tid, r = idx >> 4, c = idx & 15;
+        const int idx = i * 256 + tid, r = idx / VCH, c = idx % VCH;
         const int kv = kv0 + 4 * c;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
         if (kv < p.Tk) {
@@ -1157,8 +1161,8 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
       }
 #pragma unroll
       for (int i = 0; i < V_LOADS; ++i) {
-        const int idx = i * 256 + tid, r = idx >> 4, c = idx & 15;
-        *reinterpret_cast<f32x4*>(&Vs[buf][r * BKV + ((c ^ (r & 15)) << 2)]) = rv[i];
+        const int idx = i * 256 + tid, r = idx / VCH, c = idx % VCH;
+        *reinterpret_cast<f32x4*>(&Vs[buf][r * BKV + ((c ^ (r & (VCH - 1))) << 2)]) = rv[i];
       }
     };
 
@@ -1176,9 +1180,9 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
       const int kv0 = ch * BKV;
       if (ch + 1 < nchunks) load_chunk_regs(kv0 + BKV);
 
-      f32x4 s[4];
+      f32x4 s[NJ];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
         const int r = j * 16 + fr;
 #pragma unroll
@@ -1195,16 +1199,16 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
                         (!p.causal || (int64_t)(kv0 + BKV - 1) <= (int64_t)q0 + p.offset);
       if (full) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) mx = fmaxf(mx, s[j][v]);
       } else {
         // key kv0 + 16 j + 4 fg + v is visible when 16 j + v <= lim (one per-lane limit)
         const int lim = (int)max(min(min((int64_t)p.Tk - 1, p.causal ? (int64_t)qpos + p.offset
                                                                     : (int64_t)p.Tk - 1) -
-                                         kv0 - 4 * fg, (int64_t)64), (int64_t)-1);
+                                         kv0 - 4 * fg, (int64_t)BKV), (int64_t)-1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             s[j][v] = j * 16 + v <= lim ? s[j][v] : -INFINITY;
@@ -1227,7 +1231,7 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
       }
       const float m_ref = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[j][v], p.scale_log2, -m_ref));
@@ -1239,9 +1243,9 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
       for (int t = 0; t < DT; ++t) {
         const int r = t * 16 + fr;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           const int cc = 4 * j + fg;
-          const f32x4 vf = *reinterpret_cast<const f32x4*>(&Vs[cur][r * BKV + ((cc ^ (r & 15)) << 2)]);
+          const f32x4 vf = *reinterpret_cast<const f32x4*>(&Vs[cur][r * BKV + ((cc ^ (r & (VCH - 1))) << 2)]);
 #pragma unroll
           for (int v = 0; v < 4; ++v)
             o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[v], s[j][v], o[t], 0, 0, 0);
@@ -1347,9 +1351,9 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     const int64_t nqb = (seq_q + 63) / 64;
     const dim3 grid((unsigned)(causal ? (nqb + 1) / 2 : nqb), (unsigned)(batch * n_heads_q));
     switch (head_dim) {
-      case 32: attention_fwd_f32_kernel<32><<<grid, 256, 0, ctx->stream>>>(p); break;
-      case 64: attention_fwd_f32_kernel<64><<<grid, 256, 0, ctx->stream>>>(p); break;
-      default: attention_fwd_f32_kernel<128><<<grid, 256, 0, ctx->stream>>>(p); break;
+      case 32: attention_fwd_f32_kernel<32, 32><<<grid, 256, 0, ctx->stream>>>(p); break;
+      case 64: attention_fwd_f32_kernel<64, 32><<<grid, 256, 0, ctx->stream>>>(p); break;
+      default: attention_fwd_f32_kernel<128, 32><<<grid, 256, 0, ctx->stream>>>(p); break;
     }
     return ls.finish("attention_fwd_f32");
   }
