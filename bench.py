@@ -231,6 +231,16 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128, graph=True):
         model.forward(ids, cache, 0, last_only=True)
     e1.record()
     prefill_last_ms = e0.elapsed_ms(e1) / prefill_reps
+    # per-family kernel time of one more full prefill (HIP events around every launch)
+    xp.kprof_reset()
+    xp.kprof_enable(list(xp.KFAMILY))
+    logits = model.forward(ids, cache, 0)
+    xp.synchronize()
+    pfam = {f: xp.kprof_query(f) for f in xp.KFAMILY}
+    xp.kprof_enable([])
+    prefill_breakdown = {f: {"ms": round(r["ms"], 3), "launches": r["launches"],
+                             "tflops": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 1) if r["flops"] else None}
+                         for f, r in pfam.items() if r["launches"]}
     C, F, V, L = cfg["d"], cfg["ffn"], cfg["vocab"], cfg["layers"]
     Hq, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
     M = B * T
@@ -305,6 +315,7 @@ def gemma_bench(xp, prefill_reps=3, decode_steps=128, graph=True):
         "prefill_tokens_per_s": round(M / (prefill_ms * 1e-3), 1),
         "prefill_tflops": round(prefill_flops / (prefill_ms * 1e-3) / 1e12, 1),
         "prefill_flops": prefill_flops,
+        "prefill_kernel_breakdown": prefill_breakdown,
         "decode_steps": decode_steps,
         "decode_ms_per_step": round(decode_ms, 4),
         "decode_wall_ms_per_step": round(wall, 4),
