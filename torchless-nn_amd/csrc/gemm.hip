@@ -1837,15 +1837,17 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     return ls.finish("gemm_mfma");
   }
   if (mfma32) {
-    // 128x96 tiles when they take less rounds x width than 128x128 with two workgroups per
-    // CU (both fit twice in LDS): the N = 768 and N = 2304 products of GPT-2 small fill 0.75
-    // and 2.25 rounds of 128x128 tiles but exactly 1 and 3 rounds of 128x96
+    // 128x96 tiles when they take at least 10% less rounds x width than 128x128 with two
+    // workgroups per CU (both fit twice in LDS): the N = 768 and N = 2304 products of GPT-2
+    // small fill 0.75 and 2.25 rounds of 128x128 tiles but exactly 1 and 3 rounds of 128x96.
+    // With many rounds the narrower tile's lower flops per loaded byte costs more than the
+    // quantisation it saves (LM head, 50 rounds: 5289 us on 128x128, 5500 us on 128x96).
     const int64_t slots = 2 * (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
     auto round_width = [&](int64_t bn) {
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + bn - 1) / bn) * batch;
       return (tiles + slots - 1) / slots * bn;
     };
-    const bool n96 = round_width(96) < round_width(128);
+    const bool n96 = round_width(96) * 10 <= round_width(128) * 9;
     const int bn = n96 ? 96 : 128;
     p.tiles_m = (int)((d->M + 127) / 128);
     p.tiles_n = (int)((d->N + bn - 1) / bn);
