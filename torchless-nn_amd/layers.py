@@ -4,10 +4,11 @@ Same classes, constructor arguments, parameter lists and `forward(x) -> y` contr
 reference; every forward is a handful of libtl kernel launches on one HIP stream:
 
   Dense / FFN / projections -> tl_gemm with bias, activation and residual epilogues
-  MultiHeadAttention        -> QKV GEMM that scatters head-major Q, K and V^T, then (bf16)
-                               one fused attention kernel that writes merged heads, or
-                               (fp32 and shapes it does not take) the batched QK^T GEMM,
-                               the causal softmax row kernel and the batched P.V GEMM
+  MultiHeadAttention        -> QKV GEMM that scatters head-major Q, K and V^T, then one
+                               fused attention kernel (bf16, or fp32 on the fp32 matrix
+                               cores) that writes merged heads, or (shapes it does not take,
+                               `fused = False`) the batched QK^T GEMM, the causal softmax
+                               row kernel and the batched P.V GEMM
   LayerNorm / RMSNorm       -> one row kernel each
 
 The MFMA GEMMs read a weight in a K-contiguous copy ([out, in]) that is packed on the
