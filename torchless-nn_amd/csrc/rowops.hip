@@ -282,7 +282,7 @@ __global__ __launch_bounds__(256) void norm_wave_kernel(const T* __restrict__ x,
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int col = (c * LPR + lane) * VW;
-    raw[c] = load16<NT>(xr + (col < cols ? col : 0));
+    raw[c] = load16<NT && sizeof(T) == 4>(xr + (col < cols ? col : 0));
   }
   if constexpr (PRE) {
 #pragma unroll
@@ -425,8 +425,9 @@ __device__ __forceinline__ uint4 load_raw_partial(const T* p, int n) {
 // thread: a per-element z / temp compiles to a full-precision division sequence (about ten
 // VALU instructions per element), and a short bf16 row is bound by VALU issue, not HBM.
 // Masked elements hold -inf, so 2^((-inf - max) k) = 0 needs no per-element select.
-// NT: row loads and stores are non-temporal (set by the host for large fp32 tensors).
-template <typename T, int CH, bool CAUSAL, bool TAIL, bool NT, int LPR>
+// NTM: bit 0 makes the row loads non-temporal, bit 1 the stores (set by the host for
+// tensors far larger than the caches: both for fp32, stores only for causal bf16).
+template <typename T, int CH, bool CAUSAL, bool TAIL, int NTM, int LPR>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__ x,
                                                            T* __restrict__ y, int64_t rows,
                                                            int cols, int64_t ldx, int64_t ldy,
@@ -450,7 +451,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
     if (TAIL && col < valid && col + VW > cols)
       raw[c] = load_raw_partial(xr + col, cols - col);
     else
-      raw[c] = load16<NT>(xr + (col < valid ? col : 0));
+      raw[c] = load16<(NTM & 1) != 0>(xr + (col < valid ? col : 0));
   }
   float v[CH][VW];
   float mx = -INFINITY;
@@ -485,7 +486,7 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const T* __restrict__
 #pragma unroll
     for (int e = 0; e < VW; ++e) o[e] = v[c][e] * rs;
     if (col + VW <= cols) {
-      store16<NT>(yr + col, Elem<T>::pack(o));
+      store16<(NTM & 2) != 0>(yr + col, Elem<T>::pack(o));
     } else if (TAIL && col < cols) {
       for (int e = 0; e < VW && col + e < cols; ++e) Elem<T>::store(yr + col + e, o[e]);
     }
@@ -995,7 +996,10 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
   const int64_t cchunks = cols / VW;  // 16-byte chunks per row
   // Rows far larger than the caches (here >= 64 MiB in) are streamed non-temporally: bf16
   // LayerNorm over [16384, 4096] 5.26 -> 5.81 TB/s with gamma/beta loaded early, fp32
-  // 5.30 -> 5.75 TB/s. Smaller tensors keep cached stores, since the next kernel reads them.
+  // 5.30 -> 5.75 TB/s. For bf16 only the stores are non-temporal and the loads stay cached
+  // (LayerNorm 5.72 -> 6.57, RMSNorm 5.94 -> 6.57 TB/s, three same-box pairs); fp32 keeps
+  // both (cached loads measured 2% slower). Smaller tensors keep cached stores, since the
+  // next kernel reads them.
   const bool nt = rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
   const bool pf = ctx->prefetch.lines[0] || ctx->prefetch.lines[1] || ctx->prefetch.lines[2] ||
                   ctx->prefetch.lines[3];
@@ -1041,7 +1045,11 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
   const int64_t chunks = (cols + VW - 1) / VW;
   // Non-temporal row access for fp32 tensors far larger than the caches (causal fp32
   // [8, 12, 1024, 1024]: 5.04 -> 5.41 TB/s in a probe; the same change slowed bf16 rows).
-  const bool nt = sizeof(T) == 4 && rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
+  // Causal bf16 rows of such tensors store non-temporally and load cached (5.33 -> 5.43
+  // TB/s, three same-box pairs); fp32 rows with cached loads measured no faster.
+  const bool big = rows * ldx * (int64_t)sizeof(T) >= ((int64_t)64 << 20);
+  const bool nt = sizeof(T) == 4 && big;
+  const bool nt_store = sizeof(T) == 2 && CAUSAL && big;
   auto wave = [&](auto ch_tag, auto lpr_tag) {
     constexpr int CH = decltype(ch_tag)::value, LPR = decltype(lpr_tag)::value;
     auto go = [&](auto tail_tag, auto nt_tag) {
@@ -1050,9 +1058,10 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
           <<<(unsigned)((rows + 256 / LPR - 1) / (256 / LPR)), 256, 0, ctx->stream>>>(
               (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, temp, period, offset);
     };
-    if (cols % VW != 0) go(std::true_type(), std::false_type());
-    else if (nt) go(std::false_type(), std::true_type());
-    else go(std::false_type(), std::false_type());
+    if (cols % VW != 0) go(std::true_type(), std::integral_constant<int, 0>());
+    else if (nt) go(std::false_type(), std::integral_constant<int, 3>());
+    else if (nt_store) go(std::false_type(), std::integral_constant<int, 2>());
+    else go(std::false_type(), std::integral_constant<int, 0>());
   };
   // Long rows: (threads, keep e in registers) by TL_SOFTMAX_LONG_CFG (1: 1024, 2: 1024 kept,
   // 3: 512, 4: 512 kept, with cached loads and stores). By default (5) 512 threads for rows
