@@ -413,7 +413,8 @@ GEMM_CASES = [  # M, N, K (fp32: few tiles with K >= 256 split K over workgroups
     (1, 1, 8), (5, 7, 8), (64, 64, 64), (130, 70, 72), (128, 128, 768), (257, 300, 136),
     (512, 2304, 768), (1000, 65, 128), (8, 50257, 64), (512, 128, 512), (300, 70, 1000),
     (64, 64, 2000), (2048, 1040, 260),  # fp32 with B [N, K]: the fp32 matrix-core kernel
-    (4096, 700, 516),  # fp32: 128x96 tiles (1 round at 2 per CU, 128x128 would also take 1)
+    (4096, 700, 516),  # fp32: 128x64 tiles (one round at 3 per CU, as 128x128 would take)
+    (3072, 4096, 132),  # fp32: 128x128 tiles (one round; 128x64 would take two), K tail of 4
 ]
 
 

@@ -783,15 +783,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_kernel(GemmParams p)
 // K indices 4c + q of their chunks c; A and B use the same assignment, which covers each K
 // index of the step once. B is the first MFMA operand, so a lane's four results are four
 // consecutive output columns of one row, the layout epilogue4 stores.
-template <typename TO, int BM, int BN, int WGM, int WGN>
+template <typename TO, int BM, int BN, int WGM, int WGN, int BK = 32>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_f32_kernel(GemmParams p) {
   constexpr int NT = 64 * WGM * WGN;
-  constexpr int BK = 32;                   // fp32 elements of K per step: 8 chunks of 16 B
+  constexpr int CPR = BK / 4;              // 16-byte chunks per row of a K step (8 or 4)
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 16, TN = WN / 16;
-  constexpr int RPP = NT / 8;              // tile rows one load pass covers
+  constexpr int RPP = NT / CPR;            // tile rows one load pass covers
   constexpr int A_CH = BM / RPP, B_CH = BN / RPP;
-  static_assert(BM % RPP == 0 && BN % RPP == 0 && RPP % 8 == 0, "bad tile/thread split");
+  static_assert(BK == 32 || BK == 16, "K step of 16 or 32 fp32 elements");
+  static_assert(BM % RPP == 0 && BN % RPP == 0 && RPP % CPR == 0, "bad tile/thread split");
   static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA tile");
   __shared__ __attribute__((aligned(16))) float As[2][BM * BK];
   __shared__ __attribute__((aligned(16))) float Bs[2][BN * BK];
@@ -807,8 +808,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_f32_kernel(GemmParam
 
   const float* Ab = (const float*)p.A + zo * p.sa_o + zi * p.sa_i + m0 * p.lda;
   const float* Bb = (const float*)p.B + zo * p.sb_o + zi * p.sb_i + n0 * p.ldb;
-  const int lr = tid >> 3, lc = tid & 7;
-  const int slot = lr * BK + ((lc ^ (lr & 7)) << 2);
+  const int lr = tid / CPR, lc = tid % CPR;
+  const int slot = lr * BK + ((lc ^ (lr & (CPR - 1))) << 2);
   uint32_t a_off[A_CH], b_off[B_CH];
   {
     // rows past M or N are clamped to the last row: computed, never stored
@@ -861,8 +862,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_mfma_f32_kernel(GemmParam
     const int cur = kt & 1;
     if (kt + 1 < nk) load_tile((int64_t)(kt + 1) * BK);
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int sw = ((s * 4 + fc) ^ (fr & 7)) << 2;
+    for (int s = 0; s < BK / 16; ++s) {
+      const int sw = ((s * 4 + fc) ^ (fr & (CPR - 1))) << 2;
       f32x4 af[TM], bfr[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const f32x4*>(&As[cur][a_frag + i * 16 * BK + sw]);
@@ -1837,29 +1838,34 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     return ls.finish("gemm_mfma");
   }
   if (mfma32) {
-    // 128x96 tiles when they take at least 10% less rounds x width than 128x128 with two
-    // workgroups per CU (both fit twice in LDS): the N = 768 and N = 2304 products of GPT-2
-    // small fill 0.75 and 2.25 rounds of 128x128 tiles but exactly 1 and 3 rounds of 128x96.
-    // With many rounds the narrower tile's lower flops per loaded byte costs more than the
-    // quantisation it saves (LM head, 50 rounds: 5289 us on 128x128, 5500 us on 128x96).
-    const int64_t slots = 2 * (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
+    // 16-wide K steps: 32 KB of LDS (128x128), so three workgroups share a CU (registers
+    // allow three waves per SIMD), and tiles 128 or 64 wide (a load pass covers 64 rows),
+    // whichever takes less rounds x width over 3 x CUs slots, 128 unless 64 saves >= 10%
+    const int64_t slots = 3 * (int64_t)(ctx->num_cus > 0 ? ctx->num_cus : 256);
     auto round_width = [&](int64_t bn) {
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + bn - 1) / bn) * batch;
       return (tiles + slots - 1) / slots * bn;
     };
-    const bool n96 = round_width(96) * 10 <= round_width(128) * 9;
-    const int bn = n96 ? 96 : 128;
+    int bn = 128;
+    int64_t best = round_width(128);
+    for (int c : {64}) {
+      const int64_t w = round_width(c);
+      if (w * 10 <= round_width(128) * 9 && w < best) {
+        best = w;
+        bn = c;
+      }
+    }
     p.tiles_m = (int)((d->M + 127) / 128);
     p.tiles_n = (int)((d->N + bn - 1) / bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
     LaunchScope ls(ctx, family, flops, bytes);
-    if (n96) {
-      if (f32out) gemm_mfma_f32_kernel<float, 128, 96, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
-      else gemm_mfma_f32_kernel<bf16_t, 128, 96, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+    if (bn == 64) {
+      if (f32out) gemm_mfma_f32_kernel<float, 128, 64, 2, 2, 16><<<grid, 256, 0, ctx->stream>>>(p);
+      else gemm_mfma_f32_kernel<bf16_t, 128, 64, 2, 2, 16><<<grid, 256, 0, ctx->stream>>>(p);
     } else {
-      if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
-      else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2><<<grid, 256, 0, ctx->stream>>>(p);
+      if (f32out) gemm_mfma_f32_kernel<float, 128, 128, 2, 2, 16><<<grid, 256, 0, ctx->stream>>>(p);
+      else gemm_mfma_f32_kernel<bf16_t, 128, 128, 2, 2, 16><<<grid, 256, 0, ctx->stream>>>(p);
     }
     return ls.finish("gemm_mfma_f32");
   }
