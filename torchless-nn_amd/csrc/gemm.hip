@@ -1846,15 +1846,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + bn - 1) / bn) * batch;
       return (tiles + slots - 1) / slots * bn;
     };
-    int bn = 128;
-    int64_t best = round_width(128);
-    for (int c : {64}) {
-      const int64_t w = round_width(c);
-      if (w * 10 <= round_width(128) * 9 && w < best) {
-        best = w;
-        bn = c;
-      }
-    }
+    const int bn = round_width(64) * 10 <= round_width(128) * 9 ? 64 : 128;
     p.tiles_m = (int)((d->M + 127) / 128);
     p.tiles_n = (int)((d->N + bn - 1) / bn);
     TL_REQUIRE((int64_t)p.tiles_m * p.tiles_n < 0x7fffffff, "too many tiles");
