@@ -164,6 +164,9 @@ int tl_malloc(tl_ctx* ctx, size_t bytes, void** ptr);
 int tl_free(tl_ctx* ctx, void* ptr);
 int tl_empty_cache(tl_ctx* ctx);
 int tl_mem_stats(tl_ctx* ctx, size_t* bytes_in_use, size_t* bytes_cached);
+/* Size of the context's grow-only workspace (the split reductions' partial results), 0 until
+ * a call first needs it. No reference counterpart (CuPy's pool has no such buffer). */
+int tl_workspace_bytes(tl_ctx* ctx, size_t* bytes);
 /* Host<->device copies. Replace `xp.array(host)` (reference network.py:117-118, 152-153) and
  * `.get()` (reference demo.ipynb:1535). h2d returns once the host buffer may be reused: up to
  * 64 MiB it is copied into a pinned staging buffer and the device copy is queued behind the
@@ -186,7 +189,8 @@ int tl_sync(tl_ctx* ctx);
  * next tl_layernorm_fwd / tl_rmsnorm_fwd on this context also reads, one word per 128-byte
  * line, so a weight that the product after the norm reads arrives from the device caches
  * instead of HBM. Advisory: results do not change, the values read are discarded, and the
- * list is cleared by that launch. The region must lie inside one live tl_malloc block
+ * list is cleared by that launch. A norm over too few rows to give every CU a workgroup (a
+ * decode step) ignores the list (and still clears it). The region must lie inside one live tl_malloc block
  * (TL_ERR_INVALID otherwise); freeing that block drops it from the list. In a captured graph
  * the region is read on every replay, so it must stay allocated while the graph lives. */
 int tl_prefetch_hint(tl_ctx* ctx, const void* ptr, int64_t bytes);

@@ -22,9 +22,18 @@ Pinning (how each function is checked, in tests/test_oracle.py and tests/golden/
   mqa              without RoPE and with Hkv = Hq equals mha (zero biases, [Q|K|V]
                    columns), itself pinned; Hkv = 1 equals Hkv = Hq with the key/value
                    weights replicated per head (pins the head -> kv-head map); a cached
-                   two-call run equals one call over the whole sequence
-  gemma_forward    incremental (cached) logits equal recomputed ones; composition of the
-                   pinned pieces above; gemma_greedy ids are argmax of its own rows
+                   two-call run equals one call over the whole sequence; an uncached call
+                   with every position shifted by the same offset gives the same output
+                   (RoPE on queries and keys alike), which RoPE on the queries only fails
+  gemma_forward    golden fixture tests/golden/gemma_tiny.npz: brute-force float64 loops of
+                   the whole decoder (sqrt(C)-scaled gather, (1 + gain) RMSNorms with eps
+                   1e-6, 4 query heads on one key/value head with rotate-half RoPE on
+                   queries and keys at absolute positions, GeGLU, both residuals, final
+                   norm, tied head) written independently of this module, whole-sequence
+                   and as cached calls at positions 0, 7 and 8; planted mistakes (a dropped
+                   residual, a gain without its 1 + offset, no sqrt(C) scale, RoPE on the
+                   queries only, a cached call rotated from position 0) each fail it;
+                   gemma_greedy ids are argmax of its own rows
   patchify         brute-force index loops (token i*(W/p1)+j, feature (a*p1+c2)*C+ch)
   vit_projector    brute-force loops over the same formula at a tiny shape
   vit_forward      golden fixture tests/golden/vit_tiny.npz: brute-force float64 loops of

@@ -183,6 +183,97 @@ def vit_brute(images, P, cfg):
     return np.array(head_all), np.array(logits_all), np.array(probs_all)
 
 
+# ---- Gemma-style decoder (BASELINE config 5's architecture; no reference counterpart) ----
+GEMMA_BLOCK_KEYS = ("g1", "wqkv", "wo", "g2", "wg", "wu", "wd")
+
+
+def rms_rows(x, g, eps=1e-6):
+    """RMSNorm (Zhang & Sennrich 2019) with Gemma's (1 + gamma) gain and eps 1e-6:
+    x / sqrt(mean(x^2) + eps) * (1 + gamma[c])."""
+    out = []
+    for row in x:
+        inv = 1.0 / math.sqrt(sum(v * v for v in row) / len(row) + eps)
+        out.append([row[c] * inv * (1.0 + g[c]) for c in range(len(row))])
+    return out
+
+
+def rope_vec(v, pos, base):
+    """Rotary position embedding, rotate-half pairing (Su et al. 2021, as Gemma pairs it):
+    element i and element i + D/2 form one 2-vector, rotated by the angle
+    pos * base^(-2i/D)."""
+    D = len(v)
+    h = D // 2
+    out = list(v)
+    for i in range(h):
+        ang = pos * base ** (-2.0 * i / D)
+        c, s = math.cos(ang), math.sin(ang)
+        out[i] = v[i] * c - v[i + h] * s
+        out[i + h] = v[i + h] * c + v[i] * s
+    return out
+
+
+def gemma_params(cfg, seed, scale):
+    """Seeded fill in the decoder's layer order: the tied table [V, C], then per block [norm-1
+    gain [C], Wqkv [C, (Hq + 2 Hkv) D] with columns [Q | K | V], Wo [Hq D, C], norm-2 gain
+    [C], Wgate [C, F], Wup [C, F], Wdown [F, C]], then the final-norm gain [C]. N(0,1)*scale
+    for every tensor, gains included (they scale by 1 + gain)."""
+    V, C, L, F = cfg["vocab"], cfg["d"], cfg["layers"], cfg["ffn"]
+    Hq, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["head_dim"]
+    shapes = [("table", (V, C))]
+    for l in range(L):
+        shapes += [(f"b{l}.{k}", s) for k, s in zip(GEMMA_BLOCK_KEYS, [
+            (C,), (C, (Hq + 2 * Hkv) * D), (Hq * D, C), (C,), (C, F), (C, F), (F, C)])]
+    shapes += [("normf.g", (C,))]
+    rng = np.random.default_rng(seed)
+    P = {n: rng.standard_normal(s, dtype=F32) * F32(scale) for n, s in shapes}
+    return [n for n, _ in shapes], P
+
+
+def gemma_brute(ids, P, cfg):
+    """The Gemma-style decoder in float64 loops, per sequence: embedding row times sqrt(C);
+    L pre-norm blocks, each x + Wo(attention(RoPE(q), RoPE(k), v) of RMSNorm(x)) then
+    y + Wdown(gelu(RMSNorm(y) Wgate) * (RMSNorm(y) Wup)); query head h reads key/value head
+    h // (Hq / Hkv); queries AND keys rotated at their absolute positions 0..T-1; causal
+    softmax of q.k / sqrt(D); no biases; final RMSNorm; tied head logits = x . table[v].
+    The GeLU is the reference's tanh form (activations.py:24-28); the causal rows are those
+    of layers.py:293-304."""
+    C, Hq, Hkv, D, L = cfg["d"], cfg["heads"], cfg["kv_heads"], cfg["head_dim"], cfg["layers"]
+    base, grp = cfg["rope_base"], Hq // Hkv
+    out = []
+    for seq in ids:
+        T = len(seq)
+        x = [[P["table"][tok][c] * math.sqrt(C) for c in range(C)] for tok in seq]
+        for l in range(L):
+            g = lambda k: P[f"b{l}.{k}"]
+            qkv = [matvec(r, g("wqkv")) for r in rms_rows(x, g("g1"))]
+            q = [[rope_vec(qkv[t][h * D:(h + 1) * D], t, base) for h in range(Hq)]
+                 for t in range(T)]
+            k = [[rope_vec(qkv[t][(Hq + j) * D:(Hq + j + 1) * D], t, base) for j in range(Hkv)]
+                 for t in range(T)]
+            v = [[qkv[t][(Hq + Hkv + j) * D:(Hq + Hkv + j + 1) * D] for j in range(Hkv)]
+                 for t in range(T)]
+            heads = [[0.0] * (Hq * D) for _ in range(T)]
+            for h in range(Hq):
+                j = h // grp
+                for i in range(T):
+                    s = [sum(q[i][h][d] * k[t][j][d] for d in range(D)) / math.sqrt(D)
+                         for t in range(i + 1)]
+                    p = softmax_row(s)
+                    for d in range(D):
+                        heads[i][h * D + d] = sum(p[t] * v[t][j][d] for t in range(i + 1))
+            a = [matvec(r, g("wo")) for r in heads]
+            y = [[x[t][c] + a[t][c] for c in range(C)] for t in range(T)]
+            yn = rms_rows(y, g("g2"))
+            hid = [[gelu(gv) * uv for gv, uv in zip(matvec(r, g("wg")), matvec(r, g("wu")))]
+                   for r in yn]
+            f = [matvec(r, g("wd")) for r in hid]
+            x = [[y[t][c] + f[t][c] for c in range(C)] for t in range(T)]
+        x = rms_rows(x, P["normf.g"])
+        out.append([[sum(r[c] * P["table"][w][c] for c in range(C)) for w in range(cfg["vocab"])]
+                    for r in x])
+    return np.array(out)
+
+
 def main():
     # tiny GPT: scale 0.5 so that attention and GeLU are far from linear
     cfg = dict(vocab=11, ctx=6, layers=2, d=8, heads=2, act="gelu")
@@ -220,6 +311,19 @@ def main():
              probs=probs, param_order=np.array(names),
              **{"cfg_" + k: np.array(v) for k, v in vcfg.items()},
              **{"p_" + k: v for k, v in VP.items()})
+    # tiny Gemma-style decoder: 4 query heads sharing one key/value head, head width 32,
+    # GeGLU, (1 + gain) RMSNorms; scale 0.3 so that the gains, RoPE and GeGLU all matter;
+    # 12 positions, so a cached run (prefill 7, then 1, then 4 at positions 7.. and 8..)
+    # reads its rows from the same logits
+    gcfg = dict(vocab=97, ctx=64, layers=2, d=64, heads=4, kv_heads=1, head_dim=32, ffn=96,
+                rope_base=10000.0)
+    gnames, GP = gemma_params(gcfg, seed=13, scale=0.3)
+    gids = np.random.default_rng(14).integers(0, gcfg["vocab"], (2, 12))
+    glogits = gemma_brute(gids.tolist(), {k: v.astype(np.float64).tolist() for k, v in GP.items()},
+                          gcfg)
+    np.savez(os.path.join(HERE, "gemma_tiny.npz"), ids=gids.astype(np.int64), logits=glogits,
+             param_order=np.array(gnames), **{"cfg_" + k: np.array(v) for k, v in gcfg.items()},
+             **{"p_" + k: v for k, v in GP.items()})
     print("fixtures written to", HERE)
 
 

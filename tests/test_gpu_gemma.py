@@ -360,3 +360,60 @@ def test_gemma_config5_full_shape_decode_bf16(tl):
     for t in (32, 64, 127):
         fresh = model.last_rows(model.forward(seq[:, :2048 + t])).get()
         assert ref.max_rel(rows[t], fresh) <= 2e-2, t
+
+
+def _golden_gemma(tl):
+    """GemmaDecoder (fp32) holding the parameters of tests/golden/gemma_tiny.npz, whose
+    logits were written by brute-force float64 loops independent of the oracle."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "gemma_tiny.npz"))
+    cfg = {k[4:]: z[k].item() for k in z.files if k.startswith("cfg_")}
+    model = tl["gemma"].build_gemma(cfg, "fp32")
+    params = [p for layer in model.layers for p in layer.parameters]
+    names = [str(n) for n in z["param_order"]]
+    assert len(names) == len(params)
+    for n, p in zip(names, params):
+        assert tuple(p.shape) == z["p_" + n].shape, n
+        p.set(z["p_" + n])
+    return z, model
+
+
+def test_gemma_tiny_golden_fp32(tl):
+    """The fp32 decoder (sqrt(C)-scaled gather, (1 + gain) RMSNorms, 4 query heads on one
+    key/value head with RoPE on queries and keys, GeGLU, residuals, final norm, tied head)
+    against the float64 fixture at 1e-5: a whole-sequence prefill, with device argmax ids
+    equal to the fixture's, then the same 12 positions as a cached run (7, then 1 at
+    position 7, then 4 at positions 8..11)."""
+    xp = tl["xp"]
+    z, model = _golden_gemma(tl)
+    ids, want = z["ids"], z["logits"]
+    got = model.forward(ids).get()
+    assert ref.max_rel(got, want) <= 1e-5
+    assert np.array_equal(xp.argmax(model.back.output).get(), np.argmax(want, -1))
+    cache = model.new_cache(2, 16)
+    parts = [model.forward(ids[:, :7], cache, 0).get(), model.forward(ids[:, 7:8], cache, 7).get(),
+             model.forward(ids[:, 8:], cache, 8).get()]
+    got_c = np.concatenate(parts, 1)
+    assert ref.max_rel(got_c, want) <= 1e-5
+    assert np.array_equal(np.argmax(got_c, -1), np.argmax(want, -1))
+
+
+def test_gemma_config5_all_layers_against_oracle_bf16(tl):
+    """All 18 config-5 layers at full width (d 2048, 8 query heads of 256 on one kv head,
+    FFN 16384, vocab 256000), device-seeded N(0, 0.02) weights, B = 1, T = 256: every
+    position's logits against the oracle on the downloaded parameters at 2e-2, and the
+    device argmax equal to np.argmax of the downloaded logits."""
+    g = tl["gemma"]
+    model = g.build_gemma(g.GEMMA_2B, "bf16")
+    g.seed_gemma(model, 27, 0.02, device=True)
+    ids = np.random.default_rng(28).integers(0, 256000, (1, 256))
+    logits = model.forward(ids)
+    got = logits.get()
+    dev_ids = tl["xp"].argmax(logits).get()
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(dev_ids, np.argmax(got, -1))
+    P = _device_params(model, g.GEMMA_2B)
+    del model, logits
+    want = ref.gemma_forward(ids, P, g.GEMMA_2B, bf16=True)
+    assert ref.max_rel(got, want) <= 2e-2

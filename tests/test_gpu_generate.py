@@ -126,6 +126,34 @@ def test_choice_frequencies_and_candidates(tl):
     assert one.shape == (1, 1) and 10 <= int(one[0, 0].get()) <= 16
 
 
+# Philox stream 1205178 under key 0 gives draw 0 the largest uniform, u = 1 - 2^-24 (found by
+# a CPU search over streams; tests/test_oracle.py checks it with the KAT-pinned generator)
+TOP_STREAM = 1205178
+
+
+def test_choice_never_returns_a_zero_probability_index(tl):
+    """u = 1 - 2^-24 on a row whose last nonzero entries share a 4-entry chunk with two
+    trailing zeros: the chunk walk's running sum (0.73107517 + 0.12442544) + 0.1928604 rounds
+    one ulp below the scanned total 0.73107517 + (0.12442544 + 0.1928604), which is where
+    u * total lands, so no running sum passes it. The draw must be the last nonzero index,
+    as the oracle's float64 cumsum + searchsorted gives, not a trailing zero entry."""
+    xp = tl["xp"]
+    S, a, b = F32(0.73107517), F32(0.12442544), F32(0.1928604)
+    total, walk = F32(S + F32(a + b)), F32(F32(S + a) + b)
+    assert walk < total  # the case this test is about
+    p = np.zeros(4096, F32)  # 1024 chunks of 4 entries: entries 20..23 are chunk 5
+    p[0], p[20], p[21] = S, a, b
+    want, _, _ = ref.sample_categorical(p, ref.sample_uniforms(1, 0, TOP_STREAM))
+    assert want[0] == 21
+    saved = dict(xp._SAMPLER)
+    try:
+        xp._SAMPLER.update(seed=0, stream=TOP_STREAM)
+        got = xp.random.choice(4096, size=1, p=xp.array(p, dtype="fp32")).get()
+    finally:
+        xp._SAMPLER.update(saved)
+    assert got[0] == 21, got
+
+
 def _cdf_interval_ok(p, u, tok, tol=1e-5):
     cdf = np.cumsum(np.asarray(p, dtype=np.float64))
     x = u * cdf[-1]

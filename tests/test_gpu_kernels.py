@@ -993,6 +993,30 @@ def test_attention_decode_split_kv(xp, case):
     assert ref.max_rel(out.get(), want) <= 2e-2, case
 
 
+def test_attention_config5_prefill_shape(xp):
+    """BASELINE config 5's prefill attention at its stated size: B = 4, 8 query heads sharing
+    one key/value head of width 256, T = 2048, causal, key capacity 2056 with NaN in the
+    padding and NaN in the output beforehand (a query block no workgroup writes stays NaN).
+    Every output is finite; batch entries 0 and 3 (all heads, all 2048 rows) against the
+    float64 definition at the bf16 bar."""
+    B, Hq, Hkv, T, D, Lk = 4, 8, 1, 2048, 256, 2056
+    rng = np.random.default_rng(2048 + D)
+    q = ref.round_bf16(rng.standard_normal((B, Hq, T, D)).astype(F32))
+    k = ref.round_bf16(rng.standard_normal((B, Hkv, Lk, D)).astype(F32))
+    vt = ref.round_bf16(rng.standard_normal((B, Hkv, D, Lk)).astype(F32))
+    k[:, :, T:] = np.nan
+    vt[:, :, :, T:] = np.nan
+    out = up(xp, np.full((B, T, Hq * D), np.nan, F32), "bf16")
+    divisor = float(np.float32(np.sqrt(D)))
+    xp.attention(up(xp, q, "bf16"), up(xp, k, "bf16"), up(xp, vt, "bf16"), out, n_heads_q=Hq,
+                 n_heads_kv=Hkv, divisor=divisor, causal=True, seq_k=T)
+    got = out.get()
+    assert np.all(np.isfinite(got))
+    sel = [0, B - 1]
+    want = attention_ref(q[sel], k[sel][:, :, :T], vt[sel][:, :, :, :T], Hq, Hkv, divisor, True, 0)
+    assert ref.max_rel(got[sel], want) <= 2e-2
+
+
 def test_attention_fused_rejects_unsupported(xp):
     q = xp.empty((1, 1, 12, 64), "bf16").fill(0)
     with pytest.raises(xp.TLError):
@@ -1013,14 +1037,20 @@ def test_attention_fused_rejects_unsupported(xp):
     (2, 3, 3, 65, 65, 72, False, 0),        # ViT-like: 65 keys in a capacity of 72 (NaN pad)
     (2, 8, 1, 40, 96, 104, True, 56),       # one shared kv head, queries at an offset
     (2, 4, 2, 1, 77, 80, True, 76),         # a decode step
-    (8, 12, 12, 1024, 1024, 1024, True, 0),  # the GPT-2-small shape (D = 64 is config 3)
 ])
 def test_attention_fused_f32(xp, D, case):
     """fp32 attention on the fp32 matrix cores (the reference's FLOAT_TYPE) against the
     float64 definition at the fp32 bar, with NaN in the key/value capacity padding."""
+    _attention_f32_case(xp, D, case)
+
+
+def test_attention_fused_f32_gpt2_shape(xp):
+    """The GPT-2-small shape (B 8, 12 heads, T 1024) at its own head dim 64 in fp32."""
+    _attention_f32_case(xp, 64, (8, 12, 12, 1024, 1024, 1024, True, 0))
+
+
+def _attention_f32_case(xp, D, case):
     B, Hq, Hkv, Tq, Tk, Lk, causal, offset = case
-    if B * Hq * Tq > 20000 and D != 64:
-        pytest.skip("the GPT-2 shape runs at its own head dim only")
     rng = np.random.default_rng(Tq + Tk + D)
     q = rng.standard_normal((B, Hq, Tq, D)).astype(F32)
     k = rng.standard_normal((B, Hkv, Lk, D)).astype(F32)

@@ -240,6 +240,7 @@ def test_gpt2_small_full_shape_bf16(tl):
     agree = np.mean(ids_logits == ids_probs)
     assert agree > 0.99, agree
     full = logits.get()
+    assert np.array_equal(ids_logits, np.argmax(full, -1))  # device argmax, bit-exact
     want_p, want_l = ref.gpt_forward(ids[[0, 7]], ref.gpt_params(cfg, 1, bf16=True), cfg,
                                      bf16=True, return_logits=True)
     assert ref.max_rel(full[0], want_l[0]) <= 2e-2

@@ -494,3 +494,10 @@ def test_vit_head_brute_force():
             assert abs(float(got[n, o]) - want) < 1e-5 * (1 + abs(want))
             other = sum(float(x[n, 1, k]) * float(w[k, o]) for k in range(5)) + float(b[o])
             assert abs(float(got[n, o]) - other) > 1e-3  # a wrong token index would fail
+
+
+def test_sampler_stream_with_the_largest_uniform():
+    """Philox stream 1205178 under key 0 gives draw 0 the largest uniform the sampler can
+    draw, 1 - 2^-24 (the GPU test of the sampler's zero-probability fallback uses it)."""
+    assert ref.sample_uniforms(1, 0, 1205178)[0] == 1.0 - 2.0 ** -24
+    assert ref.sample_uniforms(1, 0, 1205177)[0] < 1.0 - 2.0 ** -24

@@ -44,6 +44,40 @@ def _run(xp, fn, q, k, vt, B, Hq, Hkv, Tq, Tk, L, D, offset):
 CASES = [(4, 8, 1, 1, 2176, 2176, 256), (2, 4, 1, 1, 300, 304, 128)]
 
 
+def _call(xp, c, fn, q, k, vt, out, B, Hq, Hkv, Tq, Tk, L, D, offset):
+    rc = getattr(c.lib, fn)(c.handle, q.ptr, k.ptr, vt.ptr, out.ptr, B, Hq, Hkv, Tq, Tk, D,
+                            out.pitch, offset, float(np.float32(D ** 0.5)), 1, L,
+                            xp.bfloat16.code)
+    assert rc == 0, (fn, rc, xp.last_error())
+
+
+def test_noalloc_first_call_on_a_fresh_context_allocates_nothing(xp):
+    """The no-alloc entry point called first on a fresh context (empty workspace, empty
+    allocator) at the config-5 decode size: afterwards the context's workspace is still 0
+    bytes and its allocator counters are unchanged, so the partials went to the static
+    scratch. tl_attention_fwd on the same context then grows the workspace (the query sees
+    it) and writes the same bytes."""
+    B, Hq, Hkv, Tq, Tk, L, D = CASES[0]
+    print(f"noalloc fresh-context case B={B} Hq={Hq} Tk={Tk} D={D}", flush=True)
+    q, k, vt = _operands(xp, np.random.default_rng(11), B, Hq, Hkv, Tq, Tk, L, D)
+    got, want = (xp.empty((B, Tq, Hq * D), "bf16").fill(7.0) for _ in range(2))
+    xp.synchronize()  # operands were written on the default context's stream
+    c2 = xp.Context(xp.ctx().device)
+    try:
+        assert c2.workspace_bytes() == 0
+        stats = c2.mem_stats()
+        _call(xp, c2, "tl_attention_fwd_noalloc", q, k, vt, got, B, Hq, Hkv, Tq, Tk, L, D, Tk - Tq)
+        c2.sync()
+        assert c2.workspace_bytes() == 0
+        assert c2.mem_stats() == stats
+        _call(xp, c2, "tl_attention_fwd", q, k, vt, want, B, Hq, Hkv, Tq, Tk, L, D, Tk - Tq)
+        c2.sync()
+        assert c2.workspace_bytes() > 0
+    finally:
+        c2.destroy()
+    assert np.array_equal(got.get_raw(), want.get_raw())
+
+
 def test_noalloc_decode_matches_allocating_entry_point_twice(xp):
     rng = np.random.default_rng(2024)
     for B, Hq, Hkv, Tq, Tk, L, D in CASES:

@@ -66,22 +66,34 @@ __global__ __launch_bounds__(256) void random_normal_kernel(T* y, int64_t n, uin
 // Categorical sampling (the notebook's xp.random.choice(..., p=probs), demo.ipynb:1531):
 // sample j draws u = (w0 >> 8) 2^-24 in [0, 1) from Philox counter (j, 0, stream) and key
 // seed, and returns the smallest index i with cdf[i] > u * total, where cdf is the running
-// sum of p (searchsorted(cdf, u * total, side='right'), clamped to the last index). One
-// workgroup: thread t sums a contiguous chunk of p, a scan over the chunk sums in LDS
-// gives each chunk its [start, end) share of [0, total), and the thread whose share holds
-// u * total walks its chunk to the index.
+// sum of p (searchsorted(cdf, u * total, side='right')). One workgroup: thread t sums a
+// contiguous chunk of p, a scan over the chunk sums in LDS gives each chunk its
+// [start, end) share of [0, total), and the thread whose share holds x = u * total walks
+// its chunk to the index. The walk adds the chunk's entries to `start` one by one, which
+// can round below the scanned `end`; when no running sum passes x, the draw takes the
+// chunk's last nonzero entry (x lies in that entry's share up to rounding), and an x at or
+// past the total takes the last nonzero entry of the row, so a zero-probability index is
+// never returned (the row's last index if every entry is zero).
 template <typename T>
 __global__ __launch_bounds__(1024) void sample_kernel(const T* p, int64_t cols, int64_t n,
                                                       uint32_t k0, uint32_t k1, uint32_t s0,
                                                       uint32_t s1, int64_t* out) {
   __shared__ float incl[1024];
+  __shared__ unsigned long long last_nz;  // 1 + the row's last nonzero index (0: none)
   const int t = threadIdx.x;
+  if (t == 0) last_nz = 0;
   const int64_t chunk = (cols + 1023) / 1024;
   const int64_t lo = min(cols, (int64_t)t * chunk), hi = min(cols, lo + chunk);
   float sum = 0.f;
-  for (int64_t i = lo; i < hi; ++i) sum += Elem<T>::load(p + i);
+  int64_t nz = -1;  // this chunk's last nonzero index
+  for (int64_t i = lo; i < hi; ++i) {
+    const float v = Elem<T>::load(p + i);
+    sum += v;
+    if (v != 0.f) nz = i;
+  }
   incl[t] = sum;
   __syncthreads();
+  if (nz >= 0) atomicMax(&last_nz, (unsigned long long)(nz + 1));
   for (int off = 1; off < 1024; off <<= 1) {  // inclusive scan (Hillis-Steele)
     const float v = t >= off ? incl[t - off] : 0.f;
     __syncthreads();
@@ -90,14 +102,13 @@ __global__ __launch_bounds__(1024) void sample_kernel(const T* p, int64_t cols, 
   }
   const float total = incl[1023];
   const float start = t > 0 ? incl[t - 1] : 0.f, end = incl[t];
+  const int64_t row_last = last_nz > 0 ? (int64_t)last_nz - 1 : cols - 1;
   for (int64_t j = 0; j < n; ++j) {
     const Philox4 w = philox4x32_10((uint32_t)j, (uint32_t)((uint64_t)j >> 32), s0, s1, k0, k1);
     const float x = (float)(w.v[0] >> 8) * 5.9604644775390625e-08f * total;
-    // the share that holds x; past the end (rounding) the last nonempty chunk takes it
-    const bool mine = (x >= start && x < end) || (t == 1023 && x >= total);
-    if (mine && lo < hi) {
+    if (x >= start && x < end) {  // a nonempty share: the chunk holds a nonzero entry
       float c = start;
-      int64_t idx = hi - 1;
+      int64_t idx = nz;
       for (int64_t i = lo; i < hi; ++i) {
         c += Elem<T>::load(p + i);
         if (c > x) {
@@ -106,8 +117,8 @@ __global__ __launch_bounds__(1024) void sample_kernel(const T* p, int64_t cols, 
         }
       }
       out[j] = idx;
-    } else if (mine) {
-      out[j] = cols - 1;
+    } else if (t == 1023 && !(x < total)) {
+      out[j] = row_last;
     }
   }
 }

@@ -239,6 +239,9 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Norm launches with fewer workgroups than this ignore the prefetch regions (one per CU).
+constexpr int kPrefetchMinGrid = 256;
+
 // Thread `tid` of `nthreads` loads one 4-byte word of every nthreads-th 128-byte line of the
 // prefetch regions, so their lines are fetched into the caches while the kernel runs; the
 // words are xor-ed together and kept only so the loads are not removed.
@@ -1009,9 +1012,11 @@ static void launch_norm(tl_ctx* ctx, const void* x, const void* g, const void* b
       constexpr bool NTV = decltype(nt_tag)::value, FULLV = decltype(full_tag)::value;
       const unsigned grid = (unsigned)((rows + 256 / LPR - 1) / (256 / LPR));
       // weights are warmed for products over in-cache activations only, so the streamed
-      // (non-temporal) instantiations carry no prefetch
+      // (non-temporal) instantiations carry no prefetch; nor do grids of fewer workgroups
+      // than CUs (a decode step's few rows): there a handful of workgroups would walk
+      // megabytes of weights line by line, which the few-row product then streams anyway
       if constexpr (!NTV) {
-        if (pf) {
+        if (pf && grid >= (unsigned)kPrefetchMinGrid) {
           norm_wave_kernel<T, CH, RMS, false, FULLV, LPR, true><<<grid, 256, 0, ctx->stream>>>(
               (const T*)x, (const T*)g, (const T*)b, (T*)y, rows, (int)cols, ldx, ldy, eps, goff,
               ctx->prefetch);

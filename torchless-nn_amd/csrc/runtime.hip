@@ -347,6 +347,14 @@ int tl_mem_stats(tl_ctx* ctx, size_t* in_use, size_t* cached) {
   return TL_OK;
 }
 
+int tl_workspace_bytes(tl_ctx* ctx, size_t* bytes) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(bytes, "null pointer");
+  *bytes = ctx->ws_bytes;
+  return TL_OK;
+}
+
 // A pinned staging buffer of at least `bytes` whose previous copy has completed (waiting
 // only for that copy), or null when the copy is too large to stage.
 static constexpr size_t kStageMax = (size_t)64 << 20;

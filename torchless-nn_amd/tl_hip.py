@@ -149,6 +149,7 @@ SIGNATURES = {
     "tl_free": [_P, _P],
     "tl_empty_cache": [_P],
     "tl_mem_stats": [_P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)],
+    "tl_workspace_bytes": [_P, ctypes.POINTER(_SZ)],
     "tl_memcpy_h2d": [_P, _P, _P, _SZ],
     "tl_memcpy_d2h": [_P, _P, _P, _SZ],
     "tl_memcpy_d2d": [_P, _P, _P, _SZ],
@@ -265,6 +266,16 @@ class Context:
 
     def empty_cache(self):
         check(self.lib.tl_empty_cache(self.handle))
+
+    def workspace_bytes(self):
+        n = ctypes.c_size_t()
+        check(self.lib.tl_workspace_bytes(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def destroy(self):
+        if self.handle:
+            check(self.lib.tl_destroy(self.handle))
+            self.handle = None
 
 
 _ctx = None
