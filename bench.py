@@ -123,87 +123,6 @@ def row_kernel_bench(xp, reps=20):
     return out
 
 
-def gemm_sweep(xp, reps=10, only_shapes=None, only_tiles=None, model="gpt"):
-    """Times every MFMA tile shape on the dense GEMMs of one forward (with their real
-    epilogues) and prints TFLOP/s per (shape, tile); used to tune the tile heuristic.
-    model="gpt": config 3 (M = 8192, d 768, 12 heads, LM head); "vit": config 4 (M = 512 x
-    65 tokens, d 384, 6 heads, no LM head)."""
-    rng = np.random.default_rng(0)
-    if model == "square":  # one long-K GEMM: per-tile start-up amortised over 128 K steps
-        a = xp.random_normal((8192, 8192), 1, 0, std=1.0, dtype="bf16")
-        bt = xp.random_normal((8192, 8192), 2, 0, std=0.02, dtype="bf16")
-        c = xp.empty((8192, 8192), "bf16")
-        table = {"square8192": {}}
-        for t in ["auto"] + [t for t in xp.GEMM_TILES if t not in ("auto", "skinny")]:
-            if only_tiles and t not in only_tiles:
-                continue
-            fn = lambda: xp.gemm(a, bt, M=8192, N=8192, K=8192, lda=8192, ldb=8192,
-                                 b_layout=xp.TL_B_NK, C=c, ldc=8192, tile=t)
-            fn()
-            e0, e1 = xp.Event(), xp.Event()
-            e0.record()
-            for _ in range(3):
-                fn()
-            e1.record()
-            ms = e0.elapsed_ms(e1) / 3
-            table["square8192"][t] = {"us": round(ms * 1e3, 1), "tflops": round(2 * 8192 ** 3 / (ms * 1e-3) / 1e12, 1)}
-        log("gemm sweep square8192: " + ", ".join(f"{t} {v['tflops']}" for t, v in table["square8192"].items()))
-        return table
-    if model == "vit":
-        BATCH_, SEQ_, C, V, H = 512, 65, 384, 10, 6
-    else:
-        BATCH_, SEQ_, C, V, H = BATCH, SEQ, CFG["d"], CFG["vocab"], CFG["heads"]
-    M, D = BATCH_ * SEQ_, C // H
-    Lk = (SEQ_ + 7) // 8 * 8
-
-    def dev(shape, scale=0.02):
-        return xp.array(rng.standard_normal(shape).astype(np.float32) * np.float32(scale), dtype="bf16")
-
-    x, x4 = dev((M, C), 1.0), dev((M, 4 * C), 1.0)
-    res = dev((M, C), 1.0)
-    w = {"qkv": dev((3 * C, C)), "out": dev((C, C)), "ffn1": dev((4 * C, C)), "ffn2": dev((C, 4 * C)),
-         "head": dev((V, C))}
-    b = {k: dev((w[k].shape[0],)) for k in w}
-    q, k, vt = (xp.empty((BATCH_, H, SEQ_, D), "bf16"), xp.empty((BATCH_, H, Lk, D), "bf16"),
-                xp.empty((BATCH_, H, D, Lk), "bf16"))
-    out_c, out_4c = xp.empty((M, C), "bf16"), xp.empty((M, 4 * C), "bf16")
-    logits = xp.empty((M, V), "bf16", pitch=(V + 7) // 8 * 8)
-    shapes = {
-        "qkv": lambda t: xp.gemm(x, w["qkv"], M=M, N=3 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                 bias=b["qkv"], qkv=(q, k, vt, SEQ_, H, H, D, Lk, 0), tile=t),
-        "out_proj": lambda t: xp.gemm(x, w["out"], M=M, N=C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                      C=out_c, ldc=C, bias=b["out"], residual=res, ldr=C, tile=t),
-        "ffn1": lambda t: xp.gemm(x, w["ffn1"], M=M, N=4 * C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                  C=out_4c, ldc=4 * C, bias=b["ffn1"], act=xp.TL_ACT_GELU, tile=t),
-        "ffn2": lambda t: xp.gemm(x4, w["ffn2"], M=M, N=C, K=4 * C, lda=4 * C, ldb=4 * C,
-                                  b_layout=xp.TL_B_NK, C=out_c, ldc=C, bias=b["ffn2"], residual=res,
-                                  ldr=C, tile=t),
-        "lm_head": lambda t: xp.gemm(x, w["head"], M=M, N=V, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                     C=logits, ldc=logits.pitch, tile=t),
-    }
-    flops = {"qkv": 2 * M * 3 * C * C, "out_proj": 2 * M * C * C, "ffn1": 2 * M * 4 * C * C,
-             "ffn2": 2 * M * C * 4 * C, "lm_head": 2 * M * V * C}
-    table = {}
-    for name, fn in shapes.items():
-        if only_shapes and name not in only_shapes or (model == "vit" and name == "lm_head"):
-            continue
-        table[name] = {}
-        for t in ["auto"] + [t for t in xp.GEMM_TILES if t not in ("auto", "skinny")]:
-            if only_tiles and t not in only_tiles:
-                continue
-            for _ in range(2):
-                fn(t)
-            e0, e1 = xp.Event(), xp.Event()
-            e0.record()
-            for _ in range(reps):
-                fn(t)
-            e1.record()
-            ms = e0.elapsed_ms(e1) / reps
-            table[name][t] = {"us": round(ms * 1e3, 1), "tflops": round(flops[name] / (ms * 1e-3) / 1e12, 1)}
-        log(f"gemm sweep {name}: " + ", ".join(f"{t} {v['tflops']}" for t, v in table[name].items()))
-    return table
-
-
 def gemma_bench(xp, prefill_reps=3, decode_steps=128, graph=True):
     """Gemma-style bf16 decoder (2.5B weights, device-seeded N(0,0.02)):
     prefill B=4 x T=2048 into the KV cache, then `decode_steps` greedy steps at M=4 whose
@@ -384,76 +303,6 @@ def vit_bench(xp, steps=10, warmup=3):
     log(f"vit config 4: {json.dumps(out)}")
     del net, x
     return out
-
-
-def decode_sweep(xp, reps=50):
-    """Times each GEMM of a config-5 decode step (M = 4) and one layer's decode attention,
-    in GB/s of algorithmic bytes (weights + activations; K and V for attention)."""
-    rng = np.random.default_rng(0)
-    B, C, F, V, D, Hq = 4, 2048, 16384, 256000, 256, 8
-    Tk, L = 2176, 2176
-
-    def dev(shape, scale=0.02):
-        return xp.random_normal(shape, int(rng.integers(1 << 30)), 0, std=scale, dtype="bf16")
-
-    x, h = dev((B, C), 1.0), dev((B, F), 1.0)
-    res = dev((B, C), 1.0)
-    w = {"qkv": dev((10 * D, C)), "out": dev((C, C)), "geglu": dev((2 * F, C)),
-         "down": dev((C, F)), "head": dev((V, C)), "down_pad": dev((C, F + 64))}
-    q, k, vt = (xp.empty((B, Hq, 1, D), "bf16"), dev((B, 1, L, D), 1.0), dev((B, 1, D, L), 1.0))
-    outc, outf = xp.empty((B, C), "bf16"), xp.empty((B, F), "bf16")
-    logits = xp.empty((B, V), "bf16", pitch=V)
-    heads = xp.empty((B, Hq * D), "bf16")
-    gam, xn = dev((C,)), xp.empty((B, C), "bf16")
-    cases = {
-        "qkv": (lambda: xp.gemm(x, w["qkv"], M=B, N=10 * D, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                qkv=(q, k, vt, 1, Hq, 1, D, L, 2100)), 2 * 10 * D * C),
-        "out": (lambda: xp.gemm(x, w["out"], M=B, N=C, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                C=outc, ldc=C, residual=res, ldr=C), 2 * C * C),
-        "geglu": (lambda: xp.gemm(x, w["geglu"], M=B, N=2 * F, K=C, lda=C, ldb=C,
-                                  b_layout=xp.TL_B_NK, C=outf, ldc=F, act=xp.TL_ACT_GELU,
-                                  geglu=True), 2 * 2 * F * C),
-        "down": (lambda: xp.gemm(h, w["down"], M=B, N=C, K=F, lda=F, ldb=F, b_layout=xp.TL_B_NK,
-                                 C=outc, ldc=C, residual=res, ldr=C), 2 * C * F),
-        "head": (lambda: xp.gemm(x, w["head"], M=B, N=V, K=C, lda=C, ldb=C, b_layout=xp.TL_B_NK,
-                                 C=logits, ldc=V), 2 * V * C),
-        # the same products with the RMSNorm's row scaling folded in, and the down projection with its
-        # weight rows padded off the 32 KiB pitch
-        "qkv_norm": (lambda: xp.gemm(x, w["qkv"], M=B, N=10 * D, K=C, lda=C, ldb=C,
-                                     b_layout=xp.TL_B_NK, qkv=(q, k, vt, 1, Hq, 1, D, L, 2100),
-                                     norm_eps=1e-6), 2 * 10 * D * C),
-        "geglu_norm": (lambda: xp.gemm(x, w["geglu"], M=B, N=2 * F, K=C, lda=C, ldb=C,
-                                       b_layout=xp.TL_B_NK, C=outf, ldc=F, act=xp.TL_ACT_GELU,
-                                       geglu=True, norm_eps=1e-6), 2 * 2 * F * C),
-        "head_norm": (lambda: xp.gemm(x, w["head"], M=B, N=V, K=C, lda=C, ldb=C,
-                                      b_layout=xp.TL_B_NK, C=logits, ldc=V,
-                                      norm_eps=1e-6), 2 * V * C),
-        "down_pad": (lambda: xp.gemm(h, w["down_pad"], M=B, N=C, K=F, lda=F, ldb=F + 64,
-                                     b_layout=xp.TL_B_NK, C=outc, ldc=C, residual=res, ldr=C),
-                     2 * C * F),
-        "rmsnorm_4x2048": (lambda: xp.rmsnorm(x, gam, np.float32(1e-6), 1.0, out=xn), 2 * 2 * B * C),
-        "attention": (lambda: xp.attention(q, k, vt, heads, n_heads_q=Hq, n_heads_kv=1,
-                                           divisor=16.0, causal=True, offset=Tk - 1, seq_k=Tk),
-                      2 * 2 * B * Tk * D),
-    }
-    out = {}
-    for name, (fn, nbytes) in cases.items():
-        for _ in range(3):
-            fn()
-        e0, e1 = xp.Event(), xp.Event()
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        us = e0.elapsed_ms(e1) / reps * 1e3
-        out[name] = {"us": round(us, 2), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
-    log(f"decode sweep (skinny cfg {os.environ.get('TL_SKINNY_CFG', '0')}, attention cfg "
-        f"{os.environ.get('TL_ATTN_DECODE_CFG', '0')}): {json.dumps(out)}")
-    return out
-
-
-VENDOR_SHAPES = {"qkv": (768, 2304), "out_proj": (768, 768), "ffn1": (768, 3072),
-                 "ffn2": (3072, 768), "lm_head": (768, 50257)}  # (K, N) at M = 8192
 
 
 def vendor_gemm_child(reps=20):
@@ -688,14 +537,6 @@ def main():
                     help="skip the config-5 decode replayed from a HIP graph (profiling runs)")
     ap.add_argument("--no-vendor", action="store_true",
                     help="skip the hipBLASLt (PyTorch F.linear) GEMM comparison")
-    ap.add_argument("--sweep-gemm", action="store_true",
-                    help="only time the dense GEMM shapes under every tile shape")
-    ap.add_argument("--sweep-shapes", default="", help="comma list of shapes for --sweep-gemm")
-    ap.add_argument("--sweep-decode", action="store_true",
-                    help="only time the config-5 decode-step GEMMs and attention")
-    ap.add_argument("--sweep-tiles", default="", help="comma list of tiles for --sweep-gemm")
-    ap.add_argument("--sweep-model", default="gpt", choices=["gpt", "vit", "square"],
-                    help="GEMM shapes for --sweep-gemm: config 3 (gpt) or config 4 (vit)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain fp32 copy kernel of 256 MiB three times (the "
                          "reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -720,17 +561,8 @@ def main():
         xp.synchronize()
         del src, dst
         log("copy calibration: 3 x cast_vec_kernel<float,float> over 256 MiB")
-    if args.sweep_decode:
-        print(json.dumps({"decode_sweep": decode_sweep(xp)}), flush=True)
-        return
     if args.only_row_kernels:
         print(json.dumps({"row_kernels": row_kernel_bench(xp)}), flush=True)
-        return
-    if args.sweep_gemm:
-        print(json.dumps({"gemm_sweep": gemm_sweep(
-            xp, only_shapes=[x for x in args.sweep_shapes.split(",") if x],
-            only_tiles=[x for x in args.sweep_tiles.split(",") if x], model=args.sweep_model)}),
-              flush=True)
         return
     log("building GPT-2-small-shape model (bf16) and seeding weights")
     net, _ = gpt.build_gpt(CFG, dtype="bf16")
