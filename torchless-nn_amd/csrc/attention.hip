@@ -82,15 +82,21 @@ __device__ __forceinline__ int vperm_slot16(int g4, int r) {
   return vperm_piece16(c2, slot >> 1, r) + ((slot & 1) << 2);
 }
 
-template <int D>
-__global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
-  constexpr int BKV = 64;
+//
+// NW = 8 (head dims 128 and 256): 8 waves, 128 query rows per workgroup, two waves per SIMD.
+// A wave's state (16 rows x D outputs, its query fragments, the next chunk's loads) fits the
+// 256 VGPRs of two waves per SIMD, so while one wave waits on its LDS fragment reads or runs
+// its softmax the other issues MFMAs; with NW = 4 the single wave per SIMD (the 128 KB of K
+// and V^T chunks at D = 256 allow one workgroup per CU) runs those phases one after another.
+template <int D, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void attention_fwd_kernel(AttnParams p) {
+  constexpr int BKV = 64, NT = 64 * NW, RB = 16 * NW;
   constexpr int KCH = D / 8;          // 16-byte chunks per K row
   constexpr int KSW = KCH >= 8 ? 7 : KCH - 1;
   constexpr int DT = D / 16;          // 16-row d tiles of the output
   constexpr int KS = D / 32;          // 32-wide k steps of Q.K
-  constexpr int K_LOADS = BKV * KCH / 256;  // chunks per thread per K tile
-  constexpr int V_LOADS = D * 8 / 256;      // V^T tile: D rows x 8 chunks
+  constexpr int K_LOADS = BKV * KCH / NT;  // chunks per thread per K tile
+  constexpr int V_LOADS = D * 8 / NT;      // V^T tile: D rows x 8 chunks
   static_assert(K_LOADS >= 1 && V_LOADS >= 1, "head_dim too small");
   __shared__ __attribute__((aligned(16))) bf16_t Ks[2][BKV * D];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[2][D * BKV];
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   const int bh = blockIdx.y;
   const int b = bh / p.Hq, h = bh - b * p.Hq;
   const int hk = h / (p.Hq / p.Hkv);
-  const int nqb = (p.Tq + 63) / 64;
+  const int nqb = (p.Tq + RB - 1) / RB;
   // Under a causal mask query blocks are processed in pairs (nqb-1-x, x): the pair's chunk
   // counts sum to nqb + 1 for every x, so all workgroups carry the same work. Without a
   // mask every block costs the same and each workgroup takes one.
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
   for (int pass = 0; pass < (p.causal ? 2 : 1); ++pass) {
     const int qb = pass == 0 ? nqb - 1 - x : x;
     if (pass == 1 && qb >= nqb - 1 - x) break;
-    const int q0 = qb * 64 + wave * 16;
+    const int q0 = qb * RB + wave * 16;
     const bf16_t* qh = p.q + ((int64_t)(b * p.Hq + h) * p.Tq) * D;
     const bf16_t* kh = p.k + ((int64_t)(b * p.Hkv + hk) * p.Lk) * D;
     const bf16_t* vh = p.vt + ((int64_t)(b * p.Hkv + hk) * D) * p.Lk;
@@ -123,7 +129,7 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
     }
 
     // kv range this block needs
-    const int q_last = min(qb * 64 + 63, p.Tq - 1);
+    const int q_last = min(qb * RB + RB - 1, p.Tq - 1);
     int kv_end = p.Tk;
     if (p.causal) kv_end = (int)min((int64_t)p.Tk, (int64_t)q_last + p.offset + 1);
     const int nchunks = (kv_end + BKV - 1) / BKV;
@@ -133,12 +139,12 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
     uint32_t k_off[K_LOADS], v_off[V_LOADS];
   #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = i * 256 + tid;
+      const int idx = i * NT + tid;
       k_off[i] = (uint32_t)((idx / KCH) * D + (idx % KCH) * 8);
     }
   #pragma unroll
     for (int i = 0; i < V_LOADS; ++i) {
-      const int idx = i * 256 + tid;
+      const int idx = i * NT + tid;
       v_off[i] = (uint32_t)((idx >> 3) * p.Lk + (idx & 7) * 8);
     }
     auto load_chunk_regs = [&](int kv0) {
@@ -153,14 +159,14 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
       }
   #pragma unroll
       for (int i = 0; i < K_LOADS; ++i) {
-        const int kv = kv0 + (i * 256 + tid) / KCH;
+        const int kv = kv0 + (i * NT + tid) / KCH;
         rk[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(kc + k_off[i]) : make_uint4(0, 0, 0, 0);
       }
   #pragma unroll
       for (int i = 0; i < V_LOADS; ++i) {
         // Lk % 8 == 0, so a chunk that starts below Tk lies inside the row; its positions
         // past Tk (capacity padding, never written) are zeroed, since 0 * NaN would not be 0
-        const int kv = kv0 + ((i * 256 + tid) & 7) * 8;
+        const int kv = kv0 + ((i * NT + tid) & 7) * 8;
         rv[i] = kv < p.Tk ? *reinterpret_cast<const uint4*>(vc + v_off[i]) : make_uint4(0, 0, 0, 0);
         if (kv < p.Tk && kv + 8 > p.Tk) rv[i] = keep_first(rv[i], p.Tk - kv);
       }
@@ -168,12 +174,12 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
     auto store_chunk_lds = [&](int buf) {
   #pragma unroll
       for (int i = 0; i < K_LOADS; ++i) {
-        const int idx = i * 256 + tid, r = idx / KCH, c = idx % KCH;
+        const int idx = i * NT + tid, r = idx / KCH, c = idx % KCH;
         *reinterpret_cast<uint4*>(&Ks[buf][r * D + ((c ^ (r & KSW)) << 3)]) = rk[i];
       }
   #pragma unroll
       for (int i = 0; i < V_LOADS; ++i) {
-        const int idx = i * 256 + tid, r = idx >> 3, c = idx & 7;
+        const int idx = i * NT + tid, r = idx >> 3, c = idx & 7;
         bf16_t* row = &Vs[buf][r * BKV];
         *reinterpret_cast<uint2*>(row + vperm_slot(2 * c, r)) = make_uint2(rv[i].x, rv[i].y);
         *reinterpret_cast<uint2*>(row + vperm_slot(2 * c + 1, r)) = make_uint2(rv[i].z, rv[i].w);
@@ -209,6 +215,9 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
           const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[cur][r * D + ((c ^ (r & KSW)) << 3)]);
           s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], s[j], 0, 0, 0);
         }
+        // two waves per SIMD: keep each key tile's fragment reads next to its MFMAs (reading
+        // all 32 of a chunk ahead would hold 128 more registers than the budget has)
+        if constexpr (NW == 8) __builtin_amdgcn_sched_barrier(0);
       }
       // mask (only chunks that cross this wave's causal diagonal or the key count need one:
       // the test is uniform across the wave), row max of the raw scores
@@ -279,6 +288,9 @@ __global__ __launch_bounds__(256) void attention_fwd_kernel(AttnParams p) {
           const int r = t * 16 + fr;
           const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&Vs[cur][r * BKV + vperm_piece(c2, fg, r)]);
           o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[t], 0, 0, 0);
+          if constexpr (NW == 8) {
+            if (t % 4 == 3) __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
 
@@ -1429,8 +1441,16 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     else attention_fwd_wide_kernel<64><<<grid, 256, 0, ctx->stream>>>(p);
     return ls.finish("attention_fwd_wide");
   }
-  const int64_t nqb = (seq_q + 63) / 64;
+  // head dims 128 and 256 beyond 64 query rows: 8 waves of 16 rows per workgroup (two per
+  // SIMD), 128-row blocks
+  const int64_t rb = head_dim >= 128 && seq_q > 64 ? 128 : 64;
+  const int64_t nqb = (seq_q + rb - 1) / rb;
   dim3 grid((unsigned)(causal ? (nqb + 1) / 2 : nqb), (unsigned)(batch * n_heads_q));
+  if (rb == 128) {
+    if (head_dim == 128) attention_fwd_kernel<128, 8><<<grid, 512, 0, ctx->stream>>>(p);
+    else attention_fwd_kernel<256, 8><<<grid, 512, 0, ctx->stream>>>(p);
+    return ls.finish("attention_fwd");
+  }
   switch (head_dim) {
     case 32: attention_fwd_kernel<32><<<grid, 256, 0, ctx->stream>>>(p); break;
     case 64: attention_fwd_kernel<64><<<grid, 256, 0, ctx->stream>>>(p); break;
