@@ -683,10 +683,13 @@ def test_gemm_every_tile_shape(xp, tile, mnk):
 
 
 @pytest.mark.parametrize("mnk", [(1, 1, 8), (4, 15, 40), (4, 2560, 2048), (16, 2048, 16384),
-                                 (7, 50257, 64), (3, 300, 776)])
+                                 (7, 50257, 64), (3, 300, 776),
+                                 # the persistent stream (K a multiple of 2048): ~5 blocks per
+                                 # workgroup with a ragged last block, 2 and 3 K parts
+                                 (5, 40001, 2048), (2, 1000, 4096), (16, 72, 6144)])
 @pytest.mark.parametrize("out_dt", ["bf16", "fp32"])
 def test_gemm_skinny_decode_rows(xp, mnk, out_dt):
-    """The weight-streaming kernel (M <= 16, chosen automatically) on ragged N and a K that
+    """The weight-streaming kernels (M <= 16, chosen automatically) on ragged N and a K that
     splits unevenly over its waves, with bias, GeLU and residual."""
     M, N, K = mnk
     rng = np.random.default_rng(M * 31 + N + K)
@@ -763,7 +766,8 @@ def test_gemm_gated_staged(xp, tile, mnk):
         assert np.all(got[:, F:] == 7.0), (tile, mnk, act)
 
 
-@pytest.mark.parametrize("mnk", [(4, 2560, 2048), (3, 300, 776), (16, 1000, 64), (1, 8, 8)])
+@pytest.mark.parametrize("mnk", [(4, 2560, 2048), (3, 300, 776), (16, 1000, 64), (1, 8, 8),
+                                 (2, 33008, 2048)])  # the stream: the row scale reused over blocks
 def test_gemm_skinny_rms_row_scaling(xp, mnk):
     """An RMSNorm folded into a decode product: the gain packed into the weight with
     tl_transpose2d_gain and the product's rows scaled by 1 / rms(a). act(RMSNorm(a) @ w +

@@ -1349,6 +1349,97 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p, floa
   }
 }
 
+// gemm_skinny_stream_kernel: the few-row product as a persistent weight stream, for K a
+// multiple of 2048 (config-5 decode: K = 2048 for QKV, out-projection, GeGLU and the LM head,
+// 16384 for the down projection). K is cut into parts of 2048 (gridDim.x = parts x
+// workgroups per part, part = blockIdx.x % parts) and a workgroup walks the 16-row blocks of
+// Bt n0 = 16 b, b = blockIdx.x / parts, + (gridDim.x / parts), ... Its 4 waves split the
+// part's K into 512-wide ranges of 16 steps of 32, one load of Bt per step and wave as in
+// gemm_skinny_kernel (lane: row lane % 16, 8 columns at 8 (lane / 16)). The A rows of a
+// wave's range are the same for every block, so they are loaded once (and, with norm_rows,
+// their X X^T taken once), and the next block's 16 Bt fragments are loaded while the current
+// block's 16 MFMAs run: each wave keeps 16 KB of weights in flight across blocks instead of
+// letting its loads drain to zero between workgroups. The 4 partial sums of a block meet in
+// LDS (two alternating buffers, one barrier per block) and wave 0 runs the epilogue, or, with
+// more than one part, writes the block's partial for gemm_skinny_reduce_kernel.
+template <typename TO, bool NORM>
+__global__ __launch_bounds__(256) void gemm_skinny_stream_kernel(GemmParams p, float* part) {
+  constexpr int NW = 4, U = 16, KW = U * 32;  // K per wave per part: 512
+  __shared__ f32x4 red[2][NW][64];
+  __shared__ float ssq[NW][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int S = (int)(p.K / (NW * KW));  // parts
+  const int ky = (int)blockIdx.x % S, wpp = (int)gridDim.x / S;
+  const int nblk = (int)((p.N + 15) / 16);
+  const int64_t k0 = (int64_t)ky * (NW * KW) + wave * KW + 8 * g;
+  const bool xrow = r < p.M;
+  const bf16_t* X = (const bf16_t*)p.A + (xrow ? r : 0) * p.lda + k0;
+  const bf16_t* Bt = (const bf16_t*)p.B + k0;
+  const bf16x8 zero = {};
+  bf16x8 x[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) x[u] = xrow ? *reinterpret_cast<const bf16x8*>(X + u * 32) : zero;
+  if constexpr (NORM) {
+    f32x4 sq = {0.f, 0.f, 0.f, 0.f};  // X X^T: lane (m, g) holds rows 4 g .. 4 g + 3 of column m
+#pragma unroll
+    for (int u = 0; u < U; ++u) sq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[u], x[u], sq, 0, 0, 0);
+    if (g == (r >> 2)) ssq[wave][r] = sq[r & 3];  // the diagonal element (r, r)
+  }
+  float rscale = 1.f;  // NORM: 1 / rms of row r (wave 0), taken after the first barrier
+  bool have_scale = false;
+  auto load = [&](bf16x8 (&w)[U], int b) {
+    const bf16_t* W = Bt + min((int64_t)b * 16 + r, p.N - 1) * p.ldb;
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = *reinterpret_cast<const bf16x8*>(W + u * 32);
+  };
+  int par = 0;
+  auto block = [&](const bf16x8 (&w)[U], int b) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[u], x[u], acc, 0, 0, 0);
+    red[par][wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 t = red[par][0][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) t += red[par][w2][lane];
+      if (S == 1) {
+        if constexpr (NORM) {
+          if (!have_scale) {  // first block: the row's 1 / rms from the waves' diagonals
+            float q = ssq[0][r];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; ++w2) q += ssq[w2][r];
+            rscale = 1.0f / sqrtf(q / (float)p.K + p.norm_eps);
+            have_scale = true;
+          }
+          t *= rscale;
+        }
+        if (xrow) {
+          float v[4] = {t[0], t[1], t[2], t[3]};
+          epilogue4<bf16_t, TO>(p, 0, 0, r, (int64_t)b * 16 + 4 * g, v);
+        }
+      } else {
+        *reinterpret_cast<f32x4*>(part + (((int64_t)b * S + ky) * 64 + lane) * 4) = t;
+      }
+    }
+    par ^= 1;
+  };
+  bf16x8 wa[U], wb[U];
+  int b = (int)blockIdx.x / S;
+  if (b < nblk) load(wa, b);
+  while (b < nblk) {
+    const int b1 = b + wpp;
+    if (b1 < nblk) load(wb, b1);
+    block(wa, b);
+    if (b1 >= nblk) break;
+    const int b2 = b1 + wpp;
+    if (b2 < nblk) load(wa, b2);
+    block(wb, b1);
+    b = b2;
+  }
+}
+
 // One wave per 16-row block: sums the `split` partials of the skinny kernel, then the epilogue.
 template <typename TO>
 __global__ __launch_bounds__(64) void gemm_skinny_reduce_kernel(GemmParams p, const float* part,
@@ -1567,6 +1658,17 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, 
 // the wide GEMMs fastest (GeGLU 134 MB in 23.9 us, LM head 1.05 GB in 197 us); the others
 // are kept for TL_SKINNY_CFG sweeps.
 
+// The streaming form (gemm_skinny_stream_kernel): `parts` K parts of 2048, `wpp` workgroups per
+// part (a multiple of nothing: the workgroups of a part stride over its 16-row blocks).
+template <typename TO>
+static void launch_skinny_stream(int parts, int wpp, int nblk, hipStream_t st, const GemmParams& p,
+                                 float* part) {
+  const dim3 grid((unsigned)(parts * wpp));
+  if (p.norm_rows) gemm_skinny_stream_kernel<TO, true><<<grid, 256, 0, st>>>(p, part);
+  else gemm_skinny_stream_kernel<TO, false><<<grid, 256, 0, st>>>(p, part);
+  if (parts > 1) gemm_skinny_reduce_kernel<TO><<<dim3((unsigned)nblk, 1, 1), 64, 0, st>>>(p, part, parts);
+}
+
 template <typename TO>
 static void launch_skinny(int cfg, dim3 grid, hipStream_t st, const GemmParams& p, float* part) {
   if (p.norm_rows) {  // the row-scaled form exists for the default shape only
@@ -1763,6 +1865,25 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     const int64_t tiles = (d->N + 15) / 16 * batch;
     const int64_t nsteps = (d->K + 31) / 32;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
+    // K a multiple of 2048, one product: the persistent weight stream, two workgroups per CU
+    // (their ~210 VGPRs per lane allow two waves per SIMD), K in parts of 2048 (a second
+    // launch sums the parts when there is more than one; the row-scaled form takes one part)
+    const int64_t parts = d->K / 2048;
+    if (cfg == 0 && batch == 1 && d->K % 2048 == 0 && parts <= 64 && tiles < (1LL << 30) &&
+        (!d->norm_rows || parts == 1)) {
+      const int64_t wpp = std::max<int64_t>(1, std::min<int64_t>(tiles, 2 * cus / parts));
+      float* part = nullptr;
+      if (parts > 1) {
+        void* ws;
+        rc = workspace(ctx, (size_t)tiles * parts * 64 * 4 * sizeof(float), &ws);
+        if (rc) return rc;
+        part = (float*)ws;
+      }
+      LaunchScope ls(ctx, family, flops, bytes);
+      if (f32out) launch_skinny_stream<float>((int)parts, (int)wpp, (int)tiles, ctx->stream, p, part);
+      else launch_skinny_stream<bf16_t>((int)parts, (int)wpp, (int)tiles, ctx->stream, p, part);
+      return ls.finish("gemm_skinny_stream");
+    }
     // Long K only (the split costs a second launch): split until there are 2 workgroups
     // per CU while every part keeps >= 4096 of K (down projection K = 16384: 4 parts,
     // 23.6 -> 18.0 us; K = 2048 shapes lose more to the extra launch than they gain).
