@@ -712,6 +712,31 @@ def test_gemm_skinny_decode_rows(xp, mnk, out_dt):
         assert ref.max_rel(out.get(), want) <= tol, (mnk, out_dt, tile)
 
 
+def test_gemm_skinny_split_k_parts_repeatable(xp):
+    """Decode products with K in several parts of 2048 (the down projection's 16384 is 8):
+    the parts are written to the context's workspace and summed by a second launch. Thirty
+    calls in a row over two shapes that share the workspace each equal the first call bit for
+    bit and the float64 product within the bf16 bar."""
+    outs = {}
+    for rep in range(15):
+        for M, N, K in ((4, 2048, 16384), (3, 1000, 6144)):
+            rng = np.random.default_rng(N + K)
+            a = ref.round_bf16(rng.standard_normal((M, K)).astype(F32))
+            wt = ref.round_bf16(rng.standard_normal((N, K)).astype(F32) / np.sqrt(K))
+            bias = ref.round_bf16(rng.standard_normal(N).astype(F32))
+            res = ref.round_bf16(rng.standard_normal((M, N)).astype(F32))
+            out = xp.empty((M, N), "bf16")
+            xp.gemm(up(xp, a, "bf16"), up(xp, wt, "bf16"), M=M, N=N, K=K, lda=K, ldb=K,
+                    b_layout=xp.TL_B_NK, C=out, ldc=N, bias=up(xp, bias, "bf16"),
+                    residual=up(xp, res, "bf16"), ldr=N)
+            got = out.get_raw()
+            if (M, N, K) not in outs:
+                outs[(M, N, K)] = got
+                want = gemm_ref(a, wt.T, bias, None, res)
+                assert ref.max_rel(xp.bf16_bits_to_f32(got).reshape(M, N), want) <= 2e-2
+            assert np.array_equal(got, outs[(M, N, K)]), (rep, M, N, K)
+
+
 @pytest.mark.parametrize("C", [512, 2048])
 def test_gemm_skinny_qkv_cache_and_gated(xp, C):
     """Decode-step epilogues through the skinny kernel: QKV scatter into a cache at a

@@ -645,45 +645,34 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
   const bf16_t* kh = p.k + (int64_t)bh * p.Lk * D;
   const bf16_t* vh = p.vt + (int64_t)bh * D * p.Lk;
   const int kc0 = (blockIdx.x * NW + wave) * KPW;
-  // a wave whose keys all lie past the valid ones (a device position short of the capacity)
-  // loads nothing: its scores are masked and its values zero
-  const bool live = kc0 < p.Tk;
 
   // All of this wave's K and V^T fragments are requested up front (the V^T reads do not
-  // depend on the softmax), so the wave waits for one memory round trip, not two. Keys past
-  // Tk are read from the cache's own rows (clamped to the capacity) and masked in the scores.
+  // depend on the softmax), so the wave waits for one memory round trip, not two. The
+  // addresses are clamped to the cache capacity and do not depend on the live key count, so
+  // with a device position the loads do not wait for it either; keys at or past Tk (cache
+  // rows never written: any bits, NaN included) are masked out of the scores by a select and
+  // their values zeroed below. A wave whose keys all lie past Tk reads a few such rows.
   bf16x8 kf[J][KS];
   // V^T rows in the key order of the P.V B operand: keys 32 hp + 4 grp + 0..3 and
   // 32 hp + 16 + 4 grp + 0..3 (values past Tk zeroed, since 0 * NaN would not be 0; the
   // capacity is a multiple of 8, so a 4-key run that starts inside it ends inside it)
   uint2 vfa[J / 2][DT], vfb[J / 2][DT];
-  if (live) {
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int key = min(kc0 + 16 * j + col, p.Lk - 1);
-      const bf16_t* krow = kh + (int64_t)key * D + 8 * grp;
+  for (int j = 0; j < J; ++j) {
+    const int key = min(kc0 + 16 * j + col, p.Lk - 1);
+    const bf16_t* krow = kh + (int64_t)key * D + 8 * grp;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[j][ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks) kf[j][ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+  }
+#pragma unroll
+  for (int hp = 0; hp < J / 2; ++hp) {
+    const int ka = min(kc0 + 32 * hp + 4 * grp, p.Lk - 4), kb = min(kc0 + 32 * hp + 16 + 4 * grp, p.Lk - 4);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
+      vfa[hp][dt] = *reinterpret_cast<const uint2*>(vrow + ka);
+      vfb[hp][dt] = *reinterpret_cast<const uint2*>(vrow + kb);
     }
-#pragma unroll
-    for (int hp = 0; hp < J / 2; ++hp) {
-      const int ka = min(kc0 + 32 * hp + 4 * grp, p.Lk - 4), kb = min(kc0 + 32 * hp + 16 + 4 * grp, p.Lk - 4);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16_t* vrow = vh + (int64_t)(dt * 16 + col) * p.Lk;
-        vfa[hp][dt] = *reinterpret_cast<const uint2*>(vrow + ka);
-        vfb[hp][dt] = *reinterpret_cast<const uint2*>(vrow + kb);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[j][ks] = zero;
-#pragma unroll
-    for (int hp = 0; hp < J / 2; ++hp)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) vfa[hp][dt] = vfb[hp][dt] = make_uint2(0, 0);
   }
   if (!rowok) {
 #pragma unroll
@@ -718,14 +707,22 @@ __global__ __launch_bounds__(64 * NW) void attention_decode_kernel(AttnParams p,
           const float* sn = cs + (int64_t)p.Tq * (D / 2);
           bf16_t* krow = const_cast<bf16_t*>(kh) + (int64_t)key * D + 8 * grp;
           // the whole table row first, then the rotations and stores (a load after a store
-          // to the cache would wait for it)
+          // to the cache would wait for it); with one query position (a decode step) the new
+          // key's row is table row 0, which every lane already holds for its query (qcs)
           float4 kcs[KH][4];
+          if (p.Tq == 1) {
 #pragma unroll
-          for (int ks = 0; ks < KH; ++ks) {
-            kcs[ks][0] = *reinterpret_cast<const float4*>(cs + 32 * ks);
-            kcs[ks][1] = *reinterpret_cast<const float4*>(cs + 32 * ks + 4);
-            kcs[ks][2] = *reinterpret_cast<const float4*>(sn + 32 * ks);
-            kcs[ks][3] = *reinterpret_cast<const float4*>(sn + 32 * ks + 4);
+            for (int ks = 0; ks < KH; ++ks)
+#pragma unroll
+              for (int c = 0; c < 4; ++c) kcs[ks][c] = qcs[ks][c];
+          } else {
+#pragma unroll
+            for (int ks = 0; ks < KH; ++ks) {
+              kcs[ks][0] = *reinterpret_cast<const float4*>(cs + 32 * ks);
+              kcs[ks][1] = *reinterpret_cast<const float4*>(cs + 32 * ks + 4);
+              kcs[ks][2] = *reinterpret_cast<const float4*>(sn + 32 * ks);
+              kcs[ks][3] = *reinterpret_cast<const float4*>(sn + 32 * ks + 4);
+            }
           }
 #pragma unroll
           for (int ks = 0; ks < KH; ++ks) {
