@@ -1865,13 +1865,15 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     const int64_t tiles = (d->N + 15) / 16 * batch;
     const int64_t nsteps = (d->K + 31) / 32;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
-    // K a multiple of 2048, one product: the persistent weight stream, two workgroups per CU
-    // (their ~210 VGPRs per lane allow two waves per SIMD), K in parts of 2048 (a second
-    // launch sums the parts when there is more than one; the row-scaled form takes one part)
+    // K a multiple of 2048, one product: the persistent weight stream, K in parts of 2048 (a
+    // second launch sums the parts when there is more than one; the row-scaled form takes
+    // one part). One workgroup per CU for one part (config-5 decode 1.485 -> 1.473 ms per step
+    // against two: GeGLU's 2048 blocks run 8 per workgroup instead of 4, with less start-up
+    // and tail per byte), two per CU (two waves per SIMD: ~230 VGPRs) over several parts.
     const int64_t parts = d->K / 2048;
     if (cfg == 0 && batch == 1 && d->K % 2048 == 0 && parts <= 64 && tiles < (1LL << 30) &&
         (!d->norm_rows || parts == 1)) {
-      const int64_t wpp = std::max<int64_t>(1, std::min<int64_t>(tiles, 2 * cus / parts));
+      const int64_t wpp = std::max<int64_t>(1, std::min<int64_t>(tiles, (parts == 1 ? 1 : 2) * cus / parts));
       float* part = nullptr;
       if (parts > 1) {
         void* ws;
