@@ -305,6 +305,10 @@ def vit_bench(xp, steps=10, warmup=3):
     return out
 
 
+VENDOR_SHAPES = {"qkv": (768, 2304), "out_proj": (768, 768), "ffn1": (768, 3072),
+                 "ffn2": (3072, 768), "lm_head": (768, 50257)}  # (K, N) at M = 8192
+
+
 def vendor_gemm_child(reps=20):
     """Child process of vendor_gemm_compare: times PyTorch's F.linear (bias, bf16; hipBLASLt
     on ROCm) at the config-3 shapes and prints {name: microseconds} as JSON. It runs in its
