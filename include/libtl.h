@@ -362,7 +362,11 @@ int tl_attention_decode_dev(tl_ctx* ctx, const void* q, void* k, const void* vt,
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). A
  * call whose partials need more than 16 MiB (batch x kv heads x key blocks of 64 keys, each
  * 16 x (head_dim + 2) floats) fails with TL_ERR_INVALID. Every call on one GPU shares that
- * GPU's array: calls that overlap on one GPU (two contexts or two host threads) race. */
+ * GPU's array, which keeps the last call's contents. Eager calls from different contexts take
+ * it in turn: a call first makes its context's stream wait (on the device, with no host wait)
+ * for the event recorded after the last call from another context. A call made while the
+ * stream is being captured into a graph is outside that order: replaying the graph while
+ * another context's call is in flight on the same GPU races with it. */
 int tl_attention_fwd_noalloc(tl_ctx* ctx, const void* q, const void* k, const void* vt,
                              void* out, int64_t batch, int64_t n_heads_q, int64_t n_heads_kv,
                              int64_t seq_q, int64_t seq_k, int64_t head_dim, int64_t ld_out,

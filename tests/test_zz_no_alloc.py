@@ -1,7 +1,8 @@
 """tl_attention_fwd_noalloc (the allocation-free variant of tl_attention_fwd) through the C
 ABI: on the decode path its results equal tl_attention_fwd's bit for bit on two calls in a
 row, the second smaller (the static scratch keeps the first call's contents); the prefill
-path agrees too; a call whose partials exceed the static scratch is refused."""
+path agrees too; calls from two contexts take the scratch in turn; a call whose partials
+exceed the static scratch is refused."""
 import ctypes
 
 import numpy as np
@@ -76,6 +77,42 @@ def test_noalloc_first_call_on_a_fresh_context_allocates_nothing(xp):
     finally:
         c2.destroy()
     assert np.array_equal(got.get_raw(), want.get_raw())
+
+
+def test_noalloc_calls_from_two_contexts_take_the_scratch_in_turn(xp):
+    """Two fresh contexts (two streams) call the no-alloc entry point back to back with no
+    host synchronisation in between, each on its own inputs at the config-5 decode size, so
+    both calls' partials land at the same static scratch addresses. Each call's stream waits
+    for the other context's last call, so every output equals tl_attention_fwd's bit for bit.
+    Destroying the context that used the scratch last leaves the other one working."""
+    B, Hq, Hkv, Tq, Tk, L, D = CASES[0]
+    print(f"noalloc two-context case B={B} Hq={Hq} Tk={Tk} D={D}", flush=True)
+    rng = np.random.default_rng(5)
+    ops = [_operands(xp, rng, B, Hq, Hkv, Tq, Tk, L, D) for _ in range(2)]
+    want = [_run(xp, "tl_attention_fwd", *o, B, Hq, Hkv, Tq, Tk, L, D, Tk - Tq) for o in ops]
+    outs = [[xp.empty((B, Tq, Hq * D), "bf16").fill(7.0) for _ in range(3)] for _ in range(2)]
+    xp.synchronize()
+    ctxs = [xp.Context(xp.ctx().device) for _ in range(2)]
+    try:
+        for r in range(3):
+            for i in range(2):
+                _call(xp, ctxs[i], "tl_attention_fwd_noalloc", *ops[i], outs[i][r],
+                      B, Hq, Hkv, Tq, Tk, L, D, Tk - Tq)
+        for c in ctxs:
+            c.sync()
+        for i in range(2):
+            for r in range(3):
+                assert np.array_equal(outs[i][r].get_raw(), want[i]), (i, r)
+        ctxs[1].destroy()  # the context that used the scratch last
+        again = xp.empty((B, Tq, Hq * D), "bf16").fill(7.0)
+        xp.synchronize()
+        _call(xp, ctxs[0], "tl_attention_fwd_noalloc", *ops[0], again, B, Hq, Hkv, Tq, Tk, L, D,
+              Tk - Tq)
+        ctxs[0].sync()
+        assert np.array_equal(again.get_raw(), want[0])
+    finally:
+        for c in ctxs:
+            c.destroy()
 
 
 def test_noalloc_decode_matches_allocating_entry_point_twice(xp):

@@ -907,22 +907,45 @@ __global__ __launch_bounds__(D < 64 ? 64 : D) void attention_combine_kernel(Attn
 constexpr size_t kNoallocScratchBytes = (size_t)16 << 20;
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
+// The turn order of each device's scratch: the context whose stream last launched kernels
+// that use it. An eager call from another context first makes its own stream wait for that
+// context's noalloc_done event (a device-side wait, the host does not block), so eager calls
+// from different contexts on one GPU take the array in turn instead of overlapping.
+struct ScratchTurn {
+  std::mutex mu;
+  const tl_ctx* last = nullptr;
+};
+static ScratchTurn g_scratch_turn[256];
+
 int attention_scratch_setup(tl_ctx* ctx) {
   static std::mutex mu;
   static void* by_device[256] = {};
   if (ctx->device < 0 || ctx->device >= 256)
     return fail(TL_ERR_NO_DEVICE, "device index %d out of range for the scratch table", ctx->device);
-  std::lock_guard<std::mutex> lock(mu);
-  if (!by_device[ctx->device]) {
-    void* ptr = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !ptr)
-      return fail(TL_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
-                  hipGetErrorString(e));
-    by_device[ctx->device] = ptr;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!by_device[ctx->device]) {
+      void* ptr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !ptr)
+        return fail(TL_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", ctx->device,
+                    hipGetErrorString(e));
+      by_device[ctx->device] = ptr;
+    }
   }
   ctx->noalloc_scratch = by_device[ctx->device];
+  TL_CHECK_HIP(hipEventCreateWithFlags(&ctx->noalloc_done, hipEventDisableTiming));
   return TL_OK;
+}
+
+void attention_scratch_release(tl_ctx* ctx) {
+  if (ctx->device >= 0 && ctx->device < 256) {
+    ScratchTurn& turn = g_scratch_turn[ctx->device];
+    std::lock_guard<std::mutex> lock(turn.mu);
+    if (turn.last == ctx) turn.last = nullptr;
+  }
+  if (ctx->noalloc_done) (void)hipEventDestroy(ctx->noalloc_done);
+  ctx->noalloc_done = nullptr;
 }
 
 // Short sequences (at most 128 queries and 128 keys, e.g. the ViT-S/4 encoder's 65): one
@@ -1278,15 +1301,16 @@ __global__ __launch_bounds__(256) void attention_fwd_f32_kernel(AttnParams p) {
   }
 }
 
+// Decode split: waves per workgroup and 16-key tiles per wave. 2 waves x 32 keys was the
+// fastest on an MI355X at the config-5 decode shape (B = 4, 2176 keys, D = 256) against
+// (4, 4), (1, 4), (1, 2), (4, 2) and (2, 4): 12.0 us per layer with the combine, 13.5 us
+// for 4 waves x 32 keys.
+constexpr int kDecodeWaves = 2, kDecodeTiles = 2;
+
 template <int D>
-static void launch_decode(int nw, int jt, dim3 g1, dim3 g2, hipStream_t st, const AttnParams& p,
+static void launch_decode(dim3 g1, dim3 g2, hipStream_t st, const AttnParams& p,
                           const DecodeWs& w) {
-  if (nw == 4 && jt == 4) attention_decode_kernel<D, 4, 4><<<g1, 256, 0, st>>>(p, w);
-  else if (nw == 2 && jt == 2) attention_decode_kernel<D, 2, 2><<<g1, 128, 0, st>>>(p, w);
-  else if (nw == 1 && jt == 2) attention_decode_kernel<D, 1, 2><<<g1, 64, 0, st>>>(p, w);
-  else if (nw == 4 && jt == 2) attention_decode_kernel<D, 4, 2><<<g1, 256, 0, st>>>(p, w);
-  else if (nw == 2 && jt == 4) attention_decode_kernel<D, 2, 4><<<g1, 128, 0, st>>>(p, w);
-  else attention_decode_kernel<D, 1, 4><<<g1, 64, 0, st>>>(p, w);
+  attention_decode_kernel<D, kDecodeWaves, kDecodeTiles><<<g1, 64 * kDecodeWaves, 0, st>>>(p, w);
   attention_combine_kernel<D><<<g2, D < 64 ? 64 : D, 0, st>>>(p, w);
 }
 
@@ -1369,12 +1393,7 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
   const int64_t rows_per_kv = (n_heads_q / n_heads_kv) * seq_q;
   if (rows_per_kv <= 16) {  // decode: split the keys over many small workgroups
     DecodeWs w;
-    // (waves per workgroup, 16-key tiles per wave); the default, 2 waves x 32 keys, was
-    // fastest on an MI355X at the config-5 decode shape (B = 4, 2176 keys, D = 256):
-    // 12.0 us per layer with the combine vs 13.5 us for 4 waves x 32 keys
-    static const int kDecodeCfg[][2] = {{2, 2}, {4, 4}, {1, 4}, {2, 2}, {1, 2}, {4, 2}, {2, 4}};
-    const int cfg = ctx->attn_decode_cfg >= 1 && ctx->attn_decode_cfg <= 6 ? ctx->attn_decode_cfg : 0;
-    const int nw = kDecodeCfg[cfg][0], jt = kDecodeCfg[cfg][1];
+    constexpr int nw = kDecodeWaves, jt = kDecodeTiles;
     // with a device position the key count is known only on the device: cover the capacity
     const int64_t keys = pos_dev ? cap : seq_k;
     w.nblk = (int)((keys + 16 * nw * jt - 1) / (16 * nw * jt));
@@ -1385,13 +1404,24 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     void* ws;
     const size_t obytes = (size_t)slots * 16 * head_dim * sizeof(float);
     const size_t need = obytes + (size_t)slots * 16 * 2 * sizeof(float);
+    // held from the wait on the previous user of the static scratch to the event recorded
+    // after these kernels; not taken while the stream is being captured into a graph
+    std::unique_lock<std::mutex> turn;
     if (noalloc) {
       if (need > kNoallocScratchBytes)
         return fail(TL_ERR_INVALID, "decode attention needs %zu bytes of partials; the "
                     "allocation-free entry point has %zu (tl_attention_fwd has no such limit)",
                     need, kNoallocScratchBytes);
-      if (!ctx->noalloc_scratch) return fail(TL_ERR_HIP, "static scratch was not set up");
+      if (!ctx->noalloc_scratch || !ctx->noalloc_done)
+        return fail(TL_ERR_HIP, "static scratch was not set up");
       ws = ctx->noalloc_scratch;
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      TL_CHECK_HIP(hipStreamIsCapturing(ctx->stream, &cs));
+      if (cs == hipStreamCaptureStatusNone) {
+        ScratchTurn& t = g_scratch_turn[ctx->device];
+        turn = std::unique_lock<std::mutex>(t.mu);
+        if (t.last && t.last != ctx) TL_CHECK_HIP(hipStreamWaitEvent(ctx->stream, t.last->noalloc_done, 0));
+      }
     } else {
       rc = workspace(ctx, need, &ws);
       if (rc) return rc;
@@ -1401,10 +1431,14 @@ static int attention_fwd(tl_ctx* ctx, const void* q, const void* k, const void* 
     const dim3 g1((unsigned)w.nblk, (unsigned)(batch * n_heads_kv));
     const dim3 g2((unsigned)rows_per_kv, (unsigned)(batch * n_heads_kv));
     switch (head_dim) {
-      case 32: launch_decode<32>(nw, jt, g1, g2, ctx->stream, p, w); break;
-      case 64: launch_decode<64>(nw, jt, g1, g2, ctx->stream, p, w); break;
-      case 128: launch_decode<128>(nw, jt, g1, g2, ctx->stream, p, w); break;
-      default: launch_decode<256>(nw, jt, g1, g2, ctx->stream, p, w); break;
+      case 32: launch_decode<32>(g1, g2, ctx->stream, p, w); break;
+      case 64: launch_decode<64>(g1, g2, ctx->stream, p, w); break;
+      case 128: launch_decode<128>(g1, g2, ctx->stream, p, w); break;
+      default: launch_decode<256>(g1, g2, ctx->stream, p, w); break;
+    }
+    if (turn.owns_lock()) {
+      TL_CHECK_HIP(hipEventRecord(ctx->noalloc_done, ctx->stream));
+      g_scratch_turn[ctx->device].last = ctx;
     }
     return ls.finish("attention_decode");
   }

@@ -1653,11 +1653,6 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, 
   return TL_TILE_64x64;
 }
 
-// (waves per workgroup, K steps in flight per wave) of the skinny kernel
-// Measured on an MI355X at the config-5 decode shapes (M = 4): (4 waves, 16 steps) streams
-// the wide GEMMs fastest (GeGLU 134 MB in 23.9 us, LM head 1.05 GB in 197 us); the others
-// are kept for TL_SKINNY_CFG sweeps.
-
 // The streaming form (gemm_skinny_stream_kernel): `parts` K parts of 2048, `wpp` workgroups per
 // part (a multiple of nothing: the workgroups of a part stride over its 16-row blocks).
 template <typename TO>
@@ -1669,21 +1664,14 @@ static void launch_skinny_stream(int parts, int wpp, int nblk, hipStream_t st, c
   if (parts > 1) gemm_skinny_reduce_kernel<TO><<<dim3((unsigned)nblk, 1, 1), 64, 0, st>>>(p, part, parts);
 }
 
+// The per-tile form: 4 waves per workgroup, 16 K steps in flight per wave. On an MI355X at
+// the config-5 decode shapes (M = 4) this streamed the wide products fastest of (4, 8),
+// (8, 16), (8, 8), (16, 4), (8, 4) and (16, 8) (GeGLU 134 MB in 23.9 us, LM head 1.05 GB in
+// 197 us, before the streaming form took those shapes).
 template <typename TO>
-static void launch_skinny(int cfg, dim3 grid, hipStream_t st, const GemmParams& p, float* part) {
-  if (p.norm_rows) {  // the row-scaled form exists for the default shape only
-    gemm_skinny_kernel<TO, 4, 16, true><<<grid, 256, 0, st>>>(p, part);
-    return;
-  }
-  switch (cfg) {
-    case 1: gemm_skinny_kernel<TO, 4, 8, false><<<grid, 256, 0, st>>>(p, part); break;
-    case 2: gemm_skinny_kernel<TO, 8, 16, false><<<grid, 512, 0, st>>>(p, part); break;
-    case 3: gemm_skinny_kernel<TO, 8, 8, false><<<grid, 512, 0, st>>>(p, part); break;
-    case 4: gemm_skinny_kernel<TO, 16, 4, false><<<grid, 1024, 0, st>>>(p, part); break;
-    case 5: gemm_skinny_kernel<TO, 8, 4, false><<<grid, 512, 0, st>>>(p, part); break;
-    case 6: gemm_skinny_kernel<TO, 16, 8, false><<<grid, 1024, 0, st>>>(p, part); break;
-    default: gemm_skinny_kernel<TO, 4, 16, false><<<grid, 256, 0, st>>>(p, part); break;
-  }
+static void launch_skinny(dim3 grid, hipStream_t st, const GemmParams& p, float* part) {
+  if (p.norm_rows) gemm_skinny_kernel<TO, 4, 16, true><<<grid, 256, 0, st>>>(p, part);
+  else gemm_skinny_kernel<TO, 4, 16, false><<<grid, 256, 0, st>>>(p, part);
   if (grid.y > 1)
     gemm_skinny_reduce_kernel<TO><<<dim3(grid.x, 1, grid.z), 64, 0, st>>>(p, part, (int)grid.y);
 }
@@ -1821,7 +1809,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (geglu && eo == 2 && !d->bias && d->divisor == 1.0f && (d->N / 2) % 8 == 0 && d->ldc % 8 == 0 &&
       ((uintptr_t)d->C % 16) == 0 && d->sc_o % 8 == 0 && d->sc_i % 8 == 0)
     p.epi = d->act == TL_ACT_GELU ? EPI_GEGLU_GELU : EPI_GEGLU_SILU;
-  p.group_m = ctx->gemm_group_m > 0 ? ctx->gemm_group_m : 8;
+  p.group_m = 8;  // tile-rows per group: 8 ties 4 and 2 and beats 16 and 32 in-model
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
   p.norm_rows = d->norm_rows != 0;
@@ -1861,7 +1849,6 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   }
   if (skinny) {
     TL_REQUIRE(d->M <= 16, "the skinny GEMM takes M <= 16");
-    const int cfg = ctx->skinny_cfg >= 1 && ctx->skinny_cfg <= 6 ? ctx->skinny_cfg : 0;
     const int64_t tiles = (d->N + 15) / 16 * batch;
     const int64_t nsteps = (d->K + 31) / 32;
     const int64_t cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
@@ -1871,7 +1858,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     // against two: GeGLU's 2048 blocks run 8 per workgroup instead of 4, with less start-up
     // and tail per byte), two per CU (two waves per SIMD: ~230 VGPRs) over several parts.
     const int64_t parts = d->K / 2048;
-    if (cfg == 0 && batch == 1 && d->K % 2048 == 0 && parts <= 64 && tiles < (1LL << 30) &&
+    if (batch == 1 && d->K % 2048 == 0 && parts <= 64 && tiles < (1LL << 30) &&
         (!d->norm_rows || parts == 1)) {
       const int64_t wpp = std::max<int64_t>(1, std::min<int64_t>(tiles, (parts == 1 ? 1 : 2) * cus / parts));
       float* part = nullptr;
@@ -1890,7 +1877,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     // per CU while every part keeps >= 4096 of K (down projection K = 16384: 4 parts,
     // 23.6 -> 18.0 us; K = 2048 shapes lose more to the extra launch than they gain).
     int64_t split = 1;
-    while (!d->norm_rows && split < std::min(16, ctx->skinny_max_split) &&
+    while (!d->norm_rows && split < 16 &&
            tiles * split < 2 * cus && nsteps / (split * 2) >= 128)
       split *= 2;
     dim3 grid((unsigned)((d->N + 15) / 16), (unsigned)split, (unsigned)batch);
@@ -1902,22 +1889,15 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       part = (float*)ws;
     }
     LaunchScope ls(ctx, family, flops, bytes);
-    if (f32out) launch_skinny<float>(cfg, grid, ctx->stream, p, part);
-    else launch_skinny<bf16_t>(cfg, grid, ctx->stream, p, part);
+    if (f32out) launch_skinny<float>(grid, ctx->stream, p, part);
+    else launch_skinny<bf16_t>(grid, ctx->stream, p, part);
     return ls.finish("gemm_skinny");
   }
   if (mfma) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const bool wide_ok = !f32out && p.epi >= EPI_PLAIN && p.epi <= EPI_RES;
     int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus, wide_ok);
-    bool fixed = d->tile != 0;  // a caller's tile, or a TL_GEMM_TILE_FOR one, is kept as is
-    if (!d->tile)
-      for (const auto& r : ctx->tile_rules)
-        if (r.M == d->M && r.N == d->N && r.K == d->K && r.tile > 0 &&
-            r.tile <= TL_TILE_DMA_256x192_W8 && r.tile != TL_TILE_SKINNY) {
-          tile = r.tile;
-          fixed = true;
-        }
+    const bool fixed = d->tile != 0;  // a caller's tile is kept as is
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
     // the persistent kernels store through a buffer resource: whole 16-byte pieces, byte
     // offsets below 2^31

@@ -521,8 +521,10 @@ __device__ __forceinline__ uint4 neg_inf_chunk() {
 // elements (those past the row's causal limit count as -inf and come out as 0), then
 // e = 2^(k (x - m_t)) with k = log2(e) / temperature (one FMA and one exp2 per element) and
 // their sum s_t; the workgroup merges the (m_t, s_t) pairs in a single reduction into the
-// row's (M, S), and each thread writes e * 2^(k (m_t - M)) / S. KEEP holds e in fp32
-// registers between the passes; otherwise the output pass recomputes it from the chunks.
+// row's (M, S), and each thread writes e * 2^(k (m_t - M)) / S, e recomputed from the chunks.
+// The row's full chunks are loaded and stored non-temporally: each logit is read once and
+// each probability written once, so keeping them out of the caches leaves more room for the
+// traffic in flight.
 __device__ __forceinline__ void merge_max_sum(float& m, float& s, float om, float os, float k) {
   const float M = fmaxf(m, om);
   if (M == -INFINITY) return;  // both empty
@@ -530,7 +532,7 @@ __device__ __forceinline__ void merge_max_sum(float& m, float& s, float om, floa
   m = M;
 }
 
-template <typename T, int NT, int CH, bool CAUSAL, bool KEEP, bool NTM = false>
+template <typename T, int NT, int CH, bool CAUSAL>
 __global__ __launch_bounds__(NT) void softmax_long_kernel(const T* __restrict__ x,
                                                           T* __restrict__ y, int64_t rows,
                                                           int cols, int64_t ldx, int64_t ldy,
@@ -557,13 +559,9 @@ __global__ __launch_bounds__(NT) void softmax_long_kernel(const T* __restrict__ 
     if (c * NT * VW >= valid) {
       raw[c] = ninf;  // whole chunk past the limit (uniform)
     } else if (col + VW <= valid) {
-      if constexpr (NTM) {
-        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-        const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(xr + col));
-        raw[c] = make_uint4(t.x, t.y, t.z, t.w);
-      } else {
-        raw[c] = *reinterpret_cast<const uint4*>(xr + col);
-      }
+      typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+      const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(xr + col));
+      raw[c] = make_uint4(t.x, t.y, t.z, t.w);
     } else if (col < valid) {
       union {
         uint4 u;
@@ -595,20 +593,15 @@ __global__ __launch_bounds__(NT) void softmax_long_kernel(const T* __restrict__ 
   }
   opaque();
   const float mk = m_t == -INFINITY ? 0.f : m_t * k;  // a thread past the row keeps e = 0
-  float ev[KEEP ? CH : 1][VW];
   float s_t = 0.f;
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     float v[VW];
     Elem<T>::unpack(raw[c], v);
 #pragma unroll
-    for (int e = 0; e < VW; ++e) {
-      const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk));
-      if (KEEP) ev[KEEP ? c : 0][e] = ex;
-      s_t += ex;
-    }
+    for (int e = 0; e < VW; ++e) s_t += __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk));
   }
-  if (!KEEP) opaque();
+  opaque();
   float m = m_t, s = s_t;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -634,24 +627,15 @@ __global__ __launch_bounds__(NT) void softmax_long_kernel(const T* __restrict__ 
     const int col = (c * NT + tid) * VW;
     if (c * NT * VW >= cols) break;  // uniform
     float o[VW];
-    if (KEEP) {
+    float v[VW];
+    Elem<T>::unpack(raw[c], v);
 #pragma unroll
-      for (int e = 0; e < VW; ++e) o[e] = ev[KEEP ? c : 0][e] * f;
-    } else {
-      float v[VW];
-      Elem<T>::unpack(raw[c], v);
-#pragma unroll
-      for (int e = 0; e < VW; ++e) o[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk)) * f;
-    }
+    for (int e = 0; e < VW; ++e) o[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(v[e], k, -mk)) * f;
     if (col + VW <= cols) {
-      if constexpr (NTM) {
-        typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-        const uint4 w = Elem<T>::pack(o);
-        const v4u t = {w.x, w.y, w.z, w.w};
-        __builtin_nontemporal_store(t, reinterpret_cast<v4u*>(yr + col));
-      } else {
-        store_chunk(yr + col, o);
-      }
+      typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+      const uint4 w = Elem<T>::pack(o);
+      const v4u t = {w.x, w.y, w.z, w.w};
+      __builtin_nontemporal_store(t, reinterpret_cast<v4u*>(yr + col));
     } else if (col < cols) {
 #pragma unroll
       for (int e = 0; e < VW; ++e)
@@ -1068,31 +1052,20 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
     else if (nt_store) go(std::false_type(), std::integral_constant<int, 2>());
     else go(std::false_type(), std::integral_constant<int, 0>());
   };
-  // Long rows: (threads, keep e in registers) by TL_SOFTMAX_LONG_CFG (1: 1024, 2: 1024 kept,
-  // 3: 512, 4: 512 kept, with cached loads and stores). By default (5) 512 threads for rows
-  // up to 8192 chunks (three rows resident per CU) and 1024 threads otherwise, e recomputed,
-  // and the row's full chunks loaded and stored non-temporally: each logit is read once and
-  // each probability written once, so keeping them out of the caches leaves more room for
-  // the traffic in flight (vocabulary rows: bf16 5.10 -> 5.16 TB/s, fp32 with e kept
+  // Long rows: 512 threads for rows up to 8192 chunks (three rows resident per CU) and 1024
+  // threads otherwise. On an MI355X this beat 1024 or 512 threads with e kept in registers
+  // and cached loads and stores (vocabulary rows: bf16 5.10 -> 5.16 TB/s, fp32 with e kept
   // 4.51 -> 4.92 TB/s). Chunks per thread: the smallest instantiated count that covers the
   // row.
-  const int lcfg = ctx->softmax_long_cfg;
-  auto longrow = [&](auto nt_tag, bool keep, bool ntm) -> bool {
+  auto longrow = [&](auto nt_tag) -> bool {
     constexpr int NT = decltype(nt_tag)::value;
     bool done = false;
     auto try_ch = [&](auto ch_tag) {
       constexpr int CH = decltype(ch_tag)::value;
       if (done || (int64_t)NT * CH < chunks) return;
       const float k = 1.4426950408889634f / temp;
-      if (keep && CH * VW <= 64)
-        softmax_long_kernel<T, NT, CH, CAUSAL, (CH * VW <= 64)><<<(unsigned)rows, NT, 0, ctx->stream>>>(
-            (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
-      else if (ntm)
-        softmax_long_kernel<T, NT, CH, CAUSAL, false, true><<<(unsigned)rows, NT, 0, ctx->stream>>>(
-            (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
-      else
-        softmax_long_kernel<T, NT, CH, CAUSAL, false><<<(unsigned)rows, NT, 0, ctx->stream>>>(
-            (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
+      softmax_long_kernel<T, NT, CH, CAUSAL><<<(unsigned)rows, NT, 0, ctx->stream>>>(
+          (const T*)x, (T*)y, rows, (int)cols, ldx, ldy, k, period, offset);
       done = true;
     };
     try_ch(std::integral_constant<int, 2>());
@@ -1106,10 +1079,8 @@ static void launch_softmax(tl_ctx* ctx, const void* x, void* y, int64_t rows, in
   if (vec && chunks <= 512) {
     dispatch_row_shape<8, false>(64, chunks, wave);
   } else if (vec && chunks <= 1024 * 16) {
-    const int c = lcfg >= 1 && lcfg <= 4 ? lcfg : 5;
-    const bool keep = c <= 4 && c % 2 == 0, ntm = c == 5;
-    if (c >= 3 && chunks <= 512 * 16) longrow(std::integral_constant<int, 512>(), keep, ntm);
-    else longrow(std::integral_constant<int, 1024>(), keep, ntm);
+    if (chunks <= 512 * 16) longrow(std::integral_constant<int, 512>());
+    else longrow(std::integral_constant<int, 1024>());
   } else {
     softmax_generic_kernel<T, CAUSAL><<<(unsigned)rows, 256, 0, ctx->stream>>>(
         (const T*)x, (T*)y, rows, cols, ldx, ldy, temp, period, offset);

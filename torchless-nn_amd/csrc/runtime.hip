@@ -170,20 +170,6 @@ int tl_init(int device, tl_ctx** out) {
   tl_ctx* ctx = new tl_ctx();
   ctx->device = device;
   ctx->num_cus = prop.multiProcessorCount;
-  if (const char* g = std::getenv("TL_GEMM_GROUP_M")) ctx->gemm_group_m = std::atoi(g);
-  if (const char* g = std::getenv("TL_SKINNY_CFG")) ctx->skinny_cfg = std::atoi(g);
-  if (const char* g = std::getenv("TL_SKINNY_MAX_SPLIT")) ctx->skinny_max_split = std::atoi(g);
-  if (const char* g = std::getenv("TL_ATTN_DECODE_CFG")) ctx->attn_decode_cfg = std::atoi(g);
-  if (const char* g = std::getenv("TL_SOFTMAX_LONG_CFG")) ctx->softmax_long_cfg = std::atoi(g);
-  if (const char* g = std::getenv("TL_GEMM_TILE_FOR")) {
-    long long m, n, k;
-    int t, used;
-    for (const char* q = g; std::sscanf(q, " %lld , %lld , %lld = %d%n", &m, &n, &k, &t, &used) == 4;) {
-      ctx->tile_rules.push_back({(int64_t)m, (int64_t)n, (int64_t)k, t});
-      q += used;
-      while (*q == ';' || *q == ' ') ++q;
-    }
-  }
   e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     delete ctx;
@@ -217,6 +203,7 @@ int tl_destroy(tl_ctx* ctx) {
     (void)hipGetLastError();
   }
   (void)hipStreamSynchronize(ctx->stream);
+  attention_scratch_release(ctx);
   for (tl_graph* g : ctx->graphs) {
     (void)hipGraphExecDestroy(g->exec);
     (void)hipGraphDestroy(g->graph);

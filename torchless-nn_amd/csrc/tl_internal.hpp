@@ -56,30 +56,17 @@ struct tl_ctx {
   std::vector<tl::KprofRecord> kprof_pending;
   tl::KprofTotals kprof_totals[TL_KF_COUNT];
   int num_cus = 0;
-  int gemm_group_m = 0;  // tile-rows per group in the GEMM tile order (TL_GEMM_GROUP_M)
-  // tuning overrides (0 = built-in choice): skinny GEMM variant (TL_SKINNY_CFG) and
-  // decode attention split (TL_ATTN_DECODE_CFG)
-  int skinny_cfg = 0;
-  int skinny_max_split = 16;  // TL_SKINNY_MAX_SPLIT
-  int attn_decode_cfg = 0;
-  // long-row softmax shape (TL_SOFTMAX_LONG_CFG): 0 default, 1..4 (threads, keep) choices
-  int softmax_long_cfg = 0;
   // regions named by tl_prefetch_hint, passed to the next LayerNorm / RMSNorm launch
   tl::PrefetchList prefetch{};
-  // per-shape GEMM tile overrides for automatic calls (TL_GEMM_TILE_FOR="M,N,K=tile;...",
-  // tile a tl_gemm_tile value): tuning sweeps inside a whole forward
-  struct TileRule {
-    int64_t M, N, K;
-    int tile;
-  };
-  std::vector<TileRule> tile_rules;
   // grow-only scratch for kernels that combine partial results (split argmax, split-KV
   // attention); used in stream order, so one buffer serves every call on this context
   void* ws = nullptr;
   size_t ws_bytes = 0;
   // device address, on this context's device, of the static scratch array behind
-  // tl_attention_fwd_noalloc (set by tl_init)
+  // tl_attention_fwd_noalloc (set by tl_init), and the event recorded on this context's
+  // stream after its last call that used that array
   void* noalloc_scratch = nullptr;
+  hipEvent_t noalloc_done = nullptr;
   // HIP graph capture of the context stream (tl_graph_*). Blocks handed out by tl_malloc
   // while a capture is open belong to the graph it produces for as long as the graph lives:
   // its replays write them, so they are not reused even after the caller frees them.
@@ -129,8 +116,12 @@ int enter(tl_ctx* ctx);
 int workspace(tl_ctx* ctx, size_t bytes, void** ptr);
 
 // Looks up, once per device and with that device current, the address of the static scratch
-// array behind tl_attention_fwd_noalloc, and stores it in ctx->noalloc_scratch.
+// array behind tl_attention_fwd_noalloc, stores it in ctx->noalloc_scratch, and creates
+// ctx->noalloc_done.
 int attention_scratch_setup(tl_ctx* ctx);
+// Takes the context out of its device's scratch turn order and destroys ctx->noalloc_done
+// (tl_destroy, after the context's stream has drained).
+void attention_scratch_release(tl_ctx* ctx);
 
 // Brackets one kernel launch with profiler events when its family is enabled (a negative
 // family never is: such a launch creates no events).
