@@ -94,7 +94,8 @@ def test_gemm_desc_layout_matches_header():
         decl = decl.strip()
         if not decl:
             continue
-        decl = re.sub(r"^(const\s+)?(void\s*\*|int64_t|int32_t|float)\s*", "", decl)
+        decl = re.sub(r"^(const\s+)?(void\s*\*|double\s*\*|float\s*\*|int64_t|int32_t|float)\s*",
+                      "", decl)
         names += [re.sub(r"[\s*]", "", n) for n in decl.split(",")]
     assert names == [f[0] for f in tl_hip._GemmDesc._fields_]
 
@@ -184,11 +185,11 @@ def test_abi_host_paths_under_address_and_ub_sanitizers():
     """Every exported entry point, called the way a binding could get it wrong (null context,
     null pointers, zero sizes) and through the no-device path, in a host build instrumented
     with ASan and UBSan: each returns a status with a message and no sanitizer reports."""
-    if not os.path.exists(SAN_LIB):
-        r = subprocess.run(["make", "-C", os.path.join(PKG, "csrc"), "san", "-j8"],
-                           capture_output=True, text=True, timeout=600)
-        if r.returncode != 0:
-            pytest.skip("sanitizer build unavailable: " + r.stderr[-500:])
+    # incremental: rebuilt when a source or header is newer than the instrumented library
+    r = subprocess.run(["make", "-C", os.path.join(PKG, "csrc"), "san", "-j8"],
+                       capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        pytest.skip("sanitizer build unavailable: " + r.stderr[-500:])
     rt = _asan_runtime()
     if rt is None:
         pytest.skip("clang ASan runtime not found")
