@@ -1607,7 +1607,8 @@ static int persistent_per_cu(int tile) { return tile == TL_TILE_PERSIST_128x128 
 // tiles when there are enough of them, else with 128-row tiles sized to the last round of
 // resident workgroups; register-prefetch tiles cover other K; 64x64 covers grids too
 // small to fill the GPU.
-static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool wide_ok) {
+static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool wide_ok,
+                       bool qkv_split) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn) * batch; };
   const int64_t t128 = tiles(128, 128), t64 = tiles(128, 64);
   if (K % 64 == 0) {
@@ -1635,6 +1636,12 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, 
         const int64_t w192 = (tiles(256, 192) + cus - 1) / cus * 192;
         if (w192 <= std::min(w96, w128)) best = TL_TILE_DMA_256x192_W8;
       }
+      // The QKV head scatter in place of 256x96: the two-per-CU 128x96 tile (the same whole
+      // rounds: GPT-2 QKV 768 tiles of 256x96 on 256 CUs, 1536 of 128x96 on 512 slots). With
+      // its weight warmed by the norm launch before it, one workgroup's scatter epilogue runs
+      // under the other's K loop: 3.482 -> 3.450 ms per GPT-2 forward (same box, three
+      // alternating rounds). The out-projection on it as well measured no further gain.
+      if (qkv_split && best == TL_TILE_DMA_256x96_W8) best = TL_TILE_DMA_128x96;
       return best;
     }
     // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
@@ -1896,7 +1903,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (mfma) {
     const int cus = ctx->num_cus > 0 ? ctx->num_cus : 256;
     const bool wide_ok = !f32out && p.epi >= EPI_PLAIN && p.epi <= EPI_RES;
-    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus, wide_ok);
+    int tile = d->tile ? d->tile : choose_tile(d->M, d->N, d->K, batch, cus, wide_ok, qkv);
     const bool fixed = d->tile != 0;  // a caller's tile is kept as is
     if (tile >= TL_TILE_DMA_128x128 && d->K % 64 != 0) tile = TL_TILE_128x128;  // DMA needs whole K steps
     // the persistent kernels store through a buffer resource: whole 16-byte pieces, byte
