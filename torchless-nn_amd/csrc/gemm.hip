@@ -1928,6 +1928,14 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       const int64_t nt = ((d->M + t.bm - 1) / t.bm) * ((d->N + t.bn - 1) / t.bn);
       if (nt >= 2LL * cus)
         tile = tile == TL_TILE_DMA_256x96_W8 ? TL_TILE_PERSIST_256x96_W8 : TL_TILE_PERSIST_256x128_W8;
+    } else if (!fixed && persist_ok && (p.epi == EPI_BIAS_GELU || p.epi == EPI_BIAS_SILU) &&
+               d->K % 64 == 0 && d->K <= 1024 && t128 >= 4LL * cus) {
+      // An activation epilogue (one exp2 and one reciprocal per element) is vector-ALU bound;
+      // on the two-per-CU persistent 128x128 tile one workgroup's epilogue runs under the
+      // other's K loop. GPT-2 FFN1 (K = 768, 1536 tiles): 3.337 -> 3.299 ms per forward
+      // against 256x192 (same box, three alternating rounds; the persistent 256x128 / 256x96
+      // / 256x256 tiles 3.319 / 3.377 / 3.415 ms).
+      tile = TL_TILE_PERSIST_128x128;
     }
     const bool persistent = is_persistent(tile);
     const TileShape& s = kTiles[tile];
