@@ -1636,12 +1636,16 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, 
         const int64_t w192 = (tiles(256, 192) + cus - 1) / cus * 192;
         if (w192 <= std::min(w96, w128)) best = TL_TILE_DMA_256x192_W8;
       }
-      // The QKV head scatter in place of 256x96: the two-per-CU 128x96 tile (the same whole
-      // rounds: GPT-2 QKV 768 tiles of 256x96 on 256 CUs, 1536 of 128x96 on 512 slots). With
-      // its weight warmed by the norm launch before it, one workgroup's scatter epilogue runs
-      // under the other's K loop: 3.482 -> 3.450 ms per GPT-2 forward (same box, three
-      // alternating rounds). The out-projection on it as well measured no further gain.
-      if (qkv_split && best == TL_TILE_DMA_256x96_W8) best = TL_TILE_DMA_128x96;
+      // The QKV head scatter (K <= 1024) on the two-per-CU 128-row tile of the same width,
+      // which takes the same whole rounds (GPT-2 QKV: 768 tiles of 256x96 on 256 CUs, 1536 of
+      // 128x96 on 512 slots): one workgroup's scatter epilogue runs under the other's K loop.
+      // GPT-2 (256x96 -> 128x96) 3.482 -> 3.450 ms per forward, same box, three alternating
+      // rounds (the out-projection on it as well: no further gain); ViT-S/4 (K = 384,
+      // 256x128 -> 128x128) 2.284 -> 2.255 ms.
+      if (qkv_split && K <= 1024) {
+        if (best == TL_TILE_DMA_256x96_W8) best = TL_TILE_DMA_128x96;
+        else if (best == TL_TILE_DMA_256x128_W8) best = TL_TILE_DMA_128x128;
+      }
       return best;
     }
     // otherwise 128-row tiles, 2 workgroups per CU: the width whose last round of
