@@ -1615,6 +1615,13 @@ static int choose_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, 
     // many 256x256 tiles (LM head, large square): 8 waves of 128x64 read the least LDS and
     // L2 per flop (787 TF on the LM head vs 627; 1335 TF at 8192^3)
     if (tiles(256, 256) >= 4LL * cus) return TL_TILE_DMA_256x256_W8;
+    // ... and for a long K loop (K >= 4096, which amortises the tile's start) when they fill
+    // at least 90% of their rounds: the config-5 down projection (K = 16384, 256 tiles on 256
+    // CUs) 256x128 -> 256x256, prefill 37.92 -> 37.40 ms (same box, two rounds)
+    {
+      const int64_t t256 = tiles(256, 256), rounds = (t256 + cus - 1) / cus;
+      if (K >= 4096 && t256 >= cus && t256 * 10 >= rounds * cus * 9) return TL_TILE_DMA_256x256_W8;
+    }
     // 256-row tiles with a 3-stage pipeline (two K steps of loads in flight, one workgroup
     // per CU) when they fill at least one round: inside a forward the weights arrive cold and
     // the activations from the previous kernel, and the deeper pipeline beats two 2-stage
