@@ -1827,7 +1827,9 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   if (geglu && eo == 2 && !d->bias && d->divisor == 1.0f && (d->N / 2) % 8 == 0 && d->ldc % 8 == 0 &&
       ((uintptr_t)d->C % 16) == 0 && d->sc_o % 8 == 0 && d->sc_i % 8 == 0)
     p.epi = d->act == TL_ACT_GELU ? EPI_GEGLU_GELU : EPI_GEGLU_SILU;
-  p.group_m = 8;  // tile-rows per group: 8 ties 4 and 2 and beats 16 and 32 in-model
+  // Tile-rows per group, measured in-model: 6 beats 3/5/7/8/10 on GPT-2 (3.422 vs 3.456 ms at
+  // 8), ties on ViT-S/4 and config-5 prefill; 16 and 32 lose 3-17%.
+  p.group_m = 6;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
   p.norm_rows = d->norm_rows != 0;
