@@ -1828,8 +1828,12 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       ((uintptr_t)d->C % 16) == 0 && d->sc_o % 8 == 0 && d->sc_i % 8 == 0)
     p.epi = d->act == TL_ACT_GELU ? EPI_GEGLU_GELU : EPI_GEGLU_SILU;
   // Tile-rows per group, measured in-model: 6 beats 3/5/7/8/10 on GPT-2 (3.422 vs 3.456 ms at
-  // 8), ties on ViT-S/4 and config-5 prefill; 16 and 32 lose 3-17%.
-  p.group_m = 6;
+  // 8; every GPT-2 product is fastest at 6) and ties on ViT-S/4; 16 and 32 lose 3-17%. The
+  // config-5 vocabulary product (K = 2048, 1000 tile-columns of 256) runs best at 8 (7291 ->
+  // 6766 us in a kernel trace; 4 is close, 2 and 3 slower; config-5 prefill 37.45 -> 37.16 ms,
+  // same box, three alternating rounds), while the config-5 GeGLU product (K = 2048, 128
+  // tile-columns) lost 0.8 ms per prefill at 8 in-model.
+  p.group_m = d->K >= 2048 && d->K < 4096 && d->N >= 512 * 256 ? 8 : 6;
   p.div_T = make_fastdiv(qkv ? (uint32_t)d->seq_len : 1u);
   p.div_Dh = make_fastdiv(qkv ? (uint32_t)d->head_dim : 1u);
   p.norm_rows = d->norm_rows != 0;
