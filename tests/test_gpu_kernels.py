@@ -614,11 +614,16 @@ def test_gemm_persistent_pipeline(xp, mnk):
 @pytest.mark.parametrize("tile", ["auto", "dma128x128", "dma256x128w8", "dma128x96", "dma256x256w8",
                                   "dma128x64s3", "dma256x96w8"])
 @pytest.mark.parametrize("cfg", [(2, 64, 12, 12, 64, 192, 0), (3, 40, 8, 1, 32, 128, 16),
-                                 (1, 136, 2, 2, 16, 64, 0), (2, 24, 3, 1, 24, 128, 8)])
+                                 (1, 136, 2, 2, 16, 64, 0), (2, 24, 3, 1, 24, 128, 8),
+                                 # T, pos0 not multiples of 8 (ViT-S/4: T = 65): V^T units
+                                 # straddle sequences and are stored element by element
+                                 (4, 65, 6, 6, 64, 384, 0), (3, 33, 8, 1, 32, 128, 5),
+                                 (2, 17, 4, 2, 16, 64, 3)])
 def test_gemm_qkv_staged_scatter(xp, tile, cfg):
-    """QKV head scatter of the direct-to-LDS tiles (bf16, D/T/L/pos0 multiples of 8): Q and
-    K rows from 16-byte row pieces, V^T rows from a transposed LDS block; wave slabs that
-    straddle Q/K/V take the generic epilogue. Cache slots outside [pos0, pos0 + T) stay 0."""
+    """QKV head scatter of the direct-to-LDS tiles (bf16, D a multiple of 8): Q and K rows
+    from 16-byte row pieces, V^T rows from a transposed LDS block (16-byte units when T, L
+    and pos0 are multiples of 8, single elements otherwise); wave slabs that straddle Q/K/V
+    take the generic epilogue. Cache slots outside [pos0, pos0 + T) stay 0."""
     B, T, Hq, Hkv, D, C, pos0 = cfg
     N = (Hq + 2 * Hkv) * D
     L = (pos0 + T + 7) // 8 * 8 + 8

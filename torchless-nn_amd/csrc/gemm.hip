@@ -529,15 +529,17 @@ __device__ __forceinline__ void staged_epilogue(const GemmParams& e, int64_t zo,
   }
 }
 
-// QKV head scatter through LDS (bf16; D, T, cache capacity L and write position all
-// multiples of 8). A wave whose column slab lies in Q or K stages its rows as above and
-// writes each 16-byte row piece (8 consecutive d of one head) to q[b, h, t, :] or
-// k[b, h, pos0 + t, :]. A slab in V is staged transposed (column c holds the WM rows, its
-// 16-byte units rotated by c against bank conflicts) and each unit, 8 consecutive t of one
-// d, goes to vt[b, h, d, pos0 + t .. + 7], so the transposed V rows are written whole
-// instead of with 2-byte stores. Returns false (nothing written) for a slab that straddles
-// two parts; the caller then runs the generic epilogue for that wave.
-template <bool BIAS, int TM, int TN, int WM, int WN>
+// QKV head scatter through LDS (bf16, D a multiple of 8). A wave whose column slab lies in Q
+// or K stages its rows as above and writes each 16-byte row piece (8 consecutive d of one
+// head) to q[b, h, t, :] or k[b, h, pos0 + t, :]. A slab in V is staged transposed (column c
+// holds the WM rows, its 16-byte units rotated by c against bank conflicts) and each unit,
+// 8 consecutive rows of one d, goes to vt[b, h, d, pos0 + t .. + 7]: as one 16-byte store
+// when T, the cache capacity L and pos0 are multiples of 8 (the 8 rows then share b and the
+// destination is aligned), or, with VELEM (any T, L and pos0; ViT-S/4: T = 65), as 8
+// 2-byte stores with a (b, t) per row, which still writes runs of consecutive t. Returns
+// false (nothing written) for a slab that straddles two parts; the caller then runs the
+// generic epilogue for that wave.
+template <bool BIAS, int TM, int TN, int WM, int WN, bool VELEM = false>
 __device__ __forceinline__ bool staged_qkv_epilogue(const GemmParams& e, int64_t mw, int64_t nw,
                                                     f32x4 (&acc)[TM][TN], bf16_t* region) {
   constexpr int U = WN / 8, RU = WM / 8;
@@ -614,12 +616,26 @@ __device__ __forceinline__ bool staged_qkv_epilogue(const GemmParams& e, int64_t
   for (int p = 0; p < WN * RU / 64; ++p) {
     const int q = p * 64 + lane, c = q / RU, ru = q - c * RU;
     const uint4 val = *reinterpret_cast<const uint4*>(reg + (c * RU + (ru + c) % RU) * 16);
-    const int64_t m = mw + 8 * ru, n = nw + c;  // rows m .. m+7 share b (T % 8 == 0)
+    const int64_t m = mw + 8 * ru, n = nw + c;
     if (m >= e.M || n >= e.N) continue;
-    const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
-    const int nn = (int)n - base;
-    const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
-    gstore16((bf16_t*)e.vt + ((int64_t)(b * e.Hkv + h) * e.Dh + d) * e.L + t + e.pos0, val);
+    if constexpr (!VELEM) {  // rows m .. m+7 share b and start an aligned run of 8 positions
+      const int b = (int)fast_div((uint32_t)m, e.div_T), t = (int)m - b * e.T;
+      const int nn = (int)n - base;
+      const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
+      gstore16((bf16_t*)e.vt + ((int64_t)(b * e.Hkv + h) * e.Dh + d) * e.L + t + e.pos0, val);
+    } else {
+      const int nn = (int)n - base;
+      const int h = (int)fast_div((uint32_t)nn, e.div_Dh), d = nn - h * e.Dh;
+      const uint32_t hw[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t mj = m + j;
+        if (mj >= e.M) break;
+        const int b = (int)fast_div((uint32_t)mj, e.div_T), t = (int)mj - b * e.T;
+        gstore((bf16_t*)e.vt + ((int64_t)(b * e.Hkv + h) * e.Dh + d) * e.L + t + e.pos0,
+               (bf16_t)(hw[j >> 1] >> (16 * (j & 1))));
+      }
+    }
   }
   return true;
 }
@@ -922,7 +938,7 @@ __device__ __forceinline__ void schedule_kstep() {
 }
 
 
-template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES>
+template <typename TO, int BM, int BN, int WGM, int WGN, int WPE, int STAGES, bool VELEM = false>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void gemm_dma_kernel(GemmParams p) {
   constexpr int NW = WGM * WGN, BK = 64;
@@ -1041,10 +1057,10 @@ void gemm_dma_kernel(GemmParams p) {
         case EPI_BIAS_SILU: staged_epilogue<EPI_BIAS_SILU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_BIAS_RES: staged_epilogue<EPI_BIAS_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_RES: staged_epilogue<EPI_RES, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
-        case EPI_QKV_BIAS: done = staged_qkv_epilogue<true, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
+        case EPI_QKV_BIAS: done = staged_qkv_epilogue<true, TM, TN, WM, WN, VELEM>(e, mw, nw, acc, region); break;
         case EPI_GEGLU_GELU: staged_geglu_epilogue<EPI_GEGLU_GELU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
         case EPI_GEGLU_SILU: staged_geglu_epilogue<EPI_GEGLU_SILU, TM, TN, WM, WN>(e, zo, zi, mw, nw, acc, region); break;
-        default: done = staged_qkv_epilogue<false, TM, TN, WM, WN>(e, mw, nw, acc, region); break;
+        default: done = staged_qkv_epilogue<false, TM, TN, WM, WN, VELEM>(e, mw, nw, acc, region); break;
       }
     }
   }
@@ -1715,6 +1731,13 @@ static void launch_mfma(int tile, dim3 grid, hipStream_t st, const GemmParams& p
   }
 }
 
+// The QKV scatter with element-wise V^T stores (T, L or pos0 not a multiple of 8) on the
+// tiles the QKV rule picks.
+static void launch_qkv_velem(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
+  if (tile == TL_TILE_DMA_128x96) gemm_dma_kernel<bf16_t, 128, 96, 2, 2, 2, 2, true><<<grid, 256, 0, st>>>(p);
+  else gemm_dma_kernel<bf16_t, 128, 128, 2, 2, 2, 2, true><<<grid, 256, 0, st>>>(p);
+}
+
 template <int KIND>
 static void launch_persistent_kind(int tile, dim3 grid, hipStream_t st, const GemmParams& p) {
   switch (tile) {
@@ -1820,10 +1843,15 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     else if (b && r && d->act == TL_ACT_NONE) p.epi = EPI_BIAS_RES;
     else if (!b && r && d->act == TL_ACT_NONE) p.epi = EPI_RES;
   }
-  if (qkv && !d->kv_pos0_dev && eo == 2 && d->divisor == 1.0f && d->act == TL_ACT_NONE && !d->residual &&
-      d->head_dim % 8 == 0 && d->seq_len % 8 == 0 && p.L % 8 == 0 && p.pos0 % 8 == 0 &&
-      ((uintptr_t)d->q % 16) == 0 && ((uintptr_t)d->k % 16) == 0 && ((uintptr_t)d->vt % 16) == 0)
-    p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;
+  // The staged QKV scatter: 16-byte V^T units need T, L and pos0 multiples of 8; otherwise
+  // the two-per-CU 128-row tiles the QKV rule picks take the element-wise V^T form
+  // (qkv_velem, decided with the tile) and other tiles the generic epilogue.
+  const bool qkv_staged = qkv && !d->kv_pos0_dev && eo == 2 && d->divisor == 1.0f &&
+                          d->act == TL_ACT_NONE && !d->residual && d->head_dim % 8 == 0 &&
+                          ((uintptr_t)d->q % 16) == 0 && ((uintptr_t)d->k % 16) == 0 &&
+                          ((uintptr_t)d->vt % 16) == 0;
+  const bool qkv_aligned = d->seq_len % 8 == 0 && p.L % 8 == 0 && p.pos0 % 8 == 0;
+  if (qkv_staged && qkv_aligned) p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;
   if (geglu && eo == 2 && !d->bias && d->divisor == 1.0f && (d->N / 2) % 8 == 0 && d->ldc % 8 == 0 &&
       ((uintptr_t)d->C % 16) == 0 && d->sc_o % 8 == 0 && d->sc_i % 8 == 0)
     p.epi = d->act == TL_ACT_GELU ? EPI_GEGLU_GELU : EPI_GEGLU_SILU;
@@ -1954,6 +1982,11 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
       // / 256x256 tiles 3.319 / 3.377 / 3.415 ms).
       tile = TL_TILE_PERSIST_128x128;
     }
+    // ViT-S/4 QKV (T = 65, 128x128) against the generic epilogue: 2.312 -> 2.221 ms per ViT
+    // forward (same box, six alternating pairs); GPT-2 within run-to-run spread
+    const bool qkv_velem = qkv_staged && !qkv_aligned &&
+                           (tile == TL_TILE_DMA_128x96 || tile == TL_TILE_DMA_128x128);
+    if (qkv_velem) p.epi = d->bias ? EPI_QKV_BIAS : EPI_QKV;
     const bool persistent = is_persistent(tile);
     const TileShape& s = kTiles[tile];
     p.tiles_m = (int)((d->M + s.bm - 1) / s.bm);
@@ -1968,6 +2001,7 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
     }
     LaunchScope ls(ctx, family, flops, bytes);
     if (persistent) launch_persistent(tile, grid, ctx->stream, p);
+    else if (qkv_velem) launch_qkv_velem(tile, grid, ctx->stream, p);
     else if (f32out) launch_mfma<float>(tile, grid, ctx->stream, p);
     else launch_mfma<bf16_t>(tile, grid, ctx->stream, p);
     return ls.finish("gemm_mfma");
