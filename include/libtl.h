@@ -260,6 +260,19 @@ int tl_transpose2d_gain(tl_ctx* ctx, const void* x, void* y, int64_t rows, int64
 int tl_patchify(tl_ctx* ctx, const void* x, void* y, int64_t batch, int64_t channels,
                 int64_t height, int64_t width, int64_t patch_h, int64_t patch_w,
                 int32_t dtype_x, int32_t dtype_y);
+/* The whole ViT front end in one launch, reference transformer_adapters.py:34-55
+ * (VitProjector.forward: patches, @ projection, class/register tokens prepended, + positions):
+ * out [B, R + L, dim] with rows r < R = n_cls_reg equal to cls_reg[r] + pos[r] and rows
+ * R + l equal to patches(x)[b, l] @ w^T + pos[R + l] for the L = (H/ph)(W/pw) patches
+ * (features in (row in patch, column in patch, channel) order, as tl_patchify). w is the
+ * projection given as [dim, K], K = ph pw C. bf16 only, K <= 64 and a multiple of 8, L <= 64,
+ * dim a multiple of 96, w and out 16-byte aligned; other shapes return TL_ERR_UNSUPPORTED
+ * (tl_patchify, tl_gemm and tl_embed_fwd compose the same result). Equal bit for bit to
+ * that composition. */
+int tl_vit_project(tl_ctx* ctx, const void* x, const void* w, const void* cls_reg,
+                   const void* pos, void* out, int64_t batch, int64_t channels, int64_t height,
+                   int64_t width, int64_t patch_h, int64_t patch_w, int64_t dim,
+                   int64_t n_cls_reg, int32_t dtype);
 /* y = a + b (elementwise, same shape). Replaces the residual adds at reference
  * layers.py:465-466 when they are not fused into a GEMM epilogue. */
 int tl_add(tl_ctx* ctx, const void* a, const void* b, void* y, int64_t n, int32_t dtype);

@@ -72,6 +72,57 @@ def test_vit_projector_layer(tl, dt, registers):
     assert ref.max_rel(y2, want) <= (1e-5 if dt == "fp32" else 2e-2)
 
 
+@pytest.mark.parametrize("cfg", [((3, 32, 32), (4, 4), 384, 0, 7), ((3, 32, 32), (4, 4), 384, 1, 3),
+                                 ((3, 32, 32), (4, 4), 384, 4, 2), ((1, 16, 16), (4, 4), 96, 2, 5),
+                                 ((3, 16, 8), (4, 2), 192, 1, 3), ((2, 32, 32), (4, 4), 288, 1, 2),
+                                 ((2, 16, 16), (2, 4), 480, 1, 3)])
+def test_vit_projector_fused_equals_three_launches(tl, cfg):
+    """tl_vit_project (one launch per forward) against the patch gather + batched GEMM +
+    class-row gather composition, bit for bit: K = 16 .. 48 features, 16 / 32 / 64 patches,
+    dim 96 .. 480 (one to five 96-column groups, so a wave may take two), 0 .. 4
+    class/register rows."""
+    xp = tl["xp"]
+    tl["backend"].set_float_type("bf16")
+    (C, H, W), patch, E, regs, B = cfg
+    layer = tl["ta"].VitProjector((C, H, W), patch, E, num_registers=regs)
+    rng = np.random.default_rng(E + regs + B)
+    for p in layer.parameters:
+        p.set(ref.round_bf16(rng.standard_normal(p.shape).astype(F32)))
+    x = xp.array(ref.round_bf16(rng.standard_normal((B, C, H, W)).astype(F32)), dtype="bf16")
+    assert xp.vit_project_ok(x, patch, E, 1 + regs)
+    layer.fused = True
+    got = layer.forward(x).get().view(np.uint16).copy()
+    layer.fused = False
+    want = layer.forward(x).get().view(np.uint16)
+    assert np.array_equal(got, want), cfg
+
+
+def test_vit_project_unsupported_shape_falls_back(tl):
+    """Patches of more than 64 features are outside tl_vit_project (TL_ERR_UNSUPPORTED at
+    the C ABI); the projector then composes the three launches and still matches the
+    oracle."""
+    xp = tl["xp"]
+    tl["backend"].set_float_type("bf16")
+    layer = tl["ta"].VitProjector((3, 32, 32), (8, 8), 192)  # K = 192
+    rng = np.random.default_rng(11)
+    P = []
+    for p in layer.parameters:
+        a = ref.round_bf16(rng.standard_normal(p.shape).astype(F32) * F32(0.5))
+        p.set(a)
+        P.append(a)
+    x = ref.round_bf16(rng.standard_normal((2, 3, 32, 32)).astype(F32))
+    dx = xp.array(x, dtype="bf16")
+    assert not xp.vit_project_ok(dx, (8, 8), 192, 1)
+    out = xp.empty((2, 17, 192), "bf16")
+    pos = layer.positional_embeddings
+    w = xp.empty((192, 192), "bf16")
+    rc = xp.lib().tl_vit_project(xp.ctx().handle, dx.ptr, w.ptr, layer.cls_reg_tokens.ptr, pos.ptr,
+                                 out.ptr, 2, 3, 32, 32, 8, 8, 192, 1, 1)
+    assert rc == xp.TL_ERR_UNSUPPORTED
+    y = layer.forward(dx).get()
+    assert ref.max_rel(y, ref.vit_projector(x, *P, (8, 8))) <= 2e-2
+
+
 def test_vit_projector_rejects_wrong_image_shape(tl):
     tl["backend"].set_float_type("fp32")
     layer = tl["ta"].VitProjector((3, 32, 32), (4, 4), 64)

@@ -2079,3 +2079,129 @@ extern "C" int tl_gemm(tl_ctx* ctx, const tl_gemm_desc* d) {
   }
   return ls.finish("gemm_simt");
 }
+
+namespace tl {
+
+// vit_project_kernel: the ViT front end (VitProjector.forward) in one launch, one workgroup
+// of 4 waves per image. The image's L <= 64 patch rows are gathered into LDS (features in
+// (row in patch, column in patch, channel) order, zero past K <= 64; 16-byte chunks
+// XOR-swizzled by row). Each wave takes 96-column groups of the projection (given as
+// [E, K], K-contiguous) and, per 16-row tile, issues the same two 16x16x32 MFMA steps with
+// the same operand order and zero-filled K tail as the tiled GEMM, adds the row's position
+// (after the GEMM epilogue's zero bias) in fp32 and rounds once, so each value equals the
+// three-launch path (patch gather, batched GEMM with the positions as residual, class-row
+// gather) bit for bit. The 16 x 96 results go through the wave's LDS region and out as
+// 16-byte row pieces. Rows 0 .. R-1 are the class/register tokens plus their positions.
+__global__ __launch_bounds__(256) void vit_project_kernel(const bf16_t* __restrict__ x,
+                                                          const bf16_t* __restrict__ w,
+                                                          const bf16_t* __restrict__ cls_reg,
+                                                          const bf16_t* __restrict__ pos,
+                                                          bf16_t* __restrict__ out, int C, int H,
+                                                          int W, int p0, int p1, int E, int R) {
+  constexpr int KP = 64, TN = 6, GW = 16 * TN;  // padded K, column tiles per wave group
+  __shared__ __attribute__((aligned(16))) bf16_t P[64 * KP];
+  __shared__ __attribute__((aligned(16))) bf16_t S[4][16 * GW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fc = lane >> 4;
+  const int64_t b = blockIdx.x;
+  const int pw = W / p1, L = (H / p0) * pw, K = p0 * p1 * C, T = R + L;
+  const bf16_t* xi = x + b * C * H * W;
+  bf16_t* ob = out + b * T * E;
+  for (int idx = tid; idx < 64 * KP; idx += 256) {
+    const int l = idx >> 6, t = idx & 63;
+    bf16_t v = 0;
+    if (l < L && t < K) {
+      const int ch = t % C, t2 = t / C, c2 = t2 % p1, a = t2 / p1;
+      const int i = l / pw, j = l - i * pw;
+      v = xi[((int64_t)ch * H + i * p0 + a) * W + j * p1 + c2];
+    }
+    P[l * KP + ((((t >> 3) ^ (l & 7))) << 3) + (t & 7)] = v;
+  }
+  // class/register rows: token + position
+  for (int idx = tid; idx < R * E / 4; idx += 256) {
+    const int r = idx / (E / 4), c = (idx - r * (E / 4)) * 4;
+    const uint2 u = gload8(cls_reg + (int64_t)r * E + c), q = gload8(pos + (int64_t)r * E + c);
+    float v[4] = {__uint_as_float(u.x << 16) + __uint_as_float(q.x << 16),
+                  __uint_as_float(u.x & 0xffff0000u) + __uint_as_float(q.x & 0xffff0000u),
+                  __uint_as_float(u.y << 16) + __uint_as_float(q.y << 16),
+                  __uint_as_float(u.y & 0xffff0000u) + __uint_as_float(q.y & 0xffff0000u)};
+    gstore8(ob + (int64_t)r * E + c, make_uint2((uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16),
+                                                (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16)));
+  }
+  __syncthreads();
+  const bf16x8 zero = {};
+  bf16_t* reg = S[wave];
+  for (int n0 = wave * GW; n0 < E; n0 += 4 * GW) {
+    bf16x8 bfr[2][TN];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int k = 32 * s + 8 * fc;
+        bfr[s][j] = k < K ? gload(reinterpret_cast<const bf16x8*>(w + (int64_t)(n0 + 16 * j + fr) * K + k))
+                          : zero;
+      }
+    for (int i = 0; i < 4 && 16 * i < L; ++i) {
+      const int r = 16 * i + fr;
+      bf16x8 af[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        af[s] = *reinterpret_cast<const bf16x8*>(&P[r * KP + (((s * 4 + fc) ^ (fr & 7)) << 3)]);
+      f32x4 acc[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s][j], af[s], acc[j], 0, 0, 0);
+      // row r's position (rows past L read row L - 1 and are not stored)
+      const bf16_t* prow = pos + (int64_t)(R + min(r, L - 1)) * E + n0;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const uint2 q = gload8(prow + 16 * j + 4 * fc);
+        const float v0 = (acc[j][0] + 0.f) + __uint_as_float(q.x << 16);
+        const float v1 = (acc[j][1] + 0.f) + __uint_as_float(q.x & 0xffff0000u);
+        const float v2 = (acc[j][2] + 0.f) + __uint_as_float(q.y << 16);
+        const float v3 = (acc[j][3] + 0.f) + __uint_as_float(q.y & 0xffff0000u);
+        *reinterpret_cast<uint2*>(&reg[fr * GW + 16 * j + 4 * fc]) =
+            make_uint2((uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16),
+                       (uint32_t)f2bf(v2) | ((uint32_t)f2bf(v3) << 16));
+      }
+      // 16 rows x 12 pieces of 16 bytes; a wave's LDS operations complete in order
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        const int q = p * 64 + lane, rr = q / 12, u = q - rr * 12;
+        const uint4 v = *reinterpret_cast<const uint4*>(&reg[rr * GW + 8 * u]);
+        if (16 * i + rr < L) gstore16(ob + (int64_t)(R + 16 * i + rr) * E + n0 + 8 * u, v);
+      }
+    }
+  }
+}
+
+}  // namespace tl
+
+extern "C" int tl_vit_project(tl_ctx* ctx, const void* x, const void* w, const void* cls_reg,
+                              const void* pos, void* out, int64_t batch, int64_t channels,
+                              int64_t height, int64_t width, int64_t patch_h, int64_t patch_w,
+                              int64_t dim, int64_t n_cls_reg, int32_t dtype) {
+  int rc = enter(ctx);
+  if (rc) return rc;
+  TL_REQUIRE(x && w && cls_reg && pos && out, "null pointer");
+  TL_REQUIRE(batch > 0 && batch < (1LL << 31) && channels > 0 && patch_h > 0 && patch_w > 0 &&
+                 height > 0 && width > 0 && height % patch_h == 0 && width % patch_w == 0,
+             "bad image or patch shape");
+  TL_REQUIRE(n_cls_reg >= 0 && dim > 0, "bad token shape");
+  const int64_t K = patch_h * patch_w * channels, L = (height / patch_h) * (width / patch_w);
+  if (dtype != TL_BF16 || K > 64 || K % 8 != 0 || L > 64 || dim % 96 != 0 || dim > 4096 ||
+      n_cls_reg > 64 || channels * height * width > (1LL << 24) || !al16(w) || !al16(out) ||
+      dim % 8 != 0 || (uintptr_t)cls_reg % 8 != 0 || (uintptr_t)pos % 8 != 0)
+    return fail(TL_ERR_UNSUPPORTED, "tl_vit_project takes bf16, K = ph pw C <= 64 (a multiple of "
+                "8), at most 64 patches, dim a multiple of 96 and aligned rows");
+  const double bytes = 2.0 * (double)batch * (channels * height * width + (L + n_cls_reg) * dim);
+  LaunchScope ls(ctx, TL_KF_GEMM_BATCHED, 2.0 * batch * L * dim * K, bytes);
+  vit_project_kernel<<<dim3((unsigned)batch), 256, 0, ctx->stream>>>(
+      (const bf16_t*)x, (const bf16_t*)w, (const bf16_t*)cls_reg, (const bf16_t*)pos, (bf16_t*)out,
+      (int)channels, (int)height, (int)width, (int)patch_h, (int)patch_w, (int)dim, (int)n_cls_reg);
+  return ls.finish("vit_project");
+}

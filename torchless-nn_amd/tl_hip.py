@@ -175,6 +175,7 @@ SIGNATURES = {
     "tl_add": [_P, _P, _P, _P, _I64, _I32],
     "tl_transpose2d_gain": [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _F32, _I32],
     "tl_patchify": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32],
+    "tl_vit_project": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32],
     "tl_embed_fwd": [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_layernorm_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _I32],
     "tl_rmsnorm_fwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _F32, _I32],
@@ -903,6 +904,38 @@ def patchify(x: DeviceTensor, patch, dtype=None) -> DeviceTensor:
     out = DeviceTensor((B, (H // p0) * (W // p1), p0 * p1 * C), dtype or x.dtype)
     lib_, h = _c()
     check(lib_.tl_patchify(h, x.ptr, out.ptr, B, C, H, W, p0, p1, x.dtype.code, out.dtype.code))
+    return out
+
+
+def vit_project_ok(x: DeviceTensor, patch, dim, n_cls_reg) -> bool:
+    """Whether tl_vit_project takes this ViT front end (bf16, K = p0 p1 C <= 64 and a
+    multiple of 8, at most 64 patches, dim a multiple of 96, n_cls_reg <= 64)."""
+    if x.dtype is not bfloat16 or x.ndim != 4 or not x.contiguous:
+        return False
+    B, C, H, W = x.shape
+    p0, p1 = patch
+    K, L = p0 * p1 * C, (H // p0) * (W // p1)
+    return (H % p0 == 0 and W % p1 == 0 and K <= 64 and K % 8 == 0 and L <= 64 and
+            dim % 96 == 0 and dim <= 4096 and 0 <= n_cls_reg <= 64)
+
+
+def vit_project(x: DeviceTensor, w: DeviceTensor, cls_reg: DeviceTensor, pos: DeviceTensor,
+                patch, out: DeviceTensor):
+    """The ViT front end in one launch (reference transformer_adapters.py:34-55): out [B, R + L,
+    dim] = class/register tokens + positions, then patches(x) @ w^T + positions; w is the
+    projection as [dim, K] (the packed form). See vit_project_ok for the shapes it takes."""
+    B, C, H, W = x.shape
+    R, dim = cls_reg.shape
+    K, L = patch[0] * patch[1] * C, (H // patch[0]) * (W // patch[1])
+    if (tuple(w.shape) != (dim, K) or tuple(pos.shape) != (R + L, dim) or
+            tuple(out.shape) != (B, R + L, dim)):
+        raise ValueError("vit_project: w [dim, K], pos [R + L, dim] and out [B, R + L, dim] expected")
+    if not all(t.contiguous for t in (x, w, cls_reg, pos, out)):
+        raise ValueError("vit_project needs contiguous tensors")
+    lib_, h = _c()
+    check(lib_.tl_vit_project(h, x.ptr, w.ptr, cls_reg.ptr, pos.ptr, out.ptr, B, C, H, W,
+                              patch[0], patch[1], dim, R, x.dtype.code))
+    _wrote(out)
     return out
 
 

@@ -20,10 +20,14 @@ class VitProjector(Layer):
     patch_size, flattened in (row, column, channel) order, projected by `projection`
     (no bias), preceded by 1 + num_registers learned tokens, plus positional embeddings.
 
-    Three launches: the patch gather (tl_patchify), one batched GEMM that writes each
-    image's patch rows after its class/register rows with the positional rows added in the
-    epilogue (a residual shared by the whole batch, stride 0), and one gather per
-    class/register row that writes that row of every image (row pitch = tokens x dim)."""
+    bf16 images whose patches have at most 64 features (ViT-S/4: 48) and at most 64
+    patches take one launch (tl_vit_project: patch gather, projection on the matrix cores,
+    class/register rows and positions in one kernel per image). Other shapes take three,
+    with the same result bit for bit: the patch gather (tl_patchify), one batched GEMM that
+    writes each image's patch rows after its class/register rows with the positional rows
+    added in the epilogue (a residual shared by the whole batch, stride 0), and one gather
+    per class/register row that writes that row of every image (row pitch = tokens x dim).
+    `fused = False` forces the three-launch form."""
 
     def __init__(self, input_size: tuple, patch_size: tuple, embedding_dim, num_registers=0):
         super(VitProjector, self).__init__()
@@ -46,6 +50,7 @@ class VitProjector(Layer):
         self.cls_reg_token_grads = self.register_param(self.cls_reg_tokens)
         self.positional_embeddings_grads = self.register_param(self.positional_embeddings)
         self._zero_ids = None
+        self.fused = True
 
     def forward(self, input):
         if not isinstance(input, xp.DeviceTensor):
@@ -57,8 +62,15 @@ class VitProjector(Layer):
         B = self.batch_size = input.shape[0]
         dt = self.projection.dtype
         L, R, E, K = self.sequence_length, self.cls_reg_size, self.embedding_dim, self.token_dim
-        self.tokens = xp.patchify(input, self.patch_size, dtype=dt)  # [B, L, K]
         out = xp.empty((B, R + L, E), dt)
+        if (self.fused and dt is xp.bfloat16 and input.dtype is dt and
+                xp.vit_project_ok(input, self.patch_size, E, R)):
+            xp.vit_project(input, _packed_nk(self.projection), self.cls_reg_tokens,
+                           self.positional_embeddings, self.patch_size, out)
+            self.embeddings = out
+            self.output = out
+            return self.output
+        self.tokens = xp.patchify(input, self.patch_size, dtype=dt)  # [B, L, K]
         es = dt.itemsize
         pos = self.positional_embeddings
         # rows R.. of every image: tokens @ projection + positions[R:]
