@@ -12,8 +12,8 @@
 //   consecutive output columns of one row, stored as one 8- or 16-byte write.
 //   Output tiles are visited in an XCD-aware grouped order: workgroups are dispatched
 //   round-robin over the 8 XCDs, so block ids are remapped to give every XCD a contiguous
-//   run of tiles, and tiles run in groups of 8 tile-rows so the A and B panels a group
-//   shares stay in that XCD's L2.
+//   run of tiles, and tiles run in groups of a few tile-rows (group_m) so the A and B panels
+//   a group shares stay in that XCD's L2.
 // gemm_simt_kernel: any dtype, layout or alignment, fp32 FMA on the vector ALUs. It
 //   serves the fp32 model and shapes the MFMA kernel's 16-byte loads cannot take.
 #include <algorithm>
