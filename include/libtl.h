@@ -266,7 +266,8 @@ int tl_patchify(tl_ctx* ctx, const void* x, void* y, int64_t batch, int64_t chan
  * R + l equal to patches(x)[b, l] @ w^T + pos[R + l] for the L = (H/ph)(W/pw) patches
  * (features in (row in patch, column in patch, channel) order, as tl_patchify). w is the
  * projection given as [dim, K], K = ph pw C. bf16 only, K <= 64 and a multiple of 8, L <= 64,
- * dim a multiple of 96, w and out 16-byte aligned; other shapes return TL_ERR_UNSUPPORTED
+ * dim a multiple of 96 and at most 4096, n_cls_reg <= 64, C H W <= 2^24, w and out 16-byte
+ * aligned, cls_reg and pos 8-byte aligned; other shapes return TL_ERR_UNSUPPORTED
  * (tl_patchify, tl_gemm and tl_embed_fwd compose the same result). Equal bit for bit to
  * that composition. */
 int tl_vit_project(tl_ctx* ctx, const void* x, const void* w, const void* cls_reg,
